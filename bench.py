@@ -1,0 +1,244 @@
+"""Benchmark of the KV-cache hot path on one MI355X.
+
+Headline (``value``): BASELINE configs[1] -- paged append with fused FP8 quantisation at
+the Llama-3-8B KV shape (32 layers, 8 KV heads, head_dim 128, page 16, 16 sequences of
+U[1k, 8k] tokens, 5% of each sequence's (layer, head) pairs x50), one step = one append
+of every layer, inputs already resident in HBM.  Reported as algorithmic GB/s
+(3 bytes per KV element + scales + block tables) and as a fraction of the 8 TB/s HBM3E
+peak.  Also measured: configs[2] (paged gather + dequant, 64 x 32k decode, 300k-page
+pool) and, when built, configs[3] (Belady tiering trace).
+
+The CPU baseline is the C oracle (oracle/zx_oracle.c, one thread) timed on a bounded
+sample of the same workload on this machine's host cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only append|gather]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "KV quant+append & gather+dequant GB/s (% HBM peak); evictions/sec"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
+    ap.add_argument("--only", choices=["append", "gather", "all"], default="all")
+    ap.add_argument("--seed", type=int, default=1)
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ workloads
+
+def make_append_workload(torch, dev, seed=1):
+    """32L, 8H, 128D, P=16, 16 seqs with T_b ~ U[1024, 8192]."""
+    L, H, D, P, B = 32, 8, 128, 16, 16
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1024, 8193, (B,), generator=g).tolist()
+    T = sum(lens)
+    nb = [(n + P - 1) // P for n in lens]
+    n_pages = sum(nb)
+    max_blocks = max(nb)
+    perm = torch.randperm(n_pages, generator=g).to(torch.int32)
+    bt = torch.full((B, max_blocks), -1, dtype=torch.int32)
+    k = 0
+    for b in range(B):
+        bt[b, :nb[b]] = perm[k:k + nb[b]]
+        k += nb[b]
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
+    # outliers: per sequence, 5% of its 256 (layer, head) pairs (13) scaled x50 on K and V
+    outl = [torch.randperm(L * H, generator=g)[:13].tolist() for _ in range(B)]
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.empty((L, T, 2, H, D), dtype=torch.bfloat16, device=dev)
+    for l in range(L):
+        x[l].normal_(generator=gd)
+    for b in range(B):
+        for lh in outl[b]:
+            l, h = divmod(lh, H)
+            x[l, cu[b]:cu[b + 1], :, h] *= 50.0
+    pool = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8, device=dev)
+    N = L * T * 2 * H * D
+    alg_bytes = 3 * N + 4 * L * 2 * H + 4 * L * n_pages + 4 * (B + 1)
+    return dict(x=x, cu=cu.to(dev), bt=bt.to(dev), pool=pool, lens=lens, T=T, n_pages=n_pages,
+                N=N, alg_bytes=alg_bytes, L=L, H=H, D=D, P=P, B=B, cu_host=cu, bt_host=bt)
+
+
+def make_gather_workload(torch, dev, seed=2):
+    """64 seqs x 32768 tokens, 300k-page FP8 pool, fragmented tables."""
+    n_pool, H, D, P, B, T, L = 300_000, 8, 128, 16, 64, 32768, 32
+    g = torch.Generator().manual_seed(seed)
+    max_blocks = T // P
+    bt = torch.randperm(n_pool, generator=g)[: B * max_blocks].to(torch.int32).reshape(B, max_blocks)
+    scales = (torch.rand((L, 2, H), generator=g) * (1 - 1e-3) + 1e-3).float()
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    pool = torch.randint(0, 256, (n_pool, 2, H, P, D), dtype=torch.uint8, device=dev, generator=gd)
+    pool[pool == 0x7F] = 0x7E
+    pool[pool == 0xFF] = 0xFE
+    seq_lens = torch.full((B,), T, dtype=torch.int32)
+    layer = 7
+    N = B * T * 2 * H * D
+    alg_bytes = 3 * N + 4 * B * max_blocks + 4 * 2 * H + 4 * B
+    return dict(pool=pool, scales=scales.to(dev), layer=layer, bt=bt.to(dev), seq_lens=seq_lens.to(dev),
+                T=T, B=B, H=H, D=D, P=P, N=N, alg_bytes=alg_bytes, bt_host=bt, scales_host=scales)
+
+
+# ------------------------------------------------------------------ timing
+
+def time_steps(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    t0 = time.perf_counter()
+    ev[0].record(st)
+    for i in range(steps):
+        fn()
+        ev[i + 1].record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return sum(per) / steps, per, wall
+
+
+def cpu_baseline_append(W, budget_s=20.0):
+    """C oracle (1 thread) on a bounded sample: whole sequences of layer 0 appended until
+    about budget_s of CPU work; GB/s at 3 B per element."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    x0 = W["x"][0].cpu().view(__import__("torch").int16).numpy().view(np.uint16)  # [T, 2, H, D]
+    lens, P, H, D = W["lens"], W["P"], W["H"], W["D"]
+    cu = W["cu_host"].numpy()
+    bt = W["bt_host"].numpy()
+    pool = np.zeros((1, W["n_pages"], 2, H, P, D), np.uint8)
+    done_tok, elapsed, b = 0, 0.0, 0
+    while b < len(lens) and elapsed < budget_s:
+        xs = np.ascontiguousarray(x0[cu[b]:cu[b + 1]])[None]
+        cub = np.array([0, lens[b]], np.int32)
+        t0 = time.perf_counter()
+        O.kv_quant_append(xs, cub, None, bt[b:b + 1], pool, P)
+        elapsed += time.perf_counter() - t0
+        done_tok += lens[b]
+        b += 1
+    n = done_tok * 2 * H * D
+    return {"value": round(3 * n / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"C oracle zxo_kv_quant_append (scalar, 1 thread) on layer 0, sequences 0..{b - 1} "
+                      f"({done_tok} tokens, {n} elements), dynamic per-head scales; {elapsed:.1f} s"}
+
+
+def cpu_baseline_gather(W, budget_s=10.0):
+    import numpy as np
+
+    from oracle import oracle as O
+
+    torch = __import__("torch")
+    H, D, P = W["H"], W["D"], W["P"]
+    bt = W["bt_host"]
+    sc = W["scales_host"][W["layer"]].numpy()
+    elapsed, n, b = 0.0, 0, 0
+    while b < W["B"] and elapsed < budget_s:
+        pages = bt[b]
+        sub = W["pool"][pages.long().to(W["pool"].device)].cpu().numpy()  # the sequence's pages
+        loc = np.arange(len(pages), dtype=np.int32)[None]
+        t0 = time.perf_counter()
+        O.kv_gather_dequant(sub, sc, loc, np.array([W["T"]], np.int32), W["T"])
+        elapsed += time.perf_counter() - t0
+        n += W["T"] * 2 * H * D
+        b += 1
+    del torch
+    return {"value": round(3 * n / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"C oracle zxo_kv_gather_dequant (1 thread), {b} of {W['B']} sequences of one layer; "
+                      f"{elapsed:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the KV hot path is benchmarked on a "
+                          "single MI355X (multi-GPU sharding is described in DESIGN.md, not run)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from zenyx_amd import kv
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    out = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic (seeded N(0,1) bf16 KV, random page tables)"}
+
+    if args.only in ("append", "all"):
+        log("building configs[1] append workload")
+        W = make_append_workload(torch, dev, seed=args.seed)
+        scales = torch.empty((W["L"], 2, W["H"]), dtype=torch.float32, device=dev)
+
+        def step():
+            kv.kv_quant_append(W["x"], W["cu"], W["bt"], W["pool"], scales=scales)
+
+        log(f"append: {W['T']} tokens x 32 layers = {W['N']} elements; timing {args.steps} steps")
+        ms, per, wall = time_steps(torch, step, args.steps, args.warmup)
+        gbps = W["alg_bytes"] / (ms * 1e-3) / 1e9
+        log(f"append: {ms:.3f} ms/step, {gbps:.1f} GB/s ({100 * gbps / HBM_PEAK_GBPS:.1f}% of peak)")
+        out.update({
+            "value": round(gbps, 2), "ms_per_step": round(ms, 4),
+            "config": {"workload": "configs[1]: paged append + fused FP8 e4m3 quant, Llama-3-8B KV shape "
+                                   "(32 layers, 8 KV heads, D=128, page 16, 16 seqs U[1k,8k], 5% heads x50)",
+                       "n_tok": W["T"], "elements": W["N"], "n_pages_per_layer": W["n_pages"],
+                       "algorithmic_bytes_per_step": W["alg_bytes"], "seed": args.seed},
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "kernel": "zx_kv_quant_append (all kernels of one append, HIP events)"},
+        })
+        if not args.skip_cpu:
+            log("CPU baseline (append)")
+            out["cpu_baseline"] = cpu_baseline_append(W)
+        del W
+        torch.cuda.empty_cache()
+
+    if args.only in ("gather", "all"):
+        log("building configs[2] gather workload")
+        G = make_gather_workload(torch, dev)
+        k = torch.empty((G["B"], G["H"], G["T"], G["D"]), dtype=torch.bfloat16, device=dev)
+        v = torch.empty_like(k)
+        sc = G["scales"][G["layer"]].contiguous()
+
+        def gstep():
+            kv.kv_gather_dequant(G["pool"], sc, G["bt"], G["seq_lens"], G["T"], out=(k, v))
+
+        ms_g, _, _ = time_steps(torch, gstep, args.steps, args.warmup)
+        gb_g = G["alg_bytes"] / (ms_g * 1e-3) / 1e9
+        log(f"gather: {ms_g:.3f} ms/step, {gb_g:.1f} GB/s ({100 * gb_g / HBM_PEAK_GBPS:.1f}% of peak)")
+        gather = {"GBps": round(gb_g, 2), "ms_per_step": round(ms_g, 4), "frac": round(gb_g / HBM_PEAK_GBPS, 4),
+                  "workload": "configs[2]: paged gather + dequant, 64 seqs x 32768, 300k-page pool, one layer K+V",
+                  "algorithmic_bytes_per_step": G["alg_bytes"]}
+        if not args.skip_cpu:
+            log("CPU baseline (gather)")
+            gather["cpu_baseline"] = cpu_baseline_gather(G)
+        out["gather_dequant"] = gather
+        if "value" not in out:
+            out.update({"value": round(gb_g, 2), "ms_per_step": round(ms_g, 4),
+                        "config": {"workload": gather["workload"]}})
+        del G
+
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,192 @@
+/*
+ * zenyx_kv.h -- C ABI of libzenyx_kv.so, the MI355X (gfx950) KV-cache hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP stream
+ * (hipStream_t passed as void*; NULL means the legacy default stream), enqueues its
+ * kernels on that stream and returns without synchronising.  Buffers are owned by
+ * the caller.  Return value: ZX_OK (0) or a negative ZX_ERR_* code; a message for
+ * the last failure on the calling thread is available from zx_last_error().
+ *
+ * Reference interfaces each group replaces (paths relative to the zenyx source tree):
+ *   - zenyx/streaming/precision.py:8-12   quantize_to_fp8_storage
+ *   - zenyx/streaming/precision.py:15-16  dequantize_for_bf16_compute
+ *   - zenyx/streaming/belady.py:39-51     BeladyApproxCache._select_victim
+ *   - zenyx/streaming/kv_tiering.py:36-66 KVTierManager tier moves (.to / .cpu copies)
+ *   - README.md:93-97, 328-331, 343-346   BeladyKVCacheTieringManager / FP8KVQuantizer
+ *     (the Phase-7/8 modules named there are absent from the source tree; their
+ *      behaviour is defined by this library, see the per-function comments)
+ *
+ * Numeric contract (shared with the CPU oracle under oracle/):
+ *   bf16 values are passed as uint16_t bit patterns, fp8 codes as uint8_t (OCP e4m3fn).
+ *   FP8 scale   s = fp32(max(amax, 1e-8f) / 448.0f)   (IEEE division; NaN amax -> NaN s)
+ *   FP8 code    c = e4m3fn_RNE(fp32(x) / s)           (IEEE division, RNE, overflow -> NaN)
+ *   dequant     y = bf16_RNE(decode(c) * s)
+ *   Slabs whose scale is not finite: s = +inf gives code 0x00/0x80 for finite x and
+ *   0x7F for non-finite x; s = NaN (any NaN in the slab) gives 0x7F everywhere.
+ */
+#ifndef ZENYX_KV_H
+#define ZENYX_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *zx_stream_t; /* hipStream_t */
+
+enum zx_status {
+  ZX_OK = 0,
+  ZX_ERR_INVALID = -1,     /* null pointer, negative size, inconsistent arguments */
+  ZX_ERR_HIP = -2,         /* a HIP runtime call failed */
+  ZX_ERR_UNSUPPORTED = -3, /* shape outside what the kernels handle */
+  ZX_ERR_WORKSPACE = -4,   /* workspace missing or too small */
+};
+
+enum zx_dtype { ZX_BF16 = 0, ZX_F16 = 1, ZX_F32 = 2 };
+
+/* Error bits a kernel ORs into the caller's device error word (see err arguments). */
+enum zx_kernel_error {
+  ZX_KERR_PAGE_RANGE = 1, /* a block-table entry outside [0, n_pages) */
+  ZX_KERR_POS_RANGE = 2,  /* a token position beyond max_blocks * page_size */
+  ZX_KERR_SPIN = 4,       /* a bounded inter-workgroup wait ran out (kernel exited early) */
+};
+
+/* Message describing the last failing call on this thread ("" if none). */
+const char *zx_last_error(void);
+/* ABI version of the library (bumped on any signature change). */
+int zx_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Legacy per-tensor int8 storage.  Replaces zenyx/streaming/precision.py:8-12.
+ *   s = max(amax(|x|), 1e-8) / 127, every step rounded to x's dtype as torch does
+ *   q = int8(clamp(round_half_even(dtype(x / s)), -127, 127))
+ * x: n elements of `dtype` (ZX_BF16, ZX_F16 or ZX_F32); q: n int8; scale: one
+ * element of `dtype` (device).  workspace: >= 256 device bytes.  n must be > 0
+ * (the reference raises on an empty tensor, precision.py:10).
+ */
+int zx_int8_legacy_quant(const void *x, int dtype, int64_t n, int8_t *q, void *scale,
+                         void *workspace, size_t workspace_bytes, zx_stream_t stream);
+
+/* Replaces zenyx/streaming/precision.py:15-16: y = bf16_RNE(float(q) * float(scale)).
+ * scale: one element of `scale_dtype` (device); y: n bf16. */
+int zx_int8_legacy_dequant(const int8_t *q, const void *scale, int scale_dtype, int64_t n,
+                           uint16_t *y, zx_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * FP8 e4m3fn with one scale per (outer, head): FP8KVQuantizer.quantize
+ * (README.md:329, 344; "per-head dynamic scaling" README.md:157).
+ * Layout of x / codes / y: [n_outer][n_batch][n_heads][run] (for a KV cache
+ * [L][2][B][H][T][D]: n_outer = 2L, run = T*D).  scales: [n_outer][n_heads] fp32,
+ * written by quant, read by dequant.  run must be a multiple of 16.
+ */
+int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_heads,
+                       int64_t run, uint8_t *codes, float *scales, zx_stream_t stream);
+int zx_fp8_dequant_heads(const uint8_t *codes, const float *scales, int64_t n_outer,
+                         int64_t n_batch, int64_t n_heads, int64_t run, uint16_t *y,
+                         zx_stream_t stream);
+
+/* Encode already-scaled fp32 values to e4m3fn codes with the same device conversion the
+ * kernels above use (utility; no reference counterpart): nearest-even, |v| > 464 or
+ * Inf/NaN -> sign | 0x7F. */
+int zx_fp8_encode_f32(const float *v, int64_t n, uint8_t *codes, zx_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged KV cache.  A layer's new tokens arrive token-major, x[n_tok][2][H][D] bf16
+ * (K then V), sequences packed by cu_seqlens[n_seqs+1].  Token i of sequence b sits
+ * at position start_pos[b] + i, in page block_tables[b][pos / P], row pos % P.
+ * Pool layout per layer: [n_pages][2][H][P][D] uint8 codes, so one (page, kv, head)
+ * is a contiguous run of P*D bytes.  Scales: [n_layers][2][H] fp32.
+ * Supported: head_dim in {64, 128, 256}, 2*H*head_dim <= 8192, page_size >= 1.
+ */
+
+/* Per-(layer, kv, head) scales of a token-major batch (dynamic amax). */
+int zx_kv_scales(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, int64_t n_tok,
+                 int32_t n_heads, int32_t head_dim, float *scales, zx_stream_t stream);
+
+/* Bytes of device workspace zx_kv_quant_append needs for these arguments. */
+size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32_t n_heads,
+                                          int32_t head_dim);
+
+#define ZX_APPEND_STATIC_SCALES 1 /* flag: use `scales` as given instead of computing them */
+
+/* Paged append with fused FP8 quantisation.  Without
+ * ZX_APPEND_STATIC_SCALES the scales are computed from this batch (amax over all
+ * of its tokens) and written to `scales`.  Rows whose page id is out of range are
+ * skipped and flagged in *err (device int32, may be NULL). */
+int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
+                       int64_t n_tok, int32_t n_heads, int32_t head_dim,
+                       const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
+                       const int32_t *block_tables, int32_t max_blocks, int32_t page_size,
+                       uint8_t *pool, int64_t pool_layer_stride, int64_t n_pages, float *scales,
+                       int32_t flags, int32_t *err, void *workspace, size_t workspace_bytes,
+                       zx_stream_t stream);
+
+/* Paged gather + dequant for decode of one layer.
+ * scales: the layer's [2][H] fp32.  Output k_out, v_out: [n_seqs][H][out_len][D] bf16;
+ * positions t >= seq_lens[b] are written as zeros, as are rows whose page id is out of
+ * range (flagged in *err, may be NULL). */
+int zx_kv_gather_dequant(const uint8_t *pool, int64_t n_pages, int32_t n_heads, int32_t head_dim,
+                         int32_t page_size, const float *scales, const int32_t *block_tables,
+                         int32_t max_blocks, const int32_t *seq_lens, int32_t n_seqs,
+                         int32_t out_len, uint16_t *k_out, uint16_t *v_out, int32_t *err,
+                         zx_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Belady victim selection.  Replaces zenyx/streaming/belady.py:39-51: among slots
+ * with resident[i] != 0, pick the largest keys[i] that is > -1; ties go to the
+ * smallest slot index.  out (device int64[2]) receives {slot, key}, or {-1, -1}
+ * when no slot qualifies.  workspace: >= zx_belady_argmax_workspace_bytes(n_slots).
+ */
+size_t zx_belady_argmax_workspace_bytes(int64_t n_slots);
+int zx_belady_argmax(const int64_t *keys, const uint8_t *resident, int64_t n_slots, int64_t *out,
+                     void *workspace, size_t workspace_bytes, zx_stream_t stream);
+
+/* Next/previous use of every trace position: next_use[i] = smallest j > i with
+ * trace[j] == trace[i], else ZX_NEVER; prev_use[i] = largest j < i, else -1.
+ * trace holds page ids in [0, n_pages); n < 2^31 - 1.  Out-of-range ids set
+ * ZX_KERR_PAGE_RANGE in *err (device int32, may be NULL). */
+#define ZX_NEVER 0x7FFFFFFF
+size_t zx_belady_next_use_workspace_bytes(int64_t n, int32_t n_pages);
+int zx_belady_next_use(const int32_t *trace, int64_t n, int32_t n_pages, int32_t *next_use,
+                       int32_t *prev_use, int32_t *err, void *workspace, size_t workspace_bytes,
+                       zx_stream_t stream);
+
+/* Belady MIN over a page trace (BeladyKVCacheTieringManager, README.md:93-97, 343):
+ * a miss with `capacity` (>= 1) pages resident evicts the resident page whose next use
+ * is farthest (ZX_NEVER counts as farthest), ties to the smallest page id, then admits
+ * the missed page; a hit moves the page's key to its next use.
+ * trace/next_use/prev_use cover the whole trace, positions [0, n_total); this call
+ * processes positions [t_begin, t_end), so a trace can be fed in pieces.  The cache
+ * state lives in the caller's buffers: resident[n_pages] (uint8), key[n_pages] (int32
+ * next use of each resident page), state[4] (int64 device: resident count, evictions so
+ * far, misses so far, hits so far); zero them all for an empty cache.  Victims are
+ * appended to evict_pos/evict_page at index state[1] (stored while < evict_cap, always
+ * counted).  miss_flags (uint8[n_total], may be NULL) receives 1 at each miss position
+ * of this call and 0 at each hit.
+ * workspace: >= zx_belady_simulate_workspace_bytes(n_total, n_pages); n_total + n_pages
+ * must not exceed 2^30. */
+size_t zx_belady_simulate_workspace_bytes(int64_t n_total, int32_t n_pages);
+int zx_belady_simulate(const int32_t *trace, const int32_t *next_use, const int32_t *prev_use,
+                       int64_t n_total, int64_t t_begin, int64_t t_end, int32_t n_pages,
+                       int64_t capacity, uint8_t *resident, int32_t *key, int64_t *state,
+                       int32_t *evict_pos, int32_t *evict_page, int64_t evict_cap,
+                       uint8_t *miss_flags, void *workspace, size_t workspace_bytes,
+                       zx_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Tier moves (replaces the .to(device) / .cpu() copies of kv_tiering.py:46, 54, 60).
+ * Copies n_runs runs of `run_bytes` bytes: run i goes from src + src_off[i] to
+ * dst + dst_off[i] (offsets in bytes, host arrays).  Adjacent runs are merged into one
+ * hipMemcpyAsync.  Host memory must be pinned (hipHostMalloc) for the copy to overlap
+ * with kernels on other streams.  `done` (hipEvent_t, may be NULL) is recorded on
+ * `stream` after the last copy. */
+int zx_tier_copy_runs(void *dst, const void *src, const int64_t *dst_off, const int64_t *src_off,
+                      int64_t n_runs, int64_t run_bytes, zx_stream_t stream, void *done);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZENYX_KV_H */

@@ -1,0 +1,437 @@
+/*
+ * zx_oracle.c -- CPU restatement of the zenyx KV-cache hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the HIP library is compared
+ * against: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+ * it.  The product (zenyx_amd/, libzenyx_kv.so) never links or calls it.
+ *
+ * Reference anchors (paths relative to the zenyx source tree):
+ *   int8 legacy quant/dequant ........ zenyx/streaming/precision.py:8-12, 15-16
+ *   Belady victim selection .......... zenyx/streaming/belady.py:25-51
+ *   ring schedule .................... zenyx/streaming/kv_tiering.py:69-73 (generalised)
+ *   FP8 per-head quant, paged append/gather, trace-level Belady: specified by the
+ *   README (README.md:93-97, 157-159, 328-331, 343-346) whose code is absent from the
+ *   tree; the exact semantics restated here are the ones include/zenyx_kv.h documents.
+ *
+ * Arithmetic is written from the definitions (OCP OFP8 v1.0 for e4m3fn, IEEE-754
+ * binary16/bfloat16 round-to-nearest-even) with double-precision helpers, not with the
+ * bit tricks the GPU kernels use, so the two implementations are independent.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ZXO_NEVER 0x7FFFFFFF
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ---------------------------------------------------------------- rounding helpers */
+
+/* Round |a| (finite, >= 0) to the grid of a binary format with `mbits` stored mantissa
+ * bits and minimum normal exponent `emin`, nearest-even.  Exact in double for every
+ * float input because the grid spacing is a power of two. */
+static double round_to_grid(double a, int mbits, int emin) {
+  if (a == 0.0) return 0.0;
+  int e;
+  frexp(a, &e); /* a = m * 2^e, m in [0.5, 1) */
+  int E = e - 1;
+  if (E < emin) E = emin;
+  double q = ldexp(1.0, E - mbits);
+  return rint(a / q) * q; /* default rounding mode is round-to-nearest-even */
+}
+
+/* OCP e4m3fn: bias 7, 3 mantissa bits, no infinities, S.1111.111 is NaN, max 448.
+ * Overflow (a value that rounds above 448) and Inf/NaN give NaN with the input sign. */
+uint8_t zxo_e4m3_encode(float f) {
+  uint8_t sign = (uint8_t)((f2u(f) >> 24) & 0x80);
+  if (isnan(f) || isinf(f)) return sign | 0x7F;
+  double r = round_to_grid(fabs((double)f), 3, -6);
+  if (r > 448.0) return sign | 0x7F;
+  if (r == 0.0) return sign;
+  int e;
+  frexp(r, &e);
+  int E = e - 1;
+  if (E < -6) return sign | (uint8_t)(r / ldexp(1.0, -9)); /* subnormal: m * 2^-9 */
+  int mant = (int)(r / ldexp(1.0, E - 3)) - 8;
+  return sign | (uint8_t)(((E + 7) << 3) | mant);
+}
+
+float zxo_e4m3_decode(uint8_t c) {
+  int s = c >> 7, e = (c >> 3) & 0xF, m = c & 7;
+  float v;
+  if (e == 15 && m == 7) v = NAN;
+  else if (e == 0) v = (float)ldexp((double)m, -9);
+  else v = (float)ldexp((double)(8 + m), e - 10);
+  return s ? -v : v;
+}
+
+/* float -> bfloat16 bits, nearest-even; NaN -> 0x7FC0. */
+uint16_t zxo_bf16_rne(float f) {
+  if (isnan(f)) return 0x7FC0;
+  uint16_t sign = (uint16_t)((f2u(f) >> 16) & 0x8000);
+  if (isinf(f)) return sign | 0x7F80;
+  double r = round_to_grid(fabs((double)f), 7, -126);
+  if (r >= 0x1p128) return sign | 0x7F80; /* rounds past the largest finite bf16 */
+  return sign | (uint16_t)(f2u((float)r) >> 16);
+}
+
+float zxo_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* float -> binary16 bits, nearest-even; NaN -> 0x7E00. */
+uint16_t zxo_f16_rne(float f) {
+  if (isnan(f)) return 0x7E00;
+  uint16_t sign = (uint16_t)((f2u(f) >> 16) & 0x8000);
+  if (isinf(f)) return sign | 0x7C00;
+  double r = round_to_grid(fabs((double)f), 10, -14);
+  if (r > 65504.0) return sign | 0x7C00;
+  if (r == 0.0) return sign;
+  int e;
+  frexp(r, &e);
+  int E = e - 1;
+  if (E < -14) return sign | (uint16_t)(r / ldexp(1.0, -24));
+  int mant = (int)(r / ldexp(1.0, E - 10)) - 1024;
+  return sign | (uint16_t)(((E + 15) << 10) | mant);
+}
+
+float zxo_f16_to_f32(uint16_t h) {
+  int s = h >> 15, e = (h >> 10) & 0x1F, m = h & 0x3FF;
+  double v;
+  if (e == 31) v = m ? NAN : INFINITY;
+  else if (e == 0) v = ldexp((double)m, -24);
+  else v = ldexp((double)(1024 + m), e - 25);
+  return (float)(s ? -v : v);
+}
+
+void zxo_e4m3_encode_array(const float *in, uint8_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = zxo_e4m3_encode(in[i]);
+}
+void zxo_e4m3_decode_array(const uint8_t *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = zxo_e4m3_decode(in[i]);
+}
+void zxo_bf16_rne_array(const float *in, uint16_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = zxo_bf16_rne(in[i]);
+}
+void zxo_f16_rne_array(const float *in, uint16_t *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = zxo_f16_rne(in[i]);
+}
+
+/* ---------------------------------------------------------------- FP8 per-head */
+
+/* s = fp32(max(amax, 1e-8f) / 448.0f); a NaN amax gives NaN. */
+float zxo_fp8_scale(float amax) {
+  if (isnan(amax)) return u2f(0x7FC00000u);
+  float a = amax < 1e-8f ? 1e-8f : amax;
+  return a / 448.0f;
+}
+
+/* Code of one value under slab scale s (include/zenyx_kv.h numeric contract). */
+uint8_t zxo_fp8_code(float x, float s) {
+  if (isnan(s)) return 0x7F;
+  if (isinf(s)) {
+    if (isnan(x) || isinf(x)) return 0x7F;
+    return (uint8_t)((f2u(x) >> 24) & 0x80);
+  }
+  return zxo_e4m3_encode(x / s);
+}
+
+uint16_t zxo_fp8_dequant_value(uint8_t c, float s) { return zxo_bf16_rne(zxo_e4m3_decode(c) * s); }
+
+/* Layout [n_outer][n_batch][n_heads][run]; scales [n_outer][n_heads]. */
+void zxo_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_heads,
+                         int64_t run, uint8_t *codes, float *scales) {
+  for (int64_t o = 0; o < n_outer; ++o)
+    for (int64_t h = 0; h < n_heads; ++h) {
+      float amax = 0.0f;
+      int nan = 0;
+      for (int64_t b = 0; b < n_batch; ++b) {
+        const uint16_t *p = x + ((o * n_batch + b) * n_heads + h) * run;
+        for (int64_t i = 0; i < run; ++i) {
+          float v = fabsf(zxo_bf16_to_f32(p[i]));
+          if (isnan(v)) nan = 1;
+          else if (v > amax) amax = v;
+        }
+      }
+      float s = zxo_fp8_scale(nan ? NAN : amax);
+      scales[o * n_heads + h] = s;
+      for (int64_t b = 0; b < n_batch; ++b) {
+        int64_t base = ((o * n_batch + b) * n_heads + h) * run;
+        for (int64_t i = 0; i < run; ++i) codes[base + i] = zxo_fp8_code(zxo_bf16_to_f32(x[base + i]), s);
+      }
+    }
+}
+
+void zxo_fp8_dequant_heads(const uint8_t *codes, const float *scales, int64_t n_outer,
+                           int64_t n_batch, int64_t n_heads, int64_t run, uint16_t *y) {
+  for (int64_t o = 0; o < n_outer; ++o)
+    for (int64_t b = 0; b < n_batch; ++b)
+      for (int64_t h = 0; h < n_heads; ++h) {
+        float s = scales[o * n_heads + h];
+        int64_t base = ((o * n_batch + b) * n_heads + h) * run;
+        for (int64_t i = 0; i < run; ++i) y[base + i] = zxo_fp8_dequant_value(codes[base + i], s);
+      }
+}
+
+/* ---------------------------------------------------------------- paged KV cache */
+
+/* Token-major layer batch x[n_tok][2][H][D] (stride x_layer_stride elements between
+ * layers) -> scales[L][2][H]. */
+void zxo_kv_scales(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, int64_t n_tok,
+                   int32_t n_heads, int32_t head_dim, float *scales) {
+  int64_t row = 2LL * n_heads * head_dim;
+  for (int32_t l = 0; l < n_layers; ++l)
+    for (int32_t s = 0; s < 2 * n_heads; ++s) {
+      float amax = 0.0f;
+      int nan = 0;
+      for (int64_t t = 0; t < n_tok; ++t) {
+        const uint16_t *p = x + l * x_layer_stride + t * row + (int64_t)s * head_dim;
+        for (int32_t d = 0; d < head_dim; ++d) {
+          float v = fabsf(zxo_bf16_to_f32(p[d]));
+          if (isnan(v)) nan = 1;
+          else if (v > amax) amax = v;
+        }
+      }
+      scales[(int64_t)l * 2 * n_heads + s] = zxo_fp8_scale(nan ? NAN : amax);
+    }
+}
+
+/* Paged append; returns the OR of ZX_KERR_* bits (1 page range, 2 position range). */
+int32_t zxo_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
+                            int64_t n_tok, int32_t n_heads, int32_t head_dim,
+                            const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
+                            const int32_t *block_tables, int32_t max_blocks, int32_t page_size,
+                            uint8_t *pool, int64_t pool_layer_stride, int64_t n_pages,
+                            float *scales, int32_t static_scales) {
+  int32_t err = 0;
+  if (!static_scales) zxo_kv_scales(x, x_layer_stride, n_layers, n_tok, n_heads, head_dim, scales);
+  int64_t row = 2LL * n_heads * head_dim;
+  for (int32_t l = 0; l < n_layers; ++l)
+    for (int32_t b = 0; b < n_seqs; ++b)
+      for (int64_t t = cu_seqlens[b]; t < cu_seqlens[b + 1]; ++t) {
+        int64_t pos = (start_pos ? start_pos[b] : 0) + (t - cu_seqlens[b]);
+        if (pos < 0 || pos >= (int64_t)max_blocks * page_size) { err |= 2; continue; }
+        int64_t page = block_tables[(int64_t)b * max_blocks + pos / page_size];
+        if (page < 0 || page >= n_pages) { err |= 1; continue; }
+        int64_t slot = pos % page_size;
+        for (int32_t s = 0; s < 2 * n_heads; ++s) {
+          float sc = scales[(int64_t)l * 2 * n_heads + s];
+          const uint16_t *src = x + l * x_layer_stride + t * row + (int64_t)s * head_dim;
+          uint8_t *dst = pool + l * pool_layer_stride +
+                         ((page * 2 * n_heads + s) * page_size + slot) * head_dim;
+          for (int32_t d = 0; d < head_dim; ++d) dst[d] = zxo_fp8_code(zxo_bf16_to_f32(src[d]), sc);
+        }
+      }
+  return err;
+}
+
+/* Paged gather + dequant of one layer -> k_out/v_out [B][H][out_len][D]. */
+int32_t zxo_kv_gather_dequant(const uint8_t *pool, int64_t n_pages, int32_t n_heads,
+                              int32_t head_dim, int32_t page_size, const float *scales,
+                              const int32_t *block_tables, int32_t max_blocks,
+                              const int32_t *seq_lens, int32_t n_seqs, int32_t out_len,
+                              uint16_t *k_out, uint16_t *v_out) {
+  int32_t err = 0;
+  for (int32_t b = 0; b < n_seqs; ++b)
+    for (int32_t kv = 0; kv < 2; ++kv)
+      for (int32_t h = 0; h < n_heads; ++h) {
+        uint16_t *out = (kv ? v_out : k_out) + (((int64_t)b * n_heads + h) * out_len) * head_dim;
+        float sc = scales[kv * n_heads + h];
+        for (int64_t t = 0; t < out_len; ++t) {
+          uint16_t *o = out + t * head_dim;
+          int64_t page = -1;
+          if (t < seq_lens[b]) {
+            if (t / page_size < max_blocks) {
+              page = block_tables[(int64_t)b * max_blocks + t / page_size];
+              if (page < 0 || page >= n_pages) { err |= 1; page = -1; }
+            } else {
+              err |= 2;
+            }
+          }
+          if (page < 0) { memset(o, 0, (size_t)head_dim * 2); continue; }
+          const uint8_t *src = pool + ((page * 2 + kv) * n_heads + h) * (int64_t)page_size * head_dim +
+                               (t % page_size) * head_dim;
+          for (int32_t d = 0; d < head_dim; ++d) o[d] = zxo_fp8_dequant_value(src[d], sc);
+        }
+      }
+  return err;
+}
+
+/* ---------------------------------------------------------------- legacy int8 */
+
+/* Round a float to the storage dtype and back (0 bf16, 1 f16, 2 f32), as torch stores
+ * every intermediate of precision.py:10-11 in the input dtype. */
+static float to_dtype(float v, int dtype) {
+  if (dtype == 0) return zxo_bf16_to_f32(zxo_bf16_rne(v));
+  if (dtype == 1) return zxo_f16_to_f32(zxo_f16_rne(v));
+  return v;
+}
+static float load_dtype(const void *x, int dtype, int64_t i) {
+  if (dtype == 0) return zxo_bf16_to_f32(((const uint16_t *)x)[i]);
+  if (dtype == 1) return zxo_f16_to_f32(((const uint16_t *)x)[i]);
+  return ((const float *)x)[i];
+}
+
+/* precision.py:10: scale = tensor.abs().amax().clamp_min(1e-8) / 127.0, all in dtype;
+ * precision.py:11: q = clamp(round(tensor / scale), -127, 127).to(int8).
+ * Division is true IEEE division computed in fp32 (torch's CPU opmath) and rounded to
+ * dtype; round() is half-to-even.  Returns the scale as a float (exactly a dtype value). */
+float zxo_int8_legacy_quant(const void *x, int dtype, int64_t n, int8_t *q) {
+  float amax = 0.0f;
+  int nan = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    float v = fabsf(load_dtype(x, dtype, i));
+    if (isnan(v)) nan = 1;
+    else if (v > amax) amax = v;
+  }
+  float a = nan ? NAN : amax;
+  float lo = to_dtype(1e-8f, dtype);
+  if (!(a >= lo) && !isnan(a)) a = lo;
+  float s = to_dtype(a / 127.0f, dtype);
+  for (int64_t i = 0; i < n; ++i) {
+    float r = rintf(to_dtype(load_dtype(x, dtype, i) / s, dtype));
+    if (isnan(r)) { q[i] = 0; continue; } /* int8 of NaN is not defined by the reference */
+    if (r > 127.0f) r = 127.0f;
+    if (r < -127.0f) r = -127.0f;
+    q[i] = (int8_t)r;
+  }
+  return s;
+}
+
+/* precision.py:16: (q.float() * scale).to(bfloat16). */
+void zxo_int8_legacy_dequant(const int8_t *q, float scale, int64_t n, uint16_t *y) {
+  for (int64_t i = 0; i < n; ++i) y[i] = zxo_bf16_rne((float)q[i] * scale);
+}
+
+/* ---------------------------------------------------------------- Belady */
+
+/* belady.py:39-51 over integer slots: the largest key > -1 among resident slots, ties to
+ * the smallest slot (the reference breaks ties by set iteration order, which Python does
+ * not fix).  out = {slot, key} or {-1, -1}. */
+void zxo_belady_argmax(const int64_t *keys, const uint8_t *resident, int64_t n, int64_t *out) {
+  int64_t best = -1, bestk = -1;
+  for (int64_t i = 0; i < n; ++i)
+    if (resident[i] && keys[i] > bestk) { bestk = keys[i]; best = i; }
+  out[0] = best;
+  out[1] = best < 0 ? -1 : bestk;
+}
+
+/* next_use[i]: next position of trace[i] or ZXO_NEVER; prev_use[i]: previous or -1. */
+void zxo_next_use(const int32_t *trace, int64_t n, int32_t n_pages, int32_t *next_use,
+                  int32_t *prev_use) {
+  int32_t *last = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  for (int32_t p = 0; p < n_pages; ++p) last[p] = ZXO_NEVER;
+  for (int64_t i = n - 1; i >= 0; --i) {
+    next_use[i] = last[trace[i]];
+    last[trace[i]] = (int32_t)i;
+  }
+  for (int32_t p = 0; p < n_pages; ++p) last[p] = -1;
+  for (int64_t i = 0; i < n; ++i) {
+    prev_use[i] = last[trace[i]];
+    last[trace[i]] = (int32_t)i;
+  }
+  free(last);
+}
+
+/* Indexed binary max-heap of resident pages ordered by (key desc, page asc). */
+typedef struct {
+  int32_t *h;   /* heap array of page ids */
+  int32_t *pos; /* page -> index in h, or -1 */
+  const int32_t *key;
+  int64_t size;
+} zxo_heap;
+
+static inline int heap_before(const zxo_heap *H, int32_t a, int32_t b) {
+  int32_t ka = H->key[a], kb = H->key[b];
+  return ka > kb || (ka == kb && a < b);
+}
+static void heap_swap(zxo_heap *H, int64_t i, int64_t j) {
+  int32_t a = H->h[i], b = H->h[j];
+  H->h[i] = b; H->h[j] = a;
+  H->pos[b] = (int32_t)i; H->pos[a] = (int32_t)j;
+}
+static void heap_up(zxo_heap *H, int64_t i) {
+  while (i > 0) {
+    int64_t p = (i - 1) / 2;
+    if (!heap_before(H, H->h[i], H->h[p])) break;
+    heap_swap(H, i, p);
+    i = p;
+  }
+}
+static void heap_down(zxo_heap *H, int64_t i) {
+  for (;;) {
+    int64_t l = 2 * i + 1, r = l + 1, m = i;
+    if (l < H->size && heap_before(H, H->h[l], H->h[m])) m = l;
+    if (r < H->size && heap_before(H, H->h[r], H->h[m])) m = r;
+    if (m == i) break;
+    heap_swap(H, i, m);
+    i = m;
+  }
+}
+
+/* Belady MIN over a whole trace (include/zenyx_kv.h, zx_belady_simulate): a miss with
+ * `capacity` pages resident evicts the page of farthest next use (ties: smallest page),
+ * then admits the missed page; a hit moves the page's key to its next use.  The per-miss
+ * argmax of belady.py:46-50 is kept exactly, with a heap instead of a linear scan.
+ * Returns the number of evictions (entries beyond evict_cap are counted, not stored);
+ * stats[0] = misses, stats[1] = hits, stats[2] = final resident count. */
+int64_t zxo_belady_simulate(const int32_t *trace, int64_t n, int32_t n_pages, int64_t capacity,
+                            int32_t *evict_pos, int32_t *evict_page, int64_t evict_cap,
+                            int64_t *stats) {
+  int32_t *next_use = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n ? n : 1));
+  int32_t *prev_use = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n ? n : 1));
+  int32_t *key = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  zxo_heap H;
+  H.h = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  H.pos = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  H.key = key;
+  H.size = 0;
+  zxo_next_use(trace, n, n_pages, next_use, prev_use);
+  for (int32_t p = 0; p < n_pages; ++p) { H.pos[p] = -1; key[p] = -1; }
+  int64_t ev = 0, misses = 0, hits = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    int32_t p = trace[i];
+    if (H.pos[p] >= 0) {
+      ++hits;
+      key[p] = next_use[i];
+      heap_up(&H, H.pos[p]);
+      heap_down(&H, H.pos[p]);
+      continue;
+    }
+    ++misses;
+    if (H.size >= capacity && H.size > 0) {
+      int32_t v = H.h[0];
+      heap_swap(&H, 0, H.size - 1);
+      H.size--;
+      H.pos[v] = -1;
+      if (H.size) heap_down(&H, 0);
+      if (ev < evict_cap) { evict_pos[ev] = (int32_t)i; evict_page[ev] = v; }
+      ++ev;
+    }
+    key[p] = next_use[i];
+    H.h[H.size] = p;
+    H.pos[p] = (int32_t)H.size;
+    H.size++;
+    heap_up(&H, H.size - 1);
+  }
+  if (stats) { stats[0] = misses; stats[1] = hits; stats[2] = H.size; }
+  free(next_use); free(prev_use); free(key); free(H.h); free(H.pos);
+  return ev;
+}
+
+/* Ring-attention access schedule of degree `ring` on one GPU (kv_tiering.py:69-73
+ * generalised).  Layer l owns pages [l*ring*shard_pages, (l+1)*ring*shard_pages), split
+ * into `ring` shards of shard_pages pages.  Forward: for each layer, for step s, for each
+ * simulated device d, the pages of shard (d - s) mod ring in order.  Backward: the exact
+ * reverse of the forward sequence.  out holds 2 * L * ring * ring * shard_pages ids. */
+void zxo_ring_trace(int32_t n_layers, int32_t ring, int32_t shard_pages, int32_t *out) {
+  int64_t k = 0;
+  for (int32_t l = 0; l < n_layers; ++l)
+    for (int32_t s = 0; s < ring; ++s)
+      for (int32_t d = 0; d < ring; ++d) {
+        int32_t shard = ((d - s) % ring + ring) % ring;
+        int32_t base = (l * ring + shard) * shard_pages;
+        for (int32_t j = 0; j < shard_pages; ++j) out[k++] = base + j;
+      }
+  for (int64_t i = 0; i < k; ++i) out[k + i] = out[k - 1 - i];
+}

@@ -1,0 +1,204 @@
+"""GPU parity of the FP8 KV kernels (libzenyx_kv.so) against the CPU oracle.
+
+Codes, scales and gathered bytes must be bit-exact; dequantized bf16 must be bit-exact
+as well (stronger than the 1-ulp tolerance BASELINE.json allows), with NaN compared as
+a class because torch itself writes different NaN payloads on different paths.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from zenyx_amd import kv
+
+pytestmark = pytest.mark.gpu
+
+
+def bits16(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def assert_bf16_equal(got: np.ndarray, want: np.ndarray):
+    g_nan = (got & 0x7FFF) > 0x7F80
+    w_nan = (want & 0x7FFF) > 0x7F80
+    np.testing.assert_array_equal(g_nan, w_nan)
+    np.testing.assert_array_equal(got[~g_nan], want[~w_nan])
+
+
+def e4m3_probe_values() -> np.ndarray:
+    """All bf16 values, every e4m3 rounding midpoint +-0..3 ulp, random fp32."""
+    allbf = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    grid = O.e4m3_decode(np.arange(256, dtype=np.uint8))
+    grid = np.unique(np.abs(grid[np.isfinite(grid)]).astype(np.float64))
+    grid = np.concatenate([grid, [480.0]])
+    mids = ((grid[:-1] + grid[1:]) / 2).astype(np.float32)
+    near = [mids]
+    up, dn = mids, mids
+    for _ in range(3):
+        up = np.nextafter(up, np.float32(np.inf))
+        dn = np.nextafter(dn, np.float32(0))
+        near += [up, dn]
+    rng = np.random.default_rng(7)
+    rnd = np.concatenate([
+        rng.uniform(-500, 500, 1 << 20).astype(np.float32),
+        (rng.choice([-1, 1], 1 << 20) * np.exp2(rng.uniform(-14, 9, 1 << 20))).astype(np.float32),
+    ])
+    near = np.concatenate(near)
+    return np.concatenate([allbf, near, -near, rnd]).astype(np.float32)
+
+
+def test_e4m3_device_encode_matches_oracle(dev):
+    v = e4m3_probe_values()
+    got = kv.fp8_encode_f32(torch.from_numpy(v).to(dev)).cpu().numpy()
+    want = O.e4m3_encode(v)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, e.g. {v[bad[:5]]} -> {got[bad[:5]]} vs {want[bad[:5]]}"
+
+
+def make_kv_cache(L, B, H, T, D, seed, outlier_heads=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((L, 2, B, H, T, D), generator=g, dtype=torch.float32)
+    if outlier_heads:
+        for l in range(L):
+            hs = torch.randperm(H, generator=g)[:outlier_heads]
+            x[l, :, :, hs] *= 50.0
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("shape,seed", [((2, 1, 12, 256, 64), 0), ((3, 2, 4, 48, 128), 1),
+                                        ((1, 3, 2, 16, 256), 2)])
+def test_fp8_quant_dequant_heads_bit_exact(dev, shape, seed):
+    L, B, H, T, D = shape
+    x = make_kv_cache(L, B, H, T, D, seed, outlier_heads=1)
+    xv = x.reshape(2 * L, B, H, T * D)
+    codes, scales = kv.fp8_quant_heads(xv.to(dev))
+    wc, ws = O.fp8_quant_heads(bits16(xv))
+    np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+    np.testing.assert_array_equal(codes.cpu().numpy(), wc)
+    y = kv.fp8_dequant_heads(codes, scales)
+    assert_bf16_equal(bits16(y), O.fp8_dequant_heads(wc, ws))
+
+
+def test_fp8_heads_special_slabs(dev):
+    """Zero slab (scale clamps to 1e-8/448), +-inf slab, NaN slab, subnormal bf16 inputs."""
+    x = torch.randn((4, 1, 4, 64), dtype=torch.float32).to(torch.bfloat16)
+    x[0, :, 0] = 0.0
+    x[1, :, 1, 5] = float("inf")
+    x[1, :, 1, 6] = -float("inf")
+    x[2, :, 2, 7] = float("nan")
+    x[3, :, 3] = torch.tensor([2.0 ** -130], dtype=torch.bfloat16) * torch.arange(64).float().to(torch.bfloat16)
+    codes, scales = kv.fp8_quant_heads(x.to(dev))
+    wc, ws = O.fp8_quant_heads(bits16(x))
+    np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+    np.testing.assert_array_equal(codes.cpu().numpy(), wc)
+    assert_bf16_equal(bits16(kv.fp8_dequant_heads(codes, scales)), O.fp8_dequant_heads(wc, ws))
+
+
+def make_append_case(L, H, D, P, lens, seed, extra_pages=7, start=None):
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    pos0 = [0] * B if start is None else list(start)
+    ends = [s + n for s, n in zip(pos0, lens)]
+    max_blocks = max((e + P - 1) // P for e in ends)
+    need = sum((e + P - 1) // P for e in ends)
+    n_pages = need + extra_pages
+    perm = torch.randperm(n_pages, generator=g).to(torch.int32)
+    bt = torch.full((B, max_blocks), -1, dtype=torch.int32)
+    k = 0
+    for b, e in enumerate(ends):
+        nb = (e + P - 1) // P
+        bt[b, :nb] = perm[k:k + nb]
+        k += nb
+    T = sum(lens)
+    x = torch.randn((L, T, 2, H, D), generator=g, dtype=torch.float32)
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
+    for b in range(B):  # 5%-style outliers: one (layer, head) per sequence x50
+        l = int(torch.randint(L, (1,), generator=g))
+        h = int(torch.randint(H, (1,), generator=g))
+        x[l, cu[b]:cu[b + 1], :, h] *= 50.0
+    sp = None if start is None else torch.tensor(pos0, dtype=torch.int32)
+    return x.to(torch.bfloat16), cu, bt, n_pages, sp
+
+
+@pytest.mark.parametrize("H,D,P", [(8, 128, 16), (12, 64, 64), (2, 256, 5)])
+def test_kv_quant_append_bit_exact(dev, H, D, P):
+    L = 3
+    lens = [1, 17, 300, 64, 129]
+    x, cu, bt, n_pages, _ = make_append_case(L, H, D, P, lens, seed=H + D + P)
+    pool = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8)
+    wpool = pool.numpy().copy()
+    wsc, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, P)
+    assert werr == 0
+    pool_d = pool.to(dev)
+    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+    np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
+    # scales alone
+    np.testing.assert_array_equal(kv.kv_scales(x.to(dev)).cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+
+
+def test_kv_quant_append_static_scales_decode_positions(dev):
+    """Decode-style append at start_pos > 0 with scales fixed by an earlier prefill."""
+    L, H, D, P = 2, 4, 128, 16
+    lens = [1, 1, 3]
+    x, cu, bt, n_pages, sp = make_append_case(L, H, D, P, lens, seed=11, start=[15, 40, 7])
+    scales = torch.rand((L, 2, H), dtype=torch.float32) * 0.05 + 1e-3
+    pool = torch.randint(0, 255, (L, n_pages, 2, H, P, D), dtype=torch.uint8)
+    wpool = pool.numpy().copy()
+    _, werr = O.kv_quant_append(bits16(x), cu.numpy(), sp.numpy(), bt.numpy(), wpool, P,
+                                scales=scales.numpy())
+    assert werr == 0
+    pool_d = pool.to(dev)
+    kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, scales=scales.to(dev),
+                       start_pos=sp.to(dev), static_scales=True, check=True)
+    np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
+
+
+def test_kv_quant_append_rejects_bad_page_ids(dev):
+    L, H, D, P = 1, 2, 64, 16
+    x, cu, bt, n_pages, _ = make_append_case(L, H, D, P, [20, 5], seed=3)
+    bt[1, 0] = n_pages + 3  # out of range: must not be written, must be flagged
+    pool = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8)
+    wpool = pool.numpy().copy()
+    _, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, P)
+    assert werr == 1
+    pool_d = pool.to(dev)
+    with pytest.raises(ValueError, match="block table"):
+        kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True)
+    np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
+
+
+@pytest.mark.parametrize("H,D,P,out_len", [(8, 128, 16, 512), (4, 64, 32, 200), (2, 256, 7, 100)])
+def test_kv_gather_dequant_bit_exact(dev, H, D, P, out_len):
+    g = torch.Generator().manual_seed(H * D + P)
+    n_pages = 300
+    B = 5
+    max_blocks = (out_len + P - 1) // P
+    pool = torch.randint(0, 256, (n_pages, 2, H, P, D), dtype=torch.uint8, generator=g)
+    pool[pool == 0x7F] = 0x11
+    pool[pool == 0xFF] = 0x91
+    seq_lens = torch.tensor([out_len, 1, out_len // 2, 0, out_len - 3], dtype=torch.int32)
+    bt = torch.stack([torch.randperm(n_pages, generator=g)[:max_blocks] for _ in range(B)]).to(torch.int32)
+    scales = (torch.rand((2, H), generator=g) * 0.999 + 1e-3).float()
+    wk, wv, werr = O.kv_gather_dequant(pool.numpy(), scales.numpy(), bt.numpy(), seq_lens.numpy(), out_len)
+    assert werr == 0
+    k, v = kv.kv_gather_dequant(pool.to(dev), scales.to(dev), bt.to(dev), seq_lens.to(dev), out_len, check=True)
+    assert_bf16_equal(bits16(k), wk)
+    assert_bf16_equal(bits16(v), wv)
+
+
+def test_kv_gather_dequant_nan_codes_and_bad_pages(dev):
+    H, D, P, out_len = 2, 64, 16, 64
+    pool = torch.full((10, 2, H, P, D), 0x7F, dtype=torch.uint8)
+    pool[:, :, :, :, 1::2] = 0xFF
+    bt = torch.tensor([[0, 1, 2, 3], [4, 5, 11, 6]], dtype=torch.int32)
+    seq_lens = torch.tensor([64, 64], dtype=torch.int32)
+    scales = torch.ones((2, H), dtype=torch.float32)
+    wk, wv, werr = O.kv_gather_dequant(pool.numpy(), scales.numpy(), bt.numpy(), seq_lens.numpy(), out_len)
+    assert werr == 1
+    with pytest.raises(ValueError, match="block table"):
+        kv.kv_gather_dequant(pool.to(dev), scales.to(dev), bt.to(dev), seq_lens.to(dev), out_len, check=True)
+    k, v = kv.kv_gather_dequant(pool.to(dev), scales.to(dev), bt.to(dev), seq_lens.to(dev), out_len)
+    assert_bf16_equal(bits16(k), wk)
+    assert_bf16_equal(bits16(v), wv)

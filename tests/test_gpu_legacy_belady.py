@@ -1,0 +1,73 @@
+"""GPU parity of the legacy int8 path (precision.py) and of Belady victim selection /
+next-use tables against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from zenyx_amd import kv
+
+pytestmark = pytest.mark.gpu
+
+
+def raw(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("mag", [1.0, 1e-3, 3e4, 0.0])
+def test_int8_legacy_quant_dequant(dev, dt, mag):
+    g = torch.Generator().manual_seed(int(mag * 7) + len(dt))
+    x = (torch.randn(4099, generator=g) * mag).to(DTYPES[dt])
+    q, s = kv.int8_legacy_quant(x.to(dev))
+    wq, ws = O.int8_legacy_quant(raw(x), dt)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+    assert s.dtype == x.dtype and s.dim() == 0
+    assert np.float32(s.float().item()).tobytes() == np.float32(ws).tobytes()
+    y = kv.int8_legacy_dequant(q, s)
+    assert y.dtype == torch.bfloat16
+    got, want = raw(y), O.int8_legacy_dequant(wq, ws)
+    # NaN (an f16 input that overflowed to inf gives an inf scale) matches NaN as a class
+    g_nan, w_nan = (got & 0x7FFF) > 0x7F80, (want & 0x7FFF) > 0x7F80
+    np.testing.assert_array_equal(g_nan, w_nan)
+    np.testing.assert_array_equal(got[~g_nan], want[~w_nan])
+
+
+def test_int8_legacy_empty_raises(dev):
+    with pytest.raises(RuntimeError):
+        kv.int8_legacy_quant(torch.empty(0, device=dev))
+
+
+def test_belady_argmax_matches_oracle(dev):
+    rng = np.random.default_rng(5)
+    for n in (1, 7, 1000, 100_003):
+        keys = rng.integers(-3, 50, n).astype(np.int64)  # many ties and many <= -1
+        keys[rng.integers(0, n, max(1, n // 10))] = 10**18
+        res = (rng.random(n) < 0.6).astype(np.uint8)
+        out = kv.belady_argmax(torch.from_numpy(keys).to(dev), torch.from_numpy(res).to(dev)).cpu().tolist()
+        assert tuple(out) == O.belady_argmax(keys, res)
+    # nothing qualifies: every resident key <= -1 (belady.py:45-51 returns None)
+    keys = np.full(10, -1, np.int64)
+    out = kv.belady_argmax(torch.from_numpy(keys).to(dev), torch.ones(10, dtype=torch.uint8, device=dev))
+    assert out.cpu().tolist() == [-1, -1]
+
+
+def test_next_use_matches_oracle(dev):
+    rng = np.random.default_rng(9)
+    for n, n_pages in ((1, 1), (50, 3), (100_000, 777), (300_000, 1 << 17)):
+        trace = rng.integers(0, n_pages, n).astype(np.int32)
+        nu, pu = kv.next_use(torch.from_numpy(trace).to(dev), n_pages, check=True)
+        wnu, wpu = O.next_use(trace, n_pages)
+        np.testing.assert_array_equal(nu.cpu().numpy(), wnu)
+        np.testing.assert_array_equal(pu.cpu().numpy(), wpu)
+    ring = O.ring_trace(2, 8, 16)
+    nu, pu = kv.next_use(torch.from_numpy(ring).to(dev), 2 * 8 * 16)
+    wnu, wpu = O.next_use(ring, 2 * 8 * 16)
+    np.testing.assert_array_equal(nu.cpu().numpy(), wnu)
+    np.testing.assert_array_equal(pu.cpu().numpy(), wpu)

@@ -1,0 +1,114 @@
+// zx_gather.hip -- paged gather + FP8 dequant for decode.
+// Pool layout per layer: [n_pages][2][H][P][D] uint8; output [B][H][T][D] bf16 per kv.
+// A block owns TT consecutive positions of one (b, h, kv) row; thread work units are
+// 16 codes (16 B in, 32 B out), consecutive threads write consecutive output bytes.
+// HBM-bound: 1 B read + 2 B written per element, plus one int32 block-table entry per
+// P positions.
+#include "zx_common.h"
+
+namespace zx {
+
+constexpr int GD_THREADS = 256;
+constexpr int GD_UNITS = 4;  // work units per thread
+
+struct GatherGeom {
+  int32_t n_heads, head_dim, page_size, max_blocks, out_len;
+  int32_t vpd_log2;  // log2(D / 16)
+  int32_t tt;        // positions per block
+  int64_t chunks_per_row;
+  int64_t n_pages;
+};
+
+__global__ void __launch_bounds__(GD_THREADS)
+gather_dequant_kernel(const uint8_t *pool, GatherGeom g, const float *scales,
+                      const int32_t *block_tables, const int32_t *seq_lens, uint16_t *k_out,
+                      uint16_t *v_out, int32_t *err) {
+  const int64_t blk = blockIdx.x;
+  const int64_t row = blk / g.chunks_per_row;
+  const int64_t chunk = blk - row * g.chunks_per_row;
+  const int kv = (int)(row & 1);
+  const int64_t bh = row >> 1;
+  const int h = (int)(bh % g.n_heads);
+  const int64_t b = bh / g.n_heads;
+  const float s = scales[kv * g.n_heads + h];
+  const int32_t len = seq_lens[b];
+  const int32_t *bt = block_tables + b * g.max_blocks;
+  const int64_t page_bytes = 2LL * g.n_heads * g.page_size * g.head_dim;
+  const uint8_t *pbase = pool + ((int64_t)kv * g.n_heads + h) * g.page_size * g.head_dim;
+  uint16_t *out = (kv ? v_out : k_out) + bh * (int64_t)g.out_len * g.head_dim;
+  const int vpd_mask = (1 << g.vpd_log2) - 1;
+
+  uint4 c[GD_UNITS];
+  int64_t o_off[GD_UNITS];
+  bool live[GD_UNITS], have[GD_UNITS];
+  int32_t e = 0;
+#pragma unroll
+  for (int k = 0; k < GD_UNITS; ++k) {
+    const int u = k * GD_THREADS + threadIdx.x;
+    const int64_t t = chunk * g.tt + (u >> g.vpd_log2);
+    const int dc = u & vpd_mask;
+    live[k] = t < g.out_len;
+    have[k] = false;
+    o_off[k] = t * g.head_dim + dc * 16;
+    c[k] = make_uint4(0, 0, 0, 0);
+    if (live[k] && t < len) {
+      const int64_t bi = t / g.page_size;
+      if (bi < g.max_blocks) {
+        const int64_t page = bt[bi];
+        if (page >= 0 && page < g.n_pages) {
+          c[k] = *reinterpret_cast<const uint4 *>(pbase + page * page_bytes +
+                                                   (t - bi * g.page_size) * g.head_dim + dc * 16);
+          have[k] = true;
+        } else {
+          e |= ZX_KERR_PAGE_RANGE;
+        }
+      } else {
+        e |= ZX_KERR_POS_RANGE;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < GD_UNITS; ++k) {
+    if (!live[k]) continue;
+    uint4 o0 = make_uint4(0, 0, 0, 0), o1 = o0;
+    if (have[k]) dequant16(c[k], s, o0, o1);
+    uint4 *dst = reinterpret_cast<uint4 *>(out + o_off[k]);
+    dst[0] = o0;
+    dst[1] = o1;
+  }
+  if (e && err) atomicOr(err, e);
+}
+
+}  // namespace zx
+
+using namespace zx;
+
+extern "C" int zx_kv_gather_dequant(const uint8_t *pool, int64_t n_pages, int32_t n_heads, int32_t head_dim,
+                                    int32_t page_size, const float *scales, const int32_t *block_tables,
+                                    int32_t max_blocks, const int32_t *seq_lens, int32_t n_seqs,
+                                    int32_t out_len, uint16_t *k_out, uint16_t *v_out, int32_t *err,
+                                    zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(pool && scales && block_tables && seq_lens && k_out && v_out,
+             "kv_gather_dequant: null pointer");
+  ZX_REQUIRE(n_pages > 0 && n_heads > 0 && page_size > 0 && max_blocks > 0 && n_seqs > 0 && out_len >= 0,
+             "kv_gather_dequant: sizes must be positive");
+  if (!(head_dim == 64 || head_dim == 128 || head_dim == 256))
+    return fail(ZX_ERR_UNSUPPORTED, "kv_gather_dequant: head_dim %d not in {64, 128, 256}", head_dim);
+  if (out_len == 0) return ZX_OK;
+  GatherGeom g;
+  g.n_heads = n_heads;
+  g.head_dim = head_dim;
+  g.page_size = page_size;
+  g.max_blocks = max_blocks;
+  g.out_len = out_len;
+  g.vpd_log2 = head_dim == 64 ? 2 : (head_dim == 128 ? 3 : 4);
+  g.tt = (GD_THREADS * GD_UNITS) >> g.vpd_log2;
+  g.chunks_per_row = ceil_div(out_len, g.tt);
+  g.n_pages = n_pages;
+  const int64_t n_blocks = 2LL * n_seqs * n_heads * g.chunks_per_row;
+  if (n_blocks >= (1LL << 31)) return fail(ZX_ERR_UNSUPPORTED, "kv_gather_dequant: output too large");
+  gather_dequant_kernel<<<(unsigned)n_blocks, GD_THREADS, 0, as_stream(stream)>>>(
+      pool, g, scales, block_tables, seq_lens, k_out, v_out, err);
+  return check_launch("gather_dequant");
+}

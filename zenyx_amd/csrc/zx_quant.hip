@@ -1,0 +1,544 @@
+// zx_quant.hip -- quantisation kernels of libzenyx_kv.so (gfx950):
+//   * legacy per-tensor int8 (zenyx/streaming/precision.py:8-16)
+//   * FP8 e4m3fn per-(outer, head) quant / dequant (FP8KVQuantizer, README.md:157, 329)
+//   * per-(layer, kv, head) scales and the paged append with fused quant
+// Every kernel streams 16-byte vectors; all are HBM-bound (no MFMA: nothing here is a
+// contraction).
+#include "zx_common.h"
+
+namespace zx {
+
+__global__ void fill_u32_kernel(uint32_t *p, int64_t n, uint32_t v) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+static int fill_u32(uint32_t *p, int64_t n, uint32_t v, hipStream_t st) {
+  if (n <= 0) return ZX_OK;
+  fill_u32_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(p, n, v);
+  return check_launch("fill_u32");
+}
+
+// Block-wide max of one uint32 per thread; result valid in every thread.
+__device__ __forceinline__ uint32_t block_max(uint32_t v) {
+  __shared__ uint32_t red[16];
+  v = group_max(v, 64);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  const int nw = (blockDim.x + 63) >> 6;
+  uint32_t m = 0;
+  for (int i = 0; i < nw; ++i) m = max(m, red[i]);
+  __syncthreads();
+  return m;
+}
+
+// ================================================================== legacy int8
+
+// Storage dtypes of the legacy path: magnitude mask and "is NaN" threshold of the raw bits.
+template <int DT> struct Dt;
+template <> struct Dt<ZX_BF16> {
+  __device__ static float load(const void *x, int64_t i) {
+    return __uint_as_float((uint32_t)((const uint16_t *)x)[i] << 16);
+  }
+  __device__ static uint32_t absbits(const void *x, int64_t i) { return ((const uint16_t *)x)[i] & 0x7FFFu; }
+  __device__ static float from_absbits(uint32_t b) { return __uint_as_float(b << 16); }
+  __device__ static float round(float v) { return (float)(__bf16)v; }
+  __device__ static void store(void *p, float v) {
+    __bf16 h = (__bf16)v;
+    *(uint16_t *)p = __builtin_bit_cast(uint16_t, h);
+  }
+};
+template <> struct Dt<ZX_F16> {
+  __device__ static float load(const void *x, int64_t i) {
+    return (float)__builtin_bit_cast(_Float16, ((const uint16_t *)x)[i]);
+  }
+  __device__ static uint32_t absbits(const void *x, int64_t i) { return ((const uint16_t *)x)[i] & 0x7FFFu; }
+  __device__ static float from_absbits(uint32_t b) { return (float)__builtin_bit_cast(_Float16, (uint16_t)b); }
+  __device__ static float round(float v) { return (float)(_Float16)v; }
+  __device__ static void store(void *p, float v) {
+    _Float16 h = (_Float16)v;
+    *(uint16_t *)p = __builtin_bit_cast(uint16_t, h);
+  }
+};
+template <> struct Dt<ZX_F32> {
+  __device__ static float load(const void *x, int64_t i) { return ((const float *)x)[i]; }
+  __device__ static uint32_t absbits(const void *x, int64_t i) {
+    return ((const uint32_t *)x)[i] & 0x7FFFFFFFu;
+  }
+  __device__ static float from_absbits(uint32_t b) { return __uint_as_float(b); }
+  __device__ static float round(float v) { return v; }
+  __device__ static void store(void *p, float v) { *(float *)p = v; }
+};
+
+// For all three formats the integer order of |x| bit patterns is the float order, with
+// NaN patterns above infinity, so an integer max is the float amax (NaN-propagating).
+template <int DT>
+__global__ void legacy_amax_kernel(const void *x, int64_t n, uint32_t *amax_bits) {
+  uint32_t m = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    m = max(m, Dt<DT>::absbits(x, i));
+  m = block_max(m);
+  if (threadIdx.x == 0) atomicMax(amax_bits, m);
+}
+
+// precision.py:10-11 with torch's CPU arithmetic: every intermediate is rounded to the
+// storage dtype, division is IEEE fp32 division, round() is half-to-even.
+template <int DT>
+__global__ void legacy_quant_kernel(const void *x, int64_t n, const uint32_t *amax_bits, int8_t *q,
+                                    void *scale_out) {
+  float a = Dt<DT>::from_absbits(*amax_bits);
+  const float lo = Dt<DT>::round(1e-8f);
+  if (a < lo) a = lo;
+  const float s = Dt<DT>::round(a / 127.0f);
+  if (blockIdx.x == 0 && threadIdx.x == 0) Dt<DT>::store(scale_out, s);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float v = __builtin_rintf(Dt<DT>::round(Dt<DT>::load(x, i) / s));
+    int8_t o;
+    if (v != v) o = 0;  // int8 of NaN is not defined by the reference; 0 is torch CPU's
+    else o = (int8_t)fminf(fmaxf(v, -127.0f), 127.0f);
+    q[i] = o;
+  }
+}
+
+template <int DT>
+__global__ void legacy_dequant_kernel(const int8_t *q, const void *scale, int64_t n, uint16_t *y) {
+  const float s = Dt<DT>::load(scale, 0);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    __bf16 h = (__bf16)((float)q[i] * s);
+    y[i] = __builtin_bit_cast(uint16_t, h);
+  }
+}
+
+static unsigned grid_for(int64_t n, int per_thread = 1) {
+  int64_t want = ceil_div(n, 256LL * per_thread);
+  int64_t cap = (int64_t)num_cus() * 16;
+  return (unsigned)(want < 1 ? 1 : (want > cap ? cap : want));
+}
+
+// ================================================================== FP8 per (outer, head)
+
+// Blocks own chunks of CHUNK_VEC 16-element vectors inside one run of one slab.
+constexpr int QH_THREADS = 256;
+constexpr int QH_VEC_PER_THREAD = 4;
+constexpr int64_t QH_CHUNK_VEC = QH_THREADS * QH_VEC_PER_THREAD;
+
+struct HeadsGeom {
+  int64_t n_batch, n_heads, vec_per_run, chunks_per_run;
+  __device__ void locate(int64_t block, int64_t &run_idx, int64_t &chunk, int64_t &slab) const {
+    run_idx = block / chunks_per_run;
+    chunk = block - run_idx * chunks_per_run;
+    const int64_t h = run_idx % n_heads;
+    const int64_t o = run_idx / (n_heads * n_batch);
+    slab = o * n_heads + h;
+  }
+};
+
+__global__ void __launch_bounds__(QH_THREADS)
+heads_amax_kernel(const uint4 *x, HeadsGeom g, uint32_t *amax_bits) {
+  int64_t run_idx, chunk, slab;
+  g.locate(blockIdx.x, run_idx, chunk, slab);
+  const uint4 *base = x + run_idx * g.vec_per_run * 2;
+  uint32_t m = 0;
+#pragma unroll
+  for (int k = 0; k < QH_VEC_PER_THREAD; ++k) {
+    int64_t v = chunk * QH_CHUNK_VEC + k * QH_THREADS + threadIdx.x;
+    if (v < g.vec_per_run) m = max(m, absmax16(base[2 * v], base[2 * v + 1]));
+  }
+  m = block_max(m);
+  if (threadIdx.x == 0) atomicMax(&amax_bits[slab], m << 16);
+}
+
+__global__ void finalize_scales_kernel(float *scales, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) scales[i] = scale_from_amax_bits(__float_as_uint(scales[i]));
+}
+
+__global__ void __launch_bounds__(QH_THREADS)
+heads_quant_kernel(const uint4 *x, HeadsGeom g, const float *scales, uint4 *codes) {
+  int64_t run_idx, chunk, slab;
+  g.locate(blockIdx.x, run_idx, chunk, slab);
+  const float s = scales[slab];
+  const int mode = scale_mode(s);
+  const float r = 1.0f / s;
+  const uint4 *src = x + run_idx * g.vec_per_run * 2;
+  uint4 *dst = codes + run_idx * g.vec_per_run;
+#pragma unroll
+  for (int k = 0; k < QH_VEC_PER_THREAD; ++k) {
+    int64_t v = chunk * QH_CHUNK_VEC + k * QH_THREADS + threadIdx.x;
+    if (v < g.vec_per_run) dst[v] = quant16(src[2 * v], src[2 * v + 1], s, r, mode);
+  }
+}
+
+__global__ void __launch_bounds__(QH_THREADS)
+heads_dequant_kernel(const uint4 *codes, HeadsGeom g, const float *scales, uint4 *y) {
+  int64_t run_idx, chunk, slab;
+  g.locate(blockIdx.x, run_idx, chunk, slab);
+  const float s = scales[slab];
+  const uint4 *src = codes + run_idx * g.vec_per_run;
+  uint4 *dst = y + run_idx * g.vec_per_run * 2;
+#pragma unroll
+  for (int k = 0; k < QH_VEC_PER_THREAD; ++k) {
+    int64_t v = chunk * QH_CHUNK_VEC + k * QH_THREADS + threadIdx.x;
+    if (v < g.vec_per_run) {
+      uint4 o0, o1;
+      dequant16(src[v], s, o0, o1);
+      dst[2 * v] = o0;
+      dst[2 * v + 1] = o1;
+    }
+  }
+}
+
+static int heads_geom(int64_t n_outer, int64_t n_batch, int64_t n_heads, int64_t run, HeadsGeom &g,
+                      int64_t &n_blocks) {
+  ZX_REQUIRE(n_outer > 0 && n_batch > 0 && n_heads > 0 && run > 0,
+             "fp8 heads: all dimensions must be positive");
+  if (run % 16) return fail(ZX_ERR_UNSUPPORTED, "fp8 heads: run (%lld) must be a multiple of 16",
+                            (long long)run);
+  g.n_batch = n_batch;
+  g.n_heads = n_heads;
+  g.vec_per_run = run / 16;
+  g.chunks_per_run = ceil_div(g.vec_per_run, QH_CHUNK_VEC);
+  n_blocks = n_outer * n_batch * n_heads * g.chunks_per_run;
+  if (n_blocks >= (1LL << 31)) return fail(ZX_ERR_UNSUPPORTED, "fp8 heads: tensor too large");
+  return ZX_OK;
+}
+
+// ================================================================== paged KV
+
+// Token-major rows x[n_tok][2][H][D]: thread t of a block owns column (16-element
+// vector) c = t % vpr of rows t / vpr + RB * j; every column lies in one (kv, head) slab.
+struct RowGeom {
+  int32_t vpr;        // 16-element vectors per row = 2*H*D/16
+  int32_t rb;         // rows per block iteration
+  int32_t vec_per_d;  // D / 16 (lanes sharing a slab)
+  int32_t n_slabs;    // 2*H
+  int64_t n_tok;
+  int64_t x_layer_stride;  // elements
+};
+
+static int row_geom(int32_t n_heads, int32_t head_dim, int64_t n_tok, int64_t x_layer_stride,
+                    RowGeom &g) {
+  ZX_REQUIRE(n_heads > 0 && n_tok >= 0, "kv: n_heads must be positive and n_tok >= 0");
+  if (!(head_dim == 64 || head_dim == 128 || head_dim == 256))
+    return fail(ZX_ERR_UNSUPPORTED, "kv: head_dim %d not in {64, 128, 256}", head_dim);
+  int64_t row = 2LL * n_heads * head_dim;
+  if (row > 8192) return fail(ZX_ERR_UNSUPPORTED, "kv: 2*H*D = %lld exceeds 8192", (long long)row);
+  g.vpr = (int32_t)(row / 16);
+  g.rb = g.vpr >= 256 ? 1 : 256 / g.vpr;
+  g.vec_per_d = head_dim / 16;
+  g.n_slabs = 2 * n_heads;
+  g.n_tok = n_tok;
+  g.x_layer_stride = x_layer_stride;
+  return ZX_OK;
+}
+
+constexpr int KV_UNROLL = 4;
+
+__global__ void __launch_bounds__(1024)
+kv_amax_kernel(const uint16_t *x, RowGeom g, uint32_t *amax_bits /* [L][2H] */) {
+  __shared__ uint32_t smax[512];
+  const int t = threadIdx.x;
+  const int c = t % g.vpr, rg = t / g.vpr;
+  const int slab = c / g.vec_per_d;
+  const int layer = blockIdx.y;
+  for (int i = t; i < g.n_slabs; i += blockDim.x) smax[i] = 0;
+  __syncthreads();
+  const uint4 *xl = reinterpret_cast<const uint4 *>(x + (int64_t)layer * g.x_layer_stride);
+  const int64_t stride = (int64_t)gridDim.x * g.rb;
+  uint32_t m = 0;
+  for (int64_t r0 = (int64_t)blockIdx.x * g.rb + rg; r0 < g.n_tok; r0 += KV_UNROLL * stride) {
+    uint4 a[KV_UNROLL], b[KV_UNROLL];
+#pragma unroll
+    for (int k = 0; k < KV_UNROLL; ++k) {
+      int64_t r = r0 + k * stride;
+      if (r < g.n_tok) {
+        const uint4 *p = xl + (r * g.vpr + c) * 2;
+        a[k] = p[0];
+        b[k] = p[1];
+      } else {
+        a[k] = b[k] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KV_UNROLL; ++k) m = max(m, absmax16(a[k], b[k]));
+  }
+  m = group_max(m, g.vec_per_d);
+  if (c % g.vec_per_d == 0) atomicMax(&smax[slab], m);
+  __syncthreads();
+  for (int i = t; i < g.n_slabs; i += blockDim.x)
+    if (smax[i]) atomicMax(&amax_bits[(int64_t)layer * g.n_slabs + i], smax[i] << 16);
+}
+
+// Pool offset (bytes within one layer) of each token's (page, row) base, or -1.
+__global__ void kv_token_offsets_kernel(const int32_t *cu_seqlens, const int32_t *start_pos,
+                                        int32_t n_seqs, const int32_t *block_tables,
+                                        int32_t max_blocks, int32_t page_size, int64_t n_pages,
+                                        int64_t page_bytes, int32_t head_dim, int64_t n_tok,
+                                        int64_t *tok_off, int32_t *err) {
+  int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_tok) return;
+  int lo = 0, hi = n_seqs - 1;  // last b with cu_seqlens[b] <= t
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (cu_seqlens[mid] <= t) lo = mid;
+    else hi = mid - 1;
+  }
+  const int b = lo;
+  int64_t off = -1;
+  if (t >= cu_seqlens[b] && t < cu_seqlens[b + 1]) {
+    int64_t pos = (start_pos ? start_pos[b] : 0) + (t - cu_seqlens[b]);
+    if (pos < 0 || pos >= (int64_t)max_blocks * page_size) {
+      if (err) atomicOr(err, ZX_KERR_POS_RANGE);
+    } else {
+      int64_t page = block_tables[(int64_t)b * max_blocks + pos / page_size];
+      if (page < 0 || page >= n_pages) {
+        if (err) atomicOr(err, ZX_KERR_PAGE_RANGE);
+      } else {
+        off = page * page_bytes + (pos % page_size) * head_dim;
+      }
+    }
+  }
+  tok_off[t] = off;
+}
+
+__global__ void __launch_bounds__(1024)
+kv_quant_append_kernel(const uint16_t *x, RowGeom g, const int64_t *tok_off, const float *scales,
+                       uint8_t *pool, int64_t pool_layer_stride, int32_t page_size,
+                       int32_t head_dim) {
+  const int t = threadIdx.x;
+  const int c = t % g.vpr, rg = t / g.vpr;
+  const int slab = c / g.vec_per_d;
+  const int layer = blockIdx.y;
+  const float s = scales[(int64_t)layer * g.n_slabs + slab];
+  const int mode = scale_mode(s);
+  const float rcp = 1.0f / s;
+  const uint4 *xl = reinterpret_cast<const uint4 *>(x + (int64_t)layer * g.x_layer_stride);
+  uint8_t *pl = pool + (int64_t)layer * pool_layer_stride +
+                (int64_t)slab * page_size * head_dim + (c % g.vec_per_d) * 16;
+  const int64_t stride = (int64_t)gridDim.x * g.rb;
+  for (int64_t r0 = (int64_t)blockIdx.x * g.rb + rg; r0 < g.n_tok; r0 += KV_UNROLL * stride) {
+    uint4 a[KV_UNROLL], b[KV_UNROLL];
+    int64_t off[KV_UNROLL];
+#pragma unroll
+    for (int k = 0; k < KV_UNROLL; ++k) {
+      int64_t r = r0 + k * stride;
+      off[k] = -1;
+      if (r < g.n_tok) {
+        off[k] = tok_off[r];
+        const uint4 *p = xl + (r * g.vpr + c) * 2;
+        a[k] = p[0];
+        b[k] = p[1];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KV_UNROLL; ++k)
+      if (off[k] >= 0) *reinterpret_cast<uint4 *>(pl + off[k]) = quant16(a[k], b[k], s, rcp, mode);
+  }
+}
+
+static dim3 kv_grid(const RowGeom &g, int32_t n_layers) {
+  int64_t rows_blocks = ceil_div(g.n_tok, g.rb);
+  int64_t want = ceil_div((int64_t)num_cus() * 8, n_layers);
+  int64_t gx = rows_blocks < want ? rows_blocks : want;
+  if (gx < 1) gx = 1;
+  return dim3((unsigned)gx, (unsigned)n_layers, 1);
+}
+
+static int kv_scales_impl(const uint16_t *x, const RowGeom &g, int32_t n_layers, float *scales,
+                          hipStream_t st) {
+  int rc = fill_u32(reinterpret_cast<uint32_t *>(scales), (int64_t)n_layers * g.n_slabs, 0, st);
+  if (rc) return rc;
+  if (g.n_tok > 0) {
+    kv_amax_kernel<<<kv_grid(g, n_layers), g.vpr * g.rb, 0, st>>>(x, g,
+                                                                 reinterpret_cast<uint32_t *>(scales));
+    if ((rc = check_launch("kv_amax"))) return rc;
+  }
+  int64_t n = (int64_t)n_layers * g.n_slabs;
+  finalize_scales_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(scales, n);
+  return check_launch("finalize_scales");
+}
+
+}  // namespace zx
+
+using namespace zx;
+
+// ================================================================== C ABI
+
+extern "C" int zx_int8_legacy_quant(const void *x, int dtype, int64_t n, int8_t *q, void *scale,
+                                    void *workspace, size_t workspace_bytes, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(x && q && scale, "int8_legacy_quant: null pointer");
+  ZX_REQUIRE(n > 0, "int8_legacy_quant: empty tensor (the reference raises on amax of an empty tensor)");
+  if (!workspace || workspace_bytes < 256) return fail(ZX_ERR_WORKSPACE, "int8_legacy_quant: workspace < 256 bytes");
+  hipStream_t st = as_stream(stream);
+  uint32_t *amax = reinterpret_cast<uint32_t *>(workspace);
+  int rc = fill_u32(amax, 1, 0, st);
+  if (rc) return rc;
+  unsigned grid = grid_for(n, 8);
+  switch (dtype) {
+    case ZX_BF16:
+      legacy_amax_kernel<ZX_BF16><<<grid, 256, 0, st>>>(x, n, amax);
+      if ((rc = check_launch("legacy_amax"))) return rc;
+      legacy_quant_kernel<ZX_BF16><<<grid, 256, 0, st>>>(x, n, amax, q, scale);
+      break;
+    case ZX_F16:
+      legacy_amax_kernel<ZX_F16><<<grid, 256, 0, st>>>(x, n, amax);
+      if ((rc = check_launch("legacy_amax"))) return rc;
+      legacy_quant_kernel<ZX_F16><<<grid, 256, 0, st>>>(x, n, amax, q, scale);
+      break;
+    case ZX_F32:
+      legacy_amax_kernel<ZX_F32><<<grid, 256, 0, st>>>(x, n, amax);
+      if ((rc = check_launch("legacy_amax"))) return rc;
+      legacy_quant_kernel<ZX_F32><<<grid, 256, 0, st>>>(x, n, amax, q, scale);
+      break;
+    default:
+      return fail(ZX_ERR_INVALID, "int8_legacy_quant: unknown dtype %d", dtype);
+  }
+  return check_launch("legacy_quant");
+}
+
+extern "C" int zx_int8_legacy_dequant(const int8_t *q, const void *scale, int scale_dtype, int64_t n,
+                                      uint16_t *y, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(q && scale && y, "int8_legacy_dequant: null pointer");
+  ZX_REQUIRE(n >= 0, "int8_legacy_dequant: negative size");
+  if (n == 0) return ZX_OK;
+  hipStream_t st = as_stream(stream);
+  unsigned grid = grid_for(n, 8);
+  switch (scale_dtype) {
+    case ZX_BF16: legacy_dequant_kernel<ZX_BF16><<<grid, 256, 0, st>>>(q, scale, n, y); break;
+    case ZX_F16: legacy_dequant_kernel<ZX_F16><<<grid, 256, 0, st>>>(q, scale, n, y); break;
+    case ZX_F32: legacy_dequant_kernel<ZX_F32><<<grid, 256, 0, st>>>(q, scale, n, y); break;
+    default: return fail(ZX_ERR_INVALID, "int8_legacy_dequant: unknown dtype %d", scale_dtype);
+  }
+  return check_launch("legacy_dequant");
+}
+
+extern "C" int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_heads,
+                                  int64_t run, uint8_t *codes, float *scales, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(x && codes && scales, "fp8_quant_heads: null pointer");
+  HeadsGeom g;
+  int64_t nb;
+  int rc = heads_geom(n_outer, n_batch, n_heads, run, g, nb);
+  if (rc) return rc;
+  hipStream_t st = as_stream(stream);
+  int64_t ns = n_outer * n_heads;
+  if ((rc = fill_u32(reinterpret_cast<uint32_t *>(scales), ns, 0, st))) return rc;
+  heads_amax_kernel<<<(unsigned)nb, QH_THREADS, 0, st>>>(reinterpret_cast<const uint4 *>(x), g,
+                                                        reinterpret_cast<uint32_t *>(scales));
+  if ((rc = check_launch("heads_amax"))) return rc;
+  finalize_scales_kernel<<<(unsigned)ceil_div(ns, 256), 256, 0, st>>>(scales, ns);
+  if ((rc = check_launch("finalize_scales"))) return rc;
+  heads_quant_kernel<<<(unsigned)nb, QH_THREADS, 0, st>>>(reinterpret_cast<const uint4 *>(x), g, scales,
+                                                         reinterpret_cast<uint4 *>(codes));
+  return check_launch("heads_quant");
+}
+
+extern "C" int zx_fp8_dequant_heads(const uint8_t *codes, const float *scales, int64_t n_outer,
+                                    int64_t n_batch, int64_t n_heads, int64_t run, uint16_t *y,
+                                    zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(codes && scales && y, "fp8_dequant_heads: null pointer");
+  HeadsGeom g;
+  int64_t nb;
+  int rc = heads_geom(n_outer, n_batch, n_heads, run, g, nb);
+  if (rc) return rc;
+  heads_dequant_kernel<<<(unsigned)nb, QH_THREADS, 0, as_stream(stream)>>>(
+      reinterpret_cast<const uint4 *>(codes), g, scales, reinterpret_cast<uint4 *>(y));
+  return check_launch("heads_dequant");
+}
+
+extern "C" int zx_kv_scales(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, int64_t n_tok,
+                            int32_t n_heads, int32_t head_dim, float *scales, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(scales && (x || n_tok == 0), "kv_scales: null pointer");
+  ZX_REQUIRE(n_layers > 0 && n_layers <= 65535, "kv_scales: n_layers out of range");
+  RowGeom g;
+  int rc = row_geom(n_heads, head_dim, n_tok, x_layer_stride, g);
+  if (rc) return rc;
+  ZX_REQUIRE(n_layers == 1 || x_layer_stride >= n_tok * 2LL * n_heads * head_dim,
+             "kv_scales: layer stride smaller than a layer");
+  return kv_scales_impl(x, g, n_layers, scales, as_stream(stream));
+}
+
+extern "C" size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32_t n_heads,
+                                                     int32_t head_dim) {
+  (void)n_layers;
+  (void)n_heads;
+  (void)head_dim;
+  return (size_t)(n_tok > 0 ? n_tok : 0) * sizeof(int64_t) + 256;
+}
+
+extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
+                                  int64_t n_tok, int32_t n_heads, int32_t head_dim,
+                                  const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
+                                  const int32_t *block_tables, int32_t max_blocks, int32_t page_size,
+                                  uint8_t *pool, int64_t pool_layer_stride, int64_t n_pages,
+                                  float *scales, int32_t flags, int32_t *err, void *workspace,
+                                  size_t workspace_bytes, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(scales && cu_seqlens && block_tables && pool, "kv_quant_append: null pointer");
+  ZX_REQUIRE(x || n_tok == 0, "kv_quant_append: null x");
+  ZX_REQUIRE(n_layers > 0 && n_layers <= 65535, "kv_quant_append: n_layers out of range");
+  ZX_REQUIRE(n_seqs > 0 && max_blocks > 0 && page_size > 0 && n_pages > 0,
+             "kv_quant_append: n_seqs, max_blocks, page_size and n_pages must be positive");
+  RowGeom g;
+  int rc = row_geom(n_heads, head_dim, n_tok, x_layer_stride, g);
+  if (rc) return rc;
+  const int64_t page_bytes = 2LL * n_heads * page_size * head_dim;
+  ZX_REQUIRE(n_layers == 1 || x_layer_stride >= n_tok * 2LL * n_heads * head_dim,
+             "kv_quant_append: x layer stride smaller than a layer");
+  ZX_REQUIRE(n_layers == 1 || pool_layer_stride >= n_pages * page_bytes,
+             "kv_quant_append: pool layer stride smaller than a layer's pages");
+  size_t need = zx_kv_quant_append_workspace_bytes(n_layers, n_tok, n_heads, head_dim);
+  if (!workspace || workspace_bytes < need)
+    return fail(ZX_ERR_WORKSPACE, "kv_quant_append: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = as_stream(stream);
+  if (!(flags & ZX_APPEND_STATIC_SCALES) && (rc = kv_scales_impl(x, g, n_layers, scales, st))) return rc;
+  if (n_tok == 0) return ZX_OK;
+  int64_t *tok_off = reinterpret_cast<int64_t *>(workspace);
+  kv_token_offsets_kernel<<<(unsigned)ceil_div(n_tok, 256), 256, 0, st>>>(
+      cu_seqlens, start_pos, n_seqs, block_tables, max_blocks, page_size, n_pages, page_bytes, head_dim,
+      n_tok, tok_off, err);
+  if ((rc = check_launch("kv_token_offsets"))) return rc;
+  kv_quant_append_kernel<<<kv_grid(g, n_layers), g.vpr * g.rb, 0, st>>>(
+      x, g, tok_off, scales, pool, pool_layer_stride, page_size, head_dim);
+  return check_launch("kv_quant_append");
+}
+
+namespace zx {
+__global__ void encode_f32_kernel(const float *v, int64_t n, uint8_t *codes) {
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= n) return;
+  float a[4];
+  uint32_t fix = 0, fixmask = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    a[k] = i + k < n ? v[i + k] : 0.0f;
+    uint32_t b = __float_as_uint(a[k]);
+    if ((b & 0x7FFFFFFFu) > 0x43E80000u) {  // beyond 464 (or Inf/NaN): e4m3fn NaN
+      fix |= (((b >> 24) & 0x80u) | 0x7Fu) << (8 * k);
+      fixmask |= 0xFFu << (8 * k);
+      a[k] = 0.0f;
+    }
+  }
+  uint32_t w = (e4m3x4(a[0], a[1], a[2], a[3]) & ~fixmask) | fix;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (i + k < n) codes[i + k] = (uint8_t)(w >> (8 * k));
+}
+}  // namespace zx
+
+extern "C" int zx_fp8_encode_f32(const float *v, int64_t n, uint8_t *codes, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(n >= 0, "fp8_encode_f32: negative size");
+  if (n == 0) return ZX_OK;
+  ZX_REQUIRE(v && codes, "fp8_encode_f32: null pointer");
+  encode_f32_kernel<<<(unsigned)ceil_div(ceil_div(n, 4), 256), 256, 0, as_stream(stream)>>>(v, n, codes);
+  return check_launch("fp8_encode_f32");
+}

@@ -1,0 +1,278 @@
+"""Torch-facing operations of the KV-cache hot path, each a thin wrapper over one entry
+point of libzenyx_kv.so (include/zenyx_kv.h).
+
+Tensors must live on the HIP device; the wrappers validate dtype/shape/contiguity on the
+host, pass raw pointers and the current torch stream, and never synchronise unless asked
+(``check=True`` reads back the kernels' error word and raises ``ValueError``).
+
+Layouts:
+  * KV cache tensor (FP8KVQuantizer): ``[L, 2, B, H, T, D]`` bf16, scales ``[L, 2, H]``.
+  * token-major append input: ``[L, n_tok, 2, H, D]`` (or one layer ``[n_tok, 2, H, D]``).
+  * page pool: ``[L, n_pages, 2, H, P, D]`` uint8 e4m3fn codes (or one layer without L).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+_DT = {torch.bfloat16: N.ZX_BF16, torch.float16: N.ZX_F16, torch.float32: N.ZX_F32}
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.int16) if t.dtype in (torch.bfloat16, torch.float16) else t
+
+
+def _err_word(device) -> torch.Tensor:
+    return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+def _raise_kernel_error(err: torch.Tensor, what: str) -> None:
+    e = int(err.item())
+    if e:
+        parts = []
+        if e & N.ZX_KERR_PAGE_RANGE:
+            parts.append("block table entry outside [0, n_pages)")
+        if e & N.ZX_KERR_POS_RANGE:
+            parts.append("token position beyond max_blocks * page_size")
+        if e & N.ZX_KERR_SPIN:
+            parts.append("bounded wait ran out")
+        raise ValueError(f"{what}: " + "; ".join(parts))
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# ------------------------------------------------------------------ legacy int8
+
+def int8_legacy_quant(x: torch.Tensor):
+    """zenyx/streaming/precision.py:8-12 on the GPU: (q int8, 0-dim scale in x.dtype)."""
+    N.ensure_gpu()
+    if x.dtype not in _DT:
+        raise TypeError(f"quantize_to_fp8_storage: unsupported dtype {x.dtype}")
+    if x.numel() == 0:
+        # precision.py:10 -- amax of an empty tensor raises in torch
+        raise RuntimeError("quantize_to_fp8_storage: cannot quantize an empty tensor (amax over zero elements)")
+    x = x.contiguous()
+    N.require_device(x, "x")
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scale = torch.empty((), dtype=x.dtype, device=x.device)
+    ws = _workspace(256, x.device)
+    N.check(N.load().zx_int8_legacy_quant(N.ptr(x), _DT[x.dtype], x.numel(), N.ptr(q), N.ptr(scale),
+                                          N.ptr(ws), ws.numel(), N.stream_ptr(x.device)),
+            "quantize_to_fp8_storage")
+    return q, scale
+
+
+def int8_legacy_dequant(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """zenyx/streaming/precision.py:15-16 on the GPU."""
+    N.ensure_gpu()
+    if q.dtype != torch.int8:
+        q = q.to(torch.int8)
+    q = q.contiguous()
+    scale = scale.reshape(()).to(q.device)
+    if scale.dtype not in _DT:
+        scale = scale.float()
+    scale = scale.contiguous()
+    N.require_device(q, "q")
+    y = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    N.check(N.load().zx_int8_legacy_dequant(N.ptr(q), N.ptr(scale), _DT[scale.dtype], q.numel(), N.ptr(y),
+                                            N.stream_ptr(q.device)), "dequantize_for_bf16_compute")
+    return y
+
+
+# ------------------------------------------------------------------ FP8 per head
+
+def fp8_quant_heads(x: torch.Tensor):
+    """x: bf16 ``[n_outer, n_batch, n_heads, run]`` -> (codes uint8 same shape, scales
+    fp32 ``[n_outer, n_heads]``), one scale per (outer, head)."""
+    N.ensure_gpu()
+    if x.dtype != torch.bfloat16 or x.dim() != 4:
+        raise ValueError("fp8_quant_heads: x must be bf16 [n_outer, n_batch, n_heads, run]")
+    N.require_device(x, "x")
+    O, B, H, R = x.shape
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scales = torch.empty((O, H), dtype=torch.float32, device=x.device)
+    N.check(N.load().zx_fp8_quant_heads(N.ptr(x), O, B, H, R, N.ptr(codes), N.ptr(scales),
+                                        N.stream_ptr(x.device)), "fp8_quant_heads")
+    return codes, scales
+
+
+def fp8_dequant_heads(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    N.ensure_gpu()
+    if codes.dtype != torch.uint8 or codes.dim() != 4:
+        raise ValueError("fp8_dequant_heads: codes must be uint8 [n_outer, n_batch, n_heads, run]")
+    O, B, H, R = codes.shape
+    if scales.shape != (O, H) or scales.dtype != torch.float32:
+        raise ValueError(f"fp8_dequant_heads: scales must be float32 {(O, H)}")
+    N.require_device(codes, "codes")
+    N.require_device(scales, "scales")
+    y = torch.empty(codes.shape, dtype=torch.bfloat16, device=codes.device)
+    N.check(N.load().zx_fp8_dequant_heads(N.ptr(codes), N.ptr(scales), O, B, H, R, N.ptr(y),
+                                          N.stream_ptr(codes.device)), "fp8_dequant_heads")
+    return y
+
+
+def fp8_encode_f32(v: torch.Tensor) -> torch.Tensor:
+    """Already-scaled fp32 values -> e4m3fn codes (uint8), nearest-even, overflow -> NaN."""
+    N.ensure_gpu()
+    if v.dtype != torch.float32:
+        raise ValueError("fp8_encode_f32: v must be float32")
+    v = v.contiguous()
+    N.require_device(v, "v")
+    codes = torch.empty(v.shape, dtype=torch.uint8, device=v.device)
+    N.check(N.load().zx_fp8_encode_f32(N.ptr(v), v.numel(), N.ptr(codes), N.stream_ptr(v.device)),
+            "fp8_encode_f32")
+    return codes
+
+
+# ------------------------------------------------------------------ paged KV
+
+def _layers(x: torch.Tensor):
+    if x.dim() == 4:
+        x = x.unsqueeze(0)
+    if x.dim() != 5 or x.shape[2] != 2:
+        raise ValueError("x must be [L, n_tok, 2, H, D] (or [n_tok, 2, H, D])")
+    if x.dtype != torch.bfloat16:
+        raise ValueError("x must be bfloat16")
+    return x
+
+
+def kv_scales(x: torch.Tensor) -> torch.Tensor:
+    """Per-(layer, kv, head) FP8 scales of a token-major batch -> ``[L, 2, H]`` fp32."""
+    N.ensure_gpu()
+    x = _layers(x)
+    N.require_device(x, "x")
+    L, T, _, H, D = x.shape
+    scales = torch.empty((L, 2, H), dtype=torch.float32, device=x.device)
+    N.check(N.load().zx_kv_scales(N.ptr(x), T * 2 * H * D, L, T, H, D, N.ptr(scales),
+                                  N.stream_ptr(x.device)), "kv_scales")
+    return scales
+
+
+def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: torch.Tensor,
+                    pool: torch.Tensor, scales: torch.Tensor | None = None,
+                    start_pos: torch.Tensor | None = None, static_scales: bool = False,
+                    check: bool = False) -> torch.Tensor:
+    """Paged append with fused FP8 quantisation.
+
+    x ``[L, n_tok, 2, H, D]`` bf16; cu_seqlens int32 ``[B+1]``; block_tables int32
+    ``[B, max_blocks]``; pool uint8 ``[L, n_pages, 2, H, P, D]`` (written in place).
+    Without ``static_scales`` the scales are computed from this batch and written into
+    ``scales`` (allocated if None); returns the scales ``[L, 2, H]``.
+    """
+    N.ensure_gpu()
+    x = _layers(x)
+    if pool.dim() == 5:
+        pool = pool.unsqueeze(0)
+    L, T, _, H, D = x.shape
+    if pool.dim() != 6 or pool.shape[0] != L or pool.shape[2:4] != (2, H) or pool.shape[5] != D:
+        raise ValueError(f"pool must be uint8 [L={L}, n_pages, 2, H={H}, P, D={D}]")
+    if pool.dtype != torch.uint8:
+        raise ValueError("pool must be uint8")
+    n_pages, P = pool.shape[1], pool.shape[4]
+    for name, t in (("cu_seqlens", cu_seqlens), ("block_tables", block_tables)):
+        if t.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32")
+    if block_tables.dim() != 2 or cu_seqlens.dim() != 1 or cu_seqlens.numel() != block_tables.shape[0] + 1:
+        raise ValueError("block_tables must be [B, max_blocks] and cu_seqlens [B+1]")
+    if start_pos is not None and (start_pos.dtype != torch.int32 or start_pos.numel() != block_tables.shape[0]):
+        raise ValueError("start_pos must be int32 [B]")
+    if scales is None:
+        if static_scales:
+            raise ValueError("static_scales needs scales")
+        scales = torch.empty((L, 2, H), dtype=torch.float32, device=x.device)
+    if scales.shape != (L, 2, H) or scales.dtype != torch.float32:
+        raise ValueError(f"scales must be float32 [{L}, 2, {H}]")
+    for name, t in (("x", x), ("cu_seqlens", cu_seqlens), ("block_tables", block_tables), ("pool", pool),
+                    ("scales", scales)) + ((("start_pos", start_pos),) if start_pos is not None else ()):
+        N.require_device(t, name)
+    lib = N.load()
+    ws = _workspace(lib.zx_kv_quant_append_workspace_bytes(L, T, H, D), x.device)
+    err = _err_word(x.device)
+    flags = N.ZX_APPEND_STATIC_SCALES if static_scales else 0
+    N.check(lib.zx_kv_quant_append(N.ptr(x), T * 2 * H * D, L, T, H, D, N.ptr(cu_seqlens), N.ptr(start_pos),
+                                   block_tables.shape[0], N.ptr(block_tables), block_tables.shape[1], P,
+                                   N.ptr(pool), pool[0].numel(), n_pages, N.ptr(scales), flags, N.ptr(err),
+                                   N.ptr(ws), ws.numel(), N.stream_ptr(x.device)), "kv_quant_append")
+    if check:
+        _raise_kernel_error(err, "kv_quant_append")
+    return scales
+
+
+def kv_gather_dequant(pool_layer: torch.Tensor, scales_layer: torch.Tensor, block_tables: torch.Tensor,
+                      seq_lens: torch.Tensor, out_len: int | None = None, check: bool = False,
+                      out: tuple[torch.Tensor, torch.Tensor] | None = None):
+    """Paged gather + dequant of one layer: pool ``[n_pages, 2, H, P, D]`` uint8, scales
+    ``[2, H]`` fp32 -> (k, v), each bf16 ``[B, H, out_len, D]``; positions at or beyond
+    ``seq_lens[b]`` are zeros."""
+    N.ensure_gpu()
+    if pool_layer.dim() != 5 or pool_layer.dtype != torch.uint8 or pool_layer.shape[1] != 2:
+        raise ValueError("pool_layer must be uint8 [n_pages, 2, H, P, D]")
+    n_pages, _, H, P, D = pool_layer.shape
+    if scales_layer.shape != (2, H) or scales_layer.dtype != torch.float32:
+        raise ValueError(f"scales_layer must be float32 [2, {H}]")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise ValueError("block_tables and seq_lens must be int32")
+    B = block_tables.shape[0]
+    if seq_lens.numel() != B:
+        raise ValueError("seq_lens must have one entry per block-table row")
+    if out_len is None:
+        out_len = block_tables.shape[1] * P
+    for name, t in (("pool_layer", pool_layer), ("scales_layer", scales_layer), ("block_tables", block_tables),
+                    ("seq_lens", seq_lens)):
+        N.require_device(t, name)
+    if out is None:
+        k = torch.empty((B, H, out_len, D), dtype=torch.bfloat16, device=pool_layer.device)
+        v = torch.empty_like(k)
+    else:
+        k, v = out
+        for t in (k, v):
+            if t.shape != (B, H, out_len, D) or t.dtype != torch.bfloat16:
+                raise ValueError(f"out tensors must be bf16 {(B, H, out_len, D)}")
+            N.require_device(t, "out")
+    err = _err_word(pool_layer.device)
+    N.check(N.load().zx_kv_gather_dequant(N.ptr(pool_layer), n_pages, H, D, P, N.ptr(scales_layer),
+                                          N.ptr(block_tables), block_tables.shape[1], N.ptr(seq_lens), B,
+                                          out_len, N.ptr(k), N.ptr(v), N.ptr(err),
+                                          N.stream_ptr(pool_layer.device)), "kv_gather_dequant")
+    if check:
+        _raise_kernel_error(err, "kv_gather_dequant")
+    return k, v
+
+
+# ------------------------------------------------------------------ Belady
+
+def belady_argmax(keys: torch.Tensor, resident: torch.Tensor) -> torch.Tensor:
+    """belady.py:39-51 over slots: device int64 ``[slot, key]`` ({-1, -1} if none)."""
+    N.ensure_gpu()
+    if keys.dtype != torch.int64 or resident.dtype != torch.uint8 or keys.shape != resident.shape:
+        raise ValueError("keys must be int64 and resident uint8 of the same shape")
+    N.require_device(keys, "keys")
+    N.require_device(resident, "resident")
+    lib = N.load()
+    out = torch.empty(2, dtype=torch.int64, device=keys.device)
+    ws = _workspace(lib.zx_belady_argmax_workspace_bytes(keys.numel()), keys.device)
+    N.check(lib.zx_belady_argmax(N.ptr(keys), N.ptr(resident), keys.numel(), N.ptr(out), N.ptr(ws), ws.numel(),
+                                 N.stream_ptr(keys.device)), "belady_argmax")
+    return out
+
+
+def next_use(trace: torch.Tensor, n_pages: int, check: bool = False):
+    """Next/previous use of every position of an int32 page trace (ZX_NEVER / -1)."""
+    N.ensure_gpu()
+    if trace.dtype != torch.int32 or trace.dim() != 1:
+        raise ValueError("trace must be a 1-D int32 tensor")
+    N.require_device(trace, "trace")
+    n = trace.numel()
+    nu = torch.empty(n, dtype=torch.int32, device=trace.device)
+    pu = torch.empty(n, dtype=torch.int32, device=trace.device)
+    lib = N.load()
+    ws = _workspace(lib.zx_belady_next_use_workspace_bytes(n, n_pages), trace.device)
+    err = _err_word(trace.device)
+    N.check(lib.zx_belady_next_use(N.ptr(trace), n, n_pages, N.ptr(nu), N.ptr(pu), N.ptr(err), N.ptr(ws),
+                                   ws.numel(), N.stream_ptr(trace.device)), "belady_next_use")
+    if check:
+        _raise_kernel_error(err, "belady_next_use")
+    return nu, pu
