@@ -202,3 +202,35 @@ def test_kv_gather_dequant_nan_codes_and_bad_pages(dev):
     k, v = kv.kv_gather_dequant(pool.to(dev), scales.to(dev), bt.to(dev), seq_lens.to(dev), out_len)
     assert_bf16_equal(bits16(k), wk)
     assert_bf16_equal(bits16(v), wv)
+
+
+@pytest.mark.parametrize("two_pass", [False, True])
+@pytest.mark.parametrize("L,H,D,P,lens", [
+    (2, 8, 128, 16, [1000, 17, 2048, 511]),   # single-pass kernel: every share fits in LDS
+    (1, 1, 256, 16, [30000, 20001]),          # share larger than an LDS buffer: spill path
+    (3, 4, 64, 32, [3, 1, 2]),                # fewer tokens than workgroups
+])
+def test_kv_quant_append_fused_and_two_pass_bit_exact(dev, two_pass, L, H, D, P, lens):
+    x, cu, bt, n_pages, _ = make_append_case(L, H, D, P, lens, seed=L * 1000 + H + D)
+    pool = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8)
+    wpool = pool.numpy().copy()
+    wsc, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, P)
+    assert werr == 0
+    pool_d = pool.to(dev)
+    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+    np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
+
+
+def test_kv_quant_append_repeated_calls_reset_state(dev):
+    """The single-pass kernel's counters live in the per-call workspace and start at zero:
+    two appends in a row (second one smaller) both match the oracle."""
+    for lens, seed in (([700, 300], 5), ([40], 6)):
+        x, cu, bt, n_pages, _ = make_append_case(2, 8, 128, 16, lens, seed=seed)
+        pool = torch.zeros((2, n_pages, 2, 8, 16, 128), dtype=torch.uint8)
+        wpool = pool.numpy().copy()
+        wsc, _ = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, 16)
+        pool_d = pool.to(dev)
+        sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True)
+        np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+        np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)

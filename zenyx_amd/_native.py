@@ -23,6 +23,7 @@ ZX_ERR_WORKSPACE = -4
 ZX_BF16, ZX_F16, ZX_F32 = 0, 1, 2
 ZX_KERR_PAGE_RANGE, ZX_KERR_POS_RANGE, ZX_KERR_SPIN = 1, 2, 4
 ZX_APPEND_STATIC_SCALES = 1
+ZX_APPEND_TWO_PASS = 2
 ZX_NEVER = 0x7FFFFFFF
 ABI_VERSION = 1
 

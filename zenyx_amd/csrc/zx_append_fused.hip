@@ -1,0 +1,387 @@
+// zx_append_fused.hip -- single-pass paged append with dynamic per-(layer, kv, head) FP8
+// scales.
+//
+// A (layer, kv, head) slab's scale needs the amax over all of its tokens before any of
+// them can be encoded.  Instead of reading the input twice (amax pass + quant pass), one
+// cooperative persistent launch keeps each workgroup's share of a slab on chip:
+//   * workgroup w (one per CU) owns tokens [w*T/G, (w+1)*T/G) of every slab;
+//   * 15 data waves stream the share of slab s+3 from HBM into registers (three register
+//     buffers per lane) while encoding slab s and reducing the max of slab s+2, so loads
+//     stay in flight continuously and no block-wide barrier is ever taken;
+//   * a wave's max goes to an LDS slot (ds_max + arrival count); the control wave (the
+//     16th) stores the workgroup's max into its own device-coherent slot of slab s
+//     (slots start as a sentinel), reads all G slots of a slab with one wave-wide load
+//     until none is the sentinel, and broadcasts the finished scale through LDS.  It
+//     publishes slab s+1 while still polling slab s, so two slabs' round trips overlap,
+//     and the data waves keep streaming throughout.
+// HBM traffic is 2 B read + 1 B written per element.  Tokens of a share beyond what the
+// registers hold are re-read from memory (both for the max and for the encode).
+// Every wait is bounded in wall time; a timeout raises a global abort flag that
+// releases every other waiter, so all waves always exit.
+#include "zx_internal.h"
+
+namespace zx {
+
+constexpr int FA_THREADS = 1024;
+constexpr int FA_DATA_WAVES = 15;
+constexpr int FA_DATA_THREADS = FA_DATA_WAVES * 64;
+constexpr int FA_SLOTS = 8;                 // LDS ring of per-slab reduction slots (>= NB + 1)
+constexpr uint32_t FA_EMPTY = 0xFFFFFFFFu;  // slot sentinel (a share max is at most 0x7FFF)
+
+struct FusedArgs {
+  const uint16_t *x;
+  int64_t x_layer_stride;  // elements
+  int64_t n_tok;
+  int32_t n_layers, n_heads, head_dim, page_size;
+  int32_t vpt_log2;  // log2(16-byte vectors per token row of one head) = log2(D / 8)
+  const int64_t *tok_off;
+  uint8_t *pool;
+  int64_t pool_layer_stride;
+  float *scales;
+  uint32_t *slots;  // [S][G] each workgroup's share max (bf16 magnitude), or FA_EMPTY
+  uint32_t *abort_flag;
+  int32_t *err;
+  uint64_t spin_ticks;  // bound of one wait in s_memrealtime ticks (100 MHz)
+};
+
+struct FusedShared {
+  uint32_t max[FA_SLOTS];    // running max of the data waves' contributions
+  uint32_t cnt[FA_SLOTS];    // data waves that contributed
+  uint32_t ready[FA_SLOTS];  // s + 1 once slab s's scale is final
+  float scale[FA_SLOTS];
+  uint32_t abort;
+};
+
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// LDS flags between the waves of one workgroup.  DS instructions of a wave execute in
+// program order, so relaxed LDS atomics plus compiler-only fences order them; acquire /
+// release orderings would also drain every outstanding global load (s_waitcnt vmcnt(0))
+// and stall the streaming data waves.
+#define ZX_COMPILER_FENCE() asm volatile("" ::: "memory")
+__device__ __forceinline__ uint32_t ld_lds(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void nt_store8(uint8_t *p, uint2 v) {
+  typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+  v2u w = {v.x, v.y};
+  __builtin_nontemporal_store(w, reinterpret_cast<v2u *>(p));
+}
+
+// Per-thread constants of the register part.  Vector k of a data thread is index
+// v = k * FA_DATA_THREADS + tid of the share (token v >> vpt_log2, 16-byte chunk
+// v & mask).  dst[k] is the offset of its 8 codes inside a layer's pool minus the slab
+// term, or -1 (the store then goes to a dummy workspace slot).  Lanes past the share
+// read the share's first vector (always valid) and leave it out of the max.  Keeping
+// the data path free of per-lane branches lets the compiler count outstanding loads
+// exactly (s_waitcnt vmcnt(N) instead of vmcnt(0)), so later slabs' loads stay in flight.
+template <int K> struct ThreadMap {
+  int64_t dst[K];
+  uint32_t live;  // bit k: vector k is part of the share
+  int nreg;       // vectors of the share held in registers (whole workgroup)
+};
+
+__device__ __forceinline__ int64_t vec_src(const FusedArgs &a, int v) {
+  const int64_t row_bytes = 4LL * a.n_heads * a.head_dim;
+  return (int64_t)(v >> a.vpt_log2) * row_bytes + (v & ((1 << a.vpt_log2) - 1)) * 16;
+}
+
+__device__ __forceinline__ const char *slab_src(const FusedArgs &a, int s, int64_t t_lo) {
+  const int two_h = 2 * a.n_heads;
+  const int l = s / two_h, j = s - l * two_h;
+  return reinterpret_cast<const char *>(a.x + (int64_t)l * a.x_layer_stride + t_lo * two_h * a.head_dim +
+                                        (int64_t)j * a.head_dim);
+}
+__device__ __forceinline__ uint8_t *slab_dst(const FusedArgs &a, int s) {
+  const int two_h = 2 * a.n_heads;
+  const int l = s / two_h, j = s - l * two_h;
+  return a.pool + (int64_t)l * a.pool_layer_stride + (int64_t)j * a.page_size * a.head_dim;
+}
+
+template <int K>
+__device__ __forceinline__ void load_share(const FusedArgs &a, const ThreadMap<K> &m, int s, int64_t t_base,
+                                           uint4 (&r)[K]) {
+  const char *base = slab_src(a, s, t_base);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int v = k * FA_DATA_THREADS + (int)threadIdx.x;
+    r[k] = *reinterpret_cast<const uint4 *>(base + ((m.live >> k) & 1 ? vec_src(a, v) : 0));
+  }
+}
+
+template <int K, bool SPILL>
+__device__ __forceinline__ uint32_t share_max(const FusedArgs &a, const ThreadMap<K> &m, int s, int64_t t_lo,
+                                              int nv, const uint4 (&r)[K]) {
+  uint32_t mx = 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) mx = max(mx, (m.live >> k) & 1 ? absmax8(r[k]) : 0u);
+  if (SPILL && nv > m.nreg) {
+    const char *base = slab_src(a, s, t_lo);
+    for (int v = m.nreg + threadIdx.x; v < nv; v += FA_DATA_THREADS)
+      mx = max(mx, absmax8(*reinterpret_cast<const uint4 *>(base + vec_src(a, v))));
+  }
+  return mx;
+}
+
+// dst: the slab's base in the pool, or nullptr for a padding step (every store then
+// goes to the dummy slot).
+template <int K, bool SPILL>
+__device__ __forceinline__ void encode_share(const FusedArgs &a, const ThreadMap<K> &m, int s, int64_t t_lo,
+                                             int nv, const uint4 (&r)[K], float sc, uint8_t *dst,
+                                             uint8_t *dummy) {
+  const int mode = scale_mode(sc);
+  const float rcp = 1.0f / sc;
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    nt_store8(dst && m.dst[k] >= 0 ? dst + m.dst[k] : dummy, quant8(r[k], sc, rcp, mode));
+  if (SPILL && dst && nv > m.nreg) {
+    const char *base = slab_src(a, s, t_lo);
+    for (int v = m.nreg + threadIdx.x; v < nv; v += FA_DATA_THREADS) {
+      const int64_t off = a.tok_off[t_lo + (v >> a.vpt_log2)];
+      const uint4 q = *reinterpret_cast<const uint4 *>(base + vec_src(a, v));
+      if (off >= 0) nt_store8(dst + off + (v & ((1 << a.vpt_log2) - 1)) * 8, quant8(q, sc, rcp, mode));
+    }
+  }
+}
+
+// Data wave: fold its max into the workgroup's LDS slot for slab s.
+__device__ __forceinline__ void contribute(FusedShared &sh, int s, uint32_t mx, bool real) {
+  mx = group_max(mx, 64);
+  if (real && (threadIdx.x & 63) == 0) {
+    const int slot = s & (FA_SLOTS - 1);
+    __hip_atomic_fetch_max(&sh.max[slot], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    ZX_COMPILER_FENCE();
+    __hip_atomic_fetch_add(&sh.cnt[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
+// Data wave: wait for slab s's scale; false if the launch was aborted.
+__device__ __forceinline__ bool wait_ready(const FusedShared &sh, int s, float &sc) {
+  const int slot = s & (FA_SLOTS - 1);
+  while (ld_lds(&sh.ready[slot]) != (uint32_t)(s + 1)) {
+    if (ld_lds(&sh.abort)) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  ZX_COMPILER_FENCE();
+  sc = __uint_as_float(ld_lds(reinterpret_cast<const uint32_t *>(&sh.scale[slot])));
+  return true;
+}
+
+// Control wave: workgroup <-> device protocol, all slabs in order.  Publishes a slab as
+// soon as the data waves' contributions are in (up to pub_ahead past the oldest
+// unresolved one), and resolves the oldest published slab once every workgroup's slot
+// is filled.  Returns false on timeout or abort.
+__device__ __forceinline__ bool control_loop(const FusedArgs &a, FusedShared &sh, int S, int S_pad,
+                                             uint32_t G, int pub_ahead) {
+  const int lane = threadIdx.x & 63;
+  int next_pub = 0, next_res = 0;
+  uint64_t t_progress = __builtin_amdgcn_s_memrealtime();
+  while (next_res < S) {
+    bool progress = false;
+    while (next_pub < S && next_pub < next_res + pub_ahead &&
+           ld_lds(&sh.cnt[next_pub & (FA_SLOTS - 1)]) == (uint32_t)FA_DATA_WAVES) {
+      const int slot = next_pub & (FA_SLOTS - 1);
+      ZX_COMPILER_FENCE();
+      const uint32_t mx = ld_lds(&sh.max[slot]);
+      if (lane == 0) {
+        __hip_atomic_store(&a.slots[(int64_t)next_pub * G + blockIdx.x], mx, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        sh.max[slot] = 0;
+        sh.cnt[slot] = 0;
+      }
+      ++next_pub;
+      progress = true;
+    }
+    if (next_res < next_pub) {
+      const uint32_t *row = a.slots + (int64_t)next_res * G;
+      uint32_t mx = 0;
+      bool full = true;
+      for (uint32_t i = lane; i < G; i += 64) {
+        const uint32_t v = __hip_atomic_load(&row[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        full = full && v != FA_EMPTY;
+        mx = max(mx, v == FA_EMPTY ? 0u : v);
+      }
+      if (__ballot(!full) == 0) {
+        mx = group_max(mx, 64);
+        const float sc = scale_from_amax_bits(mx << 16);
+        const int slot = next_res & (FA_SLOTS - 1);
+        if (lane == 0) {
+          if (blockIdx.x == 0) a.scales[next_res] = sc;
+          sh.scale[slot] = sc;
+          ZX_COMPILER_FENCE();
+          __hip_atomic_store(&sh.ready[slot], (uint32_t)(next_res + 1), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        ++next_res;
+        progress = true;
+      }
+    }
+    if (progress) {
+      t_progress = __builtin_amdgcn_s_memrealtime();
+      continue;
+    }
+    if (ld_agent(a.abort_flag) || __builtin_amdgcn_s_memrealtime() - t_progress > a.spin_ticks) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  // padding steps past the last slab: scale 1, nothing published
+  for (int s = S; s < S_pad; ++s) {
+    const int slot = s & (FA_SLOTS - 1);
+    if (lane == 0) {
+      sh.scale[slot] = 1.0f;
+      ZX_COMPILER_FENCE();
+      __hip_atomic_store(&sh.ready[slot], (uint32_t)(s + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+  return true;
+}
+
+// K: 16-byte vectors per data thread per slab kept in registers; NB: register buffers
+// (the data waves run NB - 1 slabs ahead of the oldest unresolved one).
+// SPILL: some share holds more vectors than the registers (extra loops re-read them);
+// without it the data path is straight-line code between waits.
+template <int K, int NB, bool SPILL>
+__global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArgs a) {
+  static_assert(NB + 1 <= FA_SLOTS, "slot ring too small");
+  __shared__ FusedShared sh;
+  const uint32_t G = gridDim.x;
+  const int64_t t_lo = (int64_t)blockIdx.x * a.n_tok / G;
+  const int64_t t_hi = (int64_t)(blockIdx.x + 1) * a.n_tok / G;
+  const int nv = (int)(t_hi - t_lo) << a.vpt_log2;
+  const int S = a.n_layers * 2 * a.n_heads;
+  if (threadIdx.x < FA_SLOTS) {
+    sh.max[threadIdx.x] = 0;
+    sh.cnt[threadIdx.x] = 0;
+    sh.ready[threadIdx.x] = 0;
+  }
+  if (threadIdx.x == 0) sh.abort = 0;
+  __syncthreads();
+
+  if (threadIdx.x >= FA_DATA_THREADS) {  // control wave
+    if (!control_loop(a, sh, S, (int)ceil_div(S, NB) * NB, G, NB) && threadIdx.x == FA_DATA_THREADS) {
+      __hip_atomic_fetch_or(a.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (a.err) atomicOr(a.err, ZX_KERR_SPIN);
+      __hip_atomic_store(&sh.abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    return;
+  }
+
+  ThreadMap<K> m;
+  m.nreg = nv < K * FA_DATA_THREADS ? nv : K * FA_DATA_THREADS;
+  m.live = 0;
+  // a workgroup with an empty share reads token 0 of the slab (valid: n_tok >= 1)
+  const int64_t t_base = nv > 0 ? t_lo : 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int v = k * FA_DATA_THREADS + threadIdx.x;
+    const bool live = v < m.nreg;
+    m.live |= (uint32_t)live << k;
+    const int64_t off = live ? a.tok_off[t_lo + (v >> a.vpt_log2)] : -1;
+    m.dst[k] = off < 0 ? -1 : off + (v & ((1 << a.vpt_log2) - 1)) * 8;
+  }
+  uint8_t *dummy = reinterpret_cast<uint8_t *>(a.abort_flag) + 64 + 8 * (threadIdx.x & 15);
+
+  // Slabs past the end are clamped to the last one: the loads stay unconditional (and
+  // valid) and their maxes are simply not contributed.
+  auto clamp = [&](int s) { return s < S ? s : S - 1; };
+  uint4 buf[NB][K];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) load_share<K>(a, m, clamp(i), t_base, buf[i]);
+#pragma unroll
+  for (int i = 0; i + 1 < NB; ++i) contribute(sh, i, share_max<K, SPILL>(a, m, clamp(i), t_lo, nv, buf[i]), i < S);
+
+  // step s (buffer i = s % NB): encode s, refill the buffer with s + NB, reduce s + NB - 1.
+  // The slab count is padded to a multiple of NB so every unrolled step is unconditional
+  // (padded steps encode into the dummy slot; the control wave marks them ready at the
+  // end); an aborted wait leaves the kernel directly.
+  const int S_pad = (int)ceil_div(S, NB) * NB;
+  for (int s0 = 0; s0 < S_pad; s0 += NB) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int s = s0 + i;
+      float sc;
+      if (!wait_ready(sh, s, sc)) return;
+      encode_share<K, SPILL>(a, m, s, t_lo, nv, buf[i], sc, s < S ? slab_dst(a, s) : nullptr, dummy);
+      load_share<K>(a, m, clamp(s + NB), t_base, buf[i]);
+      const int j = (i + NB - 1) % NB;  // constant after unrolling
+      contribute(sh, s + NB - 1, share_max<K, SPILL>(a, m, clamp(s + NB - 1), t_lo, nv, buf[j]), s + NB - 1 < S);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+#ifndef FA_K_CHOICE
+#define FA_K_CHOICE 5
+#endif
+#ifndef FA_NB_CHOICE
+#define FA_NB_CHOICE 4
+#endif
+constexpr int FA_K = FA_K_CHOICE;
+#define FA_KERNEL(spill) kv_append_fused_kernel<FA_K, FA_NB_CHOICE, spill>
+
+static int fused_supported() {
+  static int cached[64] = {0};
+  int dev = 0;
+  ZX_TRY_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(ZX_ERR_UNSUPPORTED, "device index out of range");
+  if (!cached[dev]) {
+    int coop = 0, per_cu = 0;
+    ZX_TRY_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
+    int per_cu2 = 0;
+    ZX_TRY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, FA_KERNEL(false), FA_THREADS, 0));
+    ZX_TRY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu2, FA_KERNEL(true), FA_THREADS, 0));
+    cached[dev] = (coop && per_cu >= 1 && per_cu2 >= 1) ? 1 : -1;
+  }
+  if (cached[dev] < 0) return fail(ZX_ERR_UNSUPPORTED, "device cannot co-schedule the single-pass append");
+  return ZX_OK;
+}
+
+// workspace: abort flag (+ 60 B pad) | dummy store slots (128 B) | slots [S][G]
+size_t append_fused_workspace_bytes(int32_t n_layers, int32_t n_heads) {
+  const size_t S = (size_t)n_layers * 2 * n_heads;
+  return 256 + align256(S * (size_t)num_cus() * 4);
+}
+
+int append_fused(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, int64_t n_tok, int32_t n_heads,
+                 int32_t head_dim, const int64_t *tok_off, uint8_t *pool, int64_t pool_layer_stride,
+                 int32_t page_size, float *scales, int32_t *err, void *ws, hipStream_t st) {
+  int rc = fused_supported();
+  if (rc) return rc;
+  const int G = num_cus();
+  if (ceil_div(n_tok, G) * (head_dim / 8) >= (1LL << 30))
+    return fail(ZX_ERR_UNSUPPORTED, "fused append: share too large");
+  const int64_t S = (int64_t)n_layers * 2 * n_heads;
+  char *w = static_cast<char *>(ws);
+  FusedArgs a;
+  a.x = x;
+  a.x_layer_stride = x_layer_stride;
+  a.n_tok = n_tok;
+  a.n_layers = n_layers;
+  a.n_heads = n_heads;
+  a.head_dim = head_dim;
+  a.page_size = page_size;
+  a.vpt_log2 = head_dim == 64 ? 3 : (head_dim == 128 ? 4 : 5);
+  a.tok_off = tok_off;
+  a.pool = pool;
+  a.pool_layer_stride = pool_layer_stride;
+  a.scales = scales;
+  a.abort_flag = reinterpret_cast<uint32_t *>(w);
+  a.slots = reinterpret_cast<uint32_t *>(w + 256);
+  a.err = err;
+  a.spin_ticks = 200000000ull;  // 2 s without progress, at 100 MHz
+  // the abort flag starts at zero and every slot at the sentinel (fill kernels, not
+  // memsets, so the sequence stays valid inside a captured graph)
+  if ((rc = fill_u32(a.abort_flag, 1, 0, st))) return rc;
+  if ((rc = fill_u32(a.slots, S * G, FA_EMPTY, st))) return rc;
+  void *args[] = {&a};
+  const bool spill = ceil_div(n_tok, G) * (head_dim / 8) > (int64_t)FA_K * FA_DATA_THREADS;
+  const void *fn = spill ? reinterpret_cast<const void *>(FA_KERNEL(true))
+                         : reinterpret_cast<const void *>(FA_KERNEL(false));
+  ZX_TRY_HIP(hipLaunchCooperativeKernel(fn, dim3(G), dim3(FA_THREADS), args, 0, st));
+  return check_launch("kv_append_fused");
+}
+
+}  // namespace zx

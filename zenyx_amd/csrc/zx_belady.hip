@@ -2,7 +2,7 @@
 // next-use tables it needs.  The trace-level simulator lives in zx_belady_sim.hip.
 #include <hipcub/hipcub.hpp>
 
-#include "zx_common.h"
+#include "zx_internal.h"
 
 namespace zx {
 
@@ -114,7 +114,7 @@ static int key_bits(int32_t n_pages) {
   return b;
 }
 
-static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
 
 static size_t sort_temp_bytes(int64_t n, int32_t n_pages) {
   size_t temp = 0;

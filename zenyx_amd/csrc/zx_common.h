@@ -31,7 +31,7 @@ int check_launch(const char *what);
     if (!(cond)) return ::zx::fail(ZX_ERR_INVALID, __VA_ARGS__);                          \
   } while (0)
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Number of compute units of the current device (cached per device).
 int num_cus();
@@ -126,6 +126,36 @@ __device__ __forceinline__ uint4 quant16(uint4 a, uint4 b, float s, float r, int
     out = make_uint4(o[0], o[1], o[2], o[3]);
   }
   return out;
+}
+
+// 8 bf16 values (one 16-byte word) -> 8 e4m3 codes (one 8-byte word).  Branch-free:
+// the non-finite-scale codes are computed alongside and selected, so callers that keep
+// several loads in flight see straight-line code.
+__device__ __forceinline__ uint2 quant8(uint4 a, float s, float r, int mode) {
+  uint32_t w[4] = {a.x, a.y, a.z, a.w};
+  uint32_t o[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    uint32_t u0 = w[2 * k], u1 = w[2 * k + 1];
+    uint32_t fin = e4m3x4(div_by_scale(bf_lo(u0), s, r), div_by_scale(bf_hi(u0), s, r),
+                          div_by_scale(bf_lo(u1), s, r), div_by_scale(bf_hi(u1), s, r));
+    uint32_t nf = code_nonfinite(u0 & 0xFFFFu, mode) | (code_nonfinite(u0 >> 16, mode) << 8) |
+                  (code_nonfinite(u1 & 0xFFFFu, mode) << 16) | (code_nonfinite(u1 >> 16, mode) << 24);
+    o[k] = mode == 0 ? fin : nf;
+  }
+  return make_uint2(o[0], o[1]);
+}
+
+// Largest |bf16| bit pattern among 8 values.
+__device__ __forceinline__ uint32_t absmax8(uint4 q) {
+  uint32_t m = 0;
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t u = w[k] & 0x7FFF7FFFu;
+    m = max(m, max(u & 0xFFFFu, u >> 16));
+  }
+  return m;
 }
 
 // Largest |bf16| bit pattern among 16 values (as a 16-bit magnitude in a uint32).

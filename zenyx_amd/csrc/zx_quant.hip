@@ -4,7 +4,7 @@
 //   * per-(layer, kv, head) scales and the paged append with fused quant
 // Every kernel streams 16-byte vectors; all are HBM-bound (no MFMA: nothing here is a
 // contraction).
-#include "zx_common.h"
+#include "zx_internal.h"
 
 namespace zx {
 
@@ -13,7 +13,7 @@ __global__ void fill_u32_kernel(uint32_t *p, int64_t n, uint32_t v) {
   if (i < n) p[i] = v;
 }
 
-static int fill_u32(uint32_t *p, int64_t n, uint32_t v, hipStream_t st) {
+int fill_u32(uint32_t *p, int64_t n, uint32_t v, hipStream_t st) {
   if (n <= 0) return ZX_OK;
   fill_u32_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(p, n, v);
   return check_launch("fill_u32");
@@ -468,10 +468,9 @@ extern "C" int zx_kv_scales(const uint16_t *x, int64_t x_layer_stride, int32_t n
 
 extern "C" size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32_t n_heads,
                                                      int32_t head_dim) {
-  (void)n_layers;
-  (void)n_heads;
   (void)head_dim;
-  return (size_t)(n_tok > 0 ? n_tok : 0) * sizeof(int64_t) + 256;
+  return align256((size_t)(n_tok > 0 ? n_tok : 0) * sizeof(int64_t)) +
+         append_fused_workspace_bytes(n_layers, n_heads);
 }
 
 extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
@@ -487,6 +486,7 @@ extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int
   ZX_REQUIRE(n_layers > 0 && n_layers <= 65535, "kv_quant_append: n_layers out of range");
   ZX_REQUIRE(n_seqs > 0 && max_blocks > 0 && page_size > 0 && n_pages > 0,
              "kv_quant_append: n_seqs, max_blocks, page_size and n_pages must be positive");
+  ZX_REQUIRE(n_tok < (1LL << 31), "kv_quant_append: n_tok must be below 2^31");
   RowGeom g;
   int rc = row_geom(n_heads, head_dim, n_tok, x_layer_stride, g);
   if (rc) return rc;
@@ -499,13 +499,21 @@ extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int
   if (!workspace || workspace_bytes < need)
     return fail(ZX_ERR_WORKSPACE, "kv_quant_append: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t st = as_stream(stream);
-  if (!(flags & ZX_APPEND_STATIC_SCALES) && (rc = kv_scales_impl(x, g, n_layers, scales, st))) return rc;
-  if (n_tok == 0) return ZX_OK;
+  const bool dynamic = !(flags & ZX_APPEND_STATIC_SCALES);
+  if (n_tok == 0) return dynamic ? kv_scales_impl(x, g, n_layers, scales, st) : ZX_OK;
   int64_t *tok_off = reinterpret_cast<int64_t *>(workspace);
   kv_token_offsets_kernel<<<(unsigned)ceil_div(n_tok, 256), 256, 0, st>>>(
       cu_seqlens, start_pos, n_seqs, block_tables, max_blocks, page_size, n_pages, page_bytes, head_dim,
       n_tok, tok_off, err);
   if ((rc = check_launch("kv_token_offsets"))) return rc;
+  if (dynamic && !(flags & ZX_APPEND_TWO_PASS)) {
+    void *fws = static_cast<char *>(workspace) + align256((size_t)n_tok * sizeof(int64_t));
+    rc = append_fused(x, x_layer_stride, n_layers, n_tok, n_heads, head_dim, tok_off, pool, pool_layer_stride,
+                      page_size, scales, err, fws, st);
+    if (rc != ZX_ERR_UNSUPPORTED) return rc;
+    clear_error();  // this device cannot run the single-pass kernel: two passes below
+  }
+  if (dynamic && (rc = kv_scales_impl(x, g, n_layers, scales, st))) return rc;
   kv_quant_append_kernel<<<kv_grid(g, n_layers), g.vpr * g.rb, 0, st>>>(
       x, g, tok_off, scales, pool, pool_layer_stride, page_size, head_dim);
   return check_launch("kv_quant_append");

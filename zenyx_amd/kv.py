@@ -154,7 +154,7 @@ def kv_scales(x: torch.Tensor) -> torch.Tensor:
 def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: torch.Tensor,
                     pool: torch.Tensor, scales: torch.Tensor | None = None,
                     start_pos: torch.Tensor | None = None, static_scales: bool = False,
-                    check: bool = False) -> torch.Tensor:
+                    check: bool = False, two_pass: bool = False) -> torch.Tensor:
     """Paged append with fused FP8 quantisation.
 
     x ``[L, n_tok, 2, H, D]`` bf16; cu_seqlens int32 ``[B+1]``; block_tables int32
@@ -191,7 +191,7 @@ def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: tor
     lib = N.load()
     ws = _workspace(lib.zx_kv_quant_append_workspace_bytes(L, T, H, D), x.device)
     err = _err_word(x.device)
-    flags = N.ZX_APPEND_STATIC_SCALES if static_scales else 0
+    flags = (N.ZX_APPEND_STATIC_SCALES if static_scales else 0) | (N.ZX_APPEND_TWO_PASS if two_pass else 0)
     N.check(lib.zx_kv_quant_append(N.ptr(x), T * 2 * H * D, L, T, H, D, N.ptr(cu_seqlens), N.ptr(start_pos),
                                    block_tables.shape[0], N.ptr(block_tables), block_tables.shape[1], P,
                                    N.ptr(pool), pool[0].numel(), n_pages, N.ptr(scales), flags, N.ptr(err),
