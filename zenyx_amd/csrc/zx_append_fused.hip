@@ -108,7 +108,11 @@ __device__ __forceinline__ void load_share(const FusedArgs &a, const ThreadMap<K
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int v = k * FA_DATA_THREADS + (int)threadIdx.x;
-    r[k] = *reinterpret_cast<const uint4 *>(base + ((m.live >> k) & 1 ? vec_src(a, v) : 0));
+    // nontemporal: the input is read exactly once (2% faster at configs[1] on MI355X)
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u q = __builtin_nontemporal_load(
+        reinterpret_cast<const v4u *>(base + ((m.live >> k) & 1 ? vec_src(a, v) : 0)));
+    r[k] = make_uint4(q.x, q.y, q.z, q.w);
   }
 }
 
