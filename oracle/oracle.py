@@ -54,7 +54,7 @@ def lib() -> ctypes.CDLL:
             "zxo_int8_legacy_dequant": (None, [P, f32, i64, P]),
             "zxo_belady_argmax": (None, [P, P, i64, P]),
             "zxo_next_use": (None, [P, i64, i32, P, P]),
-            "zxo_belady_simulate": (i64, [P, i64, i32, i64, P, P, i64, P]),
+            "zxo_belady_simulate": (i64, [P, i64, i32, i64, P, P, i64, P, P]),
             "zxo_ring_trace": (None, [i32, i32, i32, P]),
         }
         for name, (res, args) in sig.items():
@@ -215,18 +215,22 @@ def next_use(trace: np.ndarray, n_pages: int):
     return nu, pu
 
 
-def belady_simulate(trace: np.ndarray, n_pages: int, capacity: int, evict_cap: int | None = None):
-    """Heap-based Belady MIN; returns (evict_pos, evict_page, stats{misses,hits,resident})."""
+def belady_simulate(trace: np.ndarray, n_pages: int, capacity: int, evict_cap: int | None = None,
+                    miss_flags: bool = False):
+    """Heap-based Belady MIN; returns (evict_pos, evict_page, stats{misses,hits,resident}
+    [, miss_flags])."""
     trace = np.ascontiguousarray(trace, dtype=np.int32)
     cap = trace.size if evict_cap is None else evict_cap
     ep = np.empty(max(cap, 1), np.int32)
     eg = np.empty(max(cap, 1), np.int32)
     stats = np.zeros(3, np.int64)
+    mf = np.zeros(trace.size, np.uint8) if miss_flags else None
     n_ev = lib().zxo_belady_simulate(_p(trace), trace.size, n_pages, capacity, _p(ep), _p(eg),
-                                     cap, _p(stats))
+                                     cap, _p(stats), _p(mf))
     k = min(n_ev, cap)
-    return ep[:k].copy(), eg[:k].copy(), {"evictions": int(n_ev), "misses": int(stats[0]),
-                                          "hits": int(stats[1]), "resident": int(stats[2])}
+    out = (ep[:k].copy(), eg[:k].copy(), {"evictions": int(n_ev), "misses": int(stats[0]),
+                                          "hits": int(stats[1]), "resident": int(stats[2])})
+    return out + (mf,) if miss_flags else out
 
 
 def ring_trace(n_layers: int, ring: int, shard_pages: int) -> np.ndarray:

@@ -374,10 +374,11 @@ static void heap_down(zxo_heap *H, int64_t i) {
  * then admits the missed page; a hit moves the page's key to its next use.  The per-miss
  * argmax of belady.py:46-50 is kept exactly, with a heap instead of a linear scan.
  * Returns the number of evictions (entries beyond evict_cap are counted, not stored);
- * stats[0] = misses, stats[1] = hits, stats[2] = final resident count. */
+ * stats[0] = misses, stats[1] = hits, stats[2] = final resident count; miss_flags (may be
+ * NULL) receives 1 at every miss position. */
 int64_t zxo_belady_simulate(const int32_t *trace, int64_t n, int32_t n_pages, int64_t capacity,
                             int32_t *evict_pos, int32_t *evict_page, int64_t evict_cap,
-                            int64_t *stats) {
+                            int64_t *stats, uint8_t *miss_flags) {
   int32_t *next_use = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n ? n : 1));
   int32_t *prev_use = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n ? n : 1));
   int32_t *key = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
@@ -391,6 +392,7 @@ int64_t zxo_belady_simulate(const int32_t *trace, int64_t n, int32_t n_pages, in
   int64_t ev = 0, misses = 0, hits = 0;
   for (int64_t i = 0; i < n; ++i) {
     int32_t p = trace[i];
+    if (miss_flags) miss_flags[i] = H.pos[p] < 0;
     if (H.pos[p] >= 0) {
       ++hits;
       key[p] = next_use[i];

@@ -276,3 +276,61 @@ def next_use(trace: torch.Tensor, n_pages: int, check: bool = False):
     if check:
         _raise_kernel_error(err, "belady_next_use")
     return nu, pu
+
+
+class BeladyTraceSim:
+    """Belady MIN over an int32 page trace on the GPU (zx_belady_simulate).
+
+    The cache state (resident flags, next-use keys, counters) lives in device tensors, so
+    the trace can be processed in pieces with ``run(t_end)``; victims accumulate in
+    ``evict_pos`` / ``evict_page`` (device int32, first ``n_evicted`` entries valid).
+    """
+
+    def __init__(self, trace: torch.Tensor, n_pages: int, capacity: int, evict_cap: int | None = None,
+                 record_misses: bool = False):
+        N.ensure_gpu()
+        if trace.dtype != torch.int32 or trace.dim() != 1:
+            raise ValueError("trace must be a 1-D int32 device tensor")
+        if capacity < 1:
+            raise ValueError("capacity must be >= 1")
+        N.require_device(trace, "trace")
+        dev = trace.device
+        self.trace, self.n_pages, self.capacity = trace, int(n_pages), int(capacity)
+        self.n_total = trace.numel()
+        self.next_use, self.prev_use = next_use(trace, n_pages, check=True)
+        self.resident = torch.zeros(self.n_pages, dtype=torch.uint8, device=dev)
+        self.key = torch.full((self.n_pages,), N.ZX_NEVER, dtype=torch.int32, device=dev)
+        self.state = torch.zeros(4, dtype=torch.int64, device=dev)
+        cap = self.n_total if evict_cap is None else int(evict_cap)
+        self.evict_cap = cap
+        self.evict_pos = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+        self.evict_page = torch.empty(max(cap, 1), dtype=torch.int32, device=dev)
+        self.miss_flags = torch.zeros(self.n_total, dtype=torch.uint8, device=dev) if record_misses else None
+        lib = N.load()
+        self._ws = _workspace(lib.zx_belady_simulate_workspace_bytes(self.n_total, self.n_pages), dev)
+        self.t = 0
+
+    def run(self, t_end: int | None = None) -> None:
+        """Process trace positions [self.t, t_end) (default: to the end)."""
+        t_end = self.n_total if t_end is None else int(t_end)
+        if not self.t <= t_end <= self.n_total:
+            raise ValueError(f"t_end must lie in [{self.t}, {self.n_total}]")
+        N.check(N.load().zx_belady_simulate(
+            N.ptr(self.trace), N.ptr(self.next_use), N.ptr(self.prev_use), self.n_total, self.t, t_end,
+            self.n_pages, self.capacity, N.ptr(self.resident), N.ptr(self.key), N.ptr(self.state),
+            N.ptr(self.evict_pos), N.ptr(self.evict_page), self.evict_cap, N.ptr(self.miss_flags),
+            N.ptr(self._ws), self._ws.numel(), N.stream_ptr(self.trace.device)), "belady_simulate")
+        self.t = t_end
+
+    @property
+    def n_evicted(self) -> int:
+        return int(self.state[1].item())
+
+    def stats(self) -> dict:
+        s = self.state.tolist()
+        return {"resident": s[0], "evictions": s[1], "misses": s[2], "hits": s[3]}
+
+    def evictions(self):
+        """(positions, pages) of the stored victims as CPU int32 tensors."""
+        k = min(self.n_evicted, self.evict_cap)
+        return self.evict_pos[:k].cpu(), self.evict_page[:k].cpu()
