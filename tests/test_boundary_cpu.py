@@ -1,0 +1,94 @@
+"""CPU-side checks of the drop-in boundary: the C-ABI library loads and exports every entry
+point include/zenyx_kv.h declares, argument errors come back as status codes (no GPU
+needed: validation precedes every HIP call), and the host-side logic (ring access
+sequence, tiering sizes, reference timeline) matches the oracle and closed forms."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "zenyx_kv.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(zx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    from zenyx_amd import _native
+
+    lib = _native.load()
+    syms = header_symbols()
+    assert len(syms) >= 15
+    for s in syms:
+        assert hasattr(lib, s), f"libzenyx_kv.so does not export {s}"
+        assert s in _native.SIGNATURES, f"{s} has no ctypes signature"
+    assert lib.zx_abi_version() == _native.ABI_VERSION
+
+
+def test_argument_errors_are_status_codes():
+    from zenyx_amd import _native as N
+
+    lib = N.load()
+    rc = lib.zx_kv_gather_dequant(None, 10, 8, 128, 16, None, None, 4, None, 2, 64, None, None, None, None)
+    assert rc == N.ZX_ERR_INVALID and b"null pointer" in lib.zx_last_error()
+    rc = lib.zx_kv_gather_dequant(ctypes.c_void_p(16), 10, 8, 96, 16, ctypes.c_void_p(16), ctypes.c_void_p(16), 4,
+                                  ctypes.c_void_p(16), 2, 64, ctypes.c_void_p(16), ctypes.c_void_p(16), None, None)
+    assert rc == N.ZX_ERR_UNSUPPORTED and b"head_dim" in lib.zx_last_error()
+    rc = lib.zx_int8_legacy_quant(ctypes.c_void_p(16), 0, 0, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                  ctypes.c_void_p(16), 256, None)
+    assert rc == N.ZX_ERR_INVALID and b"empty" in lib.zx_last_error()
+    rc = lib.zx_belady_simulate(None, None, None, 10, 0, 10, 5, 0, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                ctypes.c_void_p(16), None, None, 0, None, None, 0, None)
+    assert rc == N.ZX_ERR_INVALID and b"capacity" in lib.zx_last_error()
+    with pytest.raises(ValueError):
+        N.check(N.ZX_ERR_INVALID, "x")
+    with pytest.raises(N.ZenyxNativeError):
+        N.check(N.ZX_ERR_HIP, "x")
+
+
+def test_workspace_queries_are_host_only():
+    from zenyx_amd import _native as N
+
+    lib = N.load()
+    assert lib.zx_kv_quant_append_workspace_bytes(32, 74902, 8, 128) >= 74902 * 8
+    assert lib.zx_belady_simulate_workspace_bytes(20_971_520, 1_310_720) >= (20_971_520 + 1_310_720) // 8
+    assert lib.zx_belady_argmax_workspace_bytes(1000) >= 16
+
+
+@pytest.mark.parametrize("L,R,S", [(1, 1, 5), (3, 8, 4), (2, 4, 7)])
+def test_ring_access_sequence_matches_oracle(L, R, S):
+    from zenyx_amd.train.belayd_kv_cache_tiering import RingAttentionAccessSequence
+
+    seq = RingAttentionAccessSequence(L, R, S)
+    tr = seq.trace("cpu").numpy()
+    np.testing.assert_array_equal(tr, O.ring_trace(L, R, S))
+    assert len(seq) == tr.size and seq.n_pages == L * R * S
+
+
+def test_tiering_manager_sizes_at_baseline_config():
+    from zenyx_amd.train.belayd_kv_cache_tiering import BeladyKVCacheTieringManager
+
+    m = BeladyKVCacheTieringManager(num_devices=8, context_length=2**20, num_layers=80, num_kv_heads=8,
+                                    head_dim=128, page_tokens=64, hbm_budget_bytes=64e9)
+    assert m.page_bytes == 128 * 1024
+    assert m.pages_per_shard == 2048
+    assert m.n_pages == 1_310_720
+    assert m.capacity == 488_281
+    assert len(m.sequence) == 20_971_520
+    # the README constructor (README.md:93-97)
+    r = BeladyKVCacheTieringManager(num_devices=8, context_length=4096, num_layers=12)
+    assert r.capacity == r.n_pages == 12 * 8 * 8
+
+
+def test_build_ring_timeline_matches_reference():
+    from zenyx_amd.streaming import build_ring_timeline
+
+    for n in (1, 2, 7):
+        assert build_ring_timeline(n) == O.ref_ring_timeline(n)

@@ -1,0 +1,152 @@
+"""Drop-in for zenyx/streaming/kv_tiering.py: T0 (HBM) / T1 (host DRAM) / T2 (cold) KV
+tiers with LRU spill, and the ring-attention access timeline.
+
+Same public surface as the reference (kv_tiering.py:11-73): ``KVBlockRef``,
+``KVTierManager(t0_capacity, t1_capacity)`` with the ``t0``/``t1``/``t2`` dicts, ``put``,
+``prefetch_to_t0``, ``evict_from_t0``, and ``build_ring_timeline``.  The copies the
+reference does with ``.to(device)`` / ``.cpu()`` (kv_tiering.py:46, 54, 60) go through
+zx_tier_copy_runs (hipMemcpyAsync) on a side stream:
+  * host -> device: the side stream waits for the caller's stream, copies, and the caller's
+    stream waits for the copy, so the returned tensor is ready for the caller's kernels
+    without blocking the host;
+  * device -> host: the destination is pinned host memory; the copy runs on the side stream
+    (overlapping kernels on other streams) and the host waits only for that copy, because
+    the reference hands back a CPU tensor that is ready to read.
+Eviction policy, capacities, KeyError on unknown ids and the aliasing of CPU tensors by
+``put`` (``.cpu()`` of a CPU tensor is the same tensor) follow the reference.
+"""
+from __future__ import annotations
+
+import ctypes
+from collections import OrderedDict
+from dataclasses import dataclass
+
+import torch
+
+from .. import _native as N
+
+
+@dataclass
+class KVBlockRef:
+    """kv_tiering.py:11-15."""
+
+    block_id: int
+    seq_start: int
+    seq_end: int
+
+
+class _SideStream:
+    """One side stream per device for tier copies."""
+
+    _streams: dict = {}
+
+    @classmethod
+    def get(cls, device: torch.device) -> torch.cuda.Stream:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        s = cls._streams.get(idx)
+        if s is None:
+            s = torch.cuda.Stream(device=idx)  # default priority
+            cls._streams[idx] = s
+        return s
+
+
+def _copy(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) -> None:
+    nbytes = src.numel() * src.element_size()
+    if nbytes == 0:
+        return
+    off = (ctypes.c_int64 * 1)(0)
+    N.check(N.load().zx_tier_copy_runs(N.ptr(dst), N.ptr(src), off, off, 1, nbytes,
+                                       ctypes.c_void_p(stream.cuda_stream), None), "tier copy")
+
+
+def to_device(cpu_tensor: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """Host tensor -> new device tensor, copied on the side stream, ordered before any later
+    work on the caller's current stream."""
+    N.ensure_gpu()
+    src = cpu_tensor.contiguous()
+    cur = torch.cuda.current_stream(device)
+    side = _SideStream.get(device)
+    out = torch.empty(src.shape, dtype=src.dtype, device=device)
+    side.wait_stream(cur)
+    _copy(out, src, side)
+    out.record_stream(side)
+    cur.wait_stream(side)
+    return out
+
+
+def to_host(gpu_tensor: torch.Tensor) -> torch.Tensor:
+    """Device tensor -> pinned host tensor; returns once the copy (on the side stream) is done."""
+    N.ensure_gpu()
+    src = gpu_tensor.detach().contiguous()
+    dev = src.device
+    cur = torch.cuda.current_stream(dev)
+    side = _SideStream.get(dev)
+    out = torch.empty(src.shape, dtype=src.dtype, pin_memory=True)
+    side.wait_stream(cur)
+    _copy(out, src, side)
+    src.record_stream(side)
+    done = torch.cuda.Event()
+    done.record(side)
+    done.synchronize()
+    return out
+
+
+class KVTierManager:
+    """T0/T1/T2 KV cache hierarchy (kv_tiering.py:18-66).
+
+    - T0: active HBM blocks (tiny)
+    - T1: host DRAM recent blocks (pinned)
+    - T2: cold storage (disk-backed emulation)
+    """
+
+    def __init__(self, t0_capacity: int = 2, t1_capacity: int = 32):
+        self.t0: OrderedDict[int, torch.Tensor] = OrderedDict()
+        self.t1: OrderedDict[int, torch.Tensor] = OrderedDict()
+        self.t2: dict[int, torch.Tensor] = {}
+        self.t0_capacity = t0_capacity
+        self.t1_capacity = t1_capacity
+
+    def put(self, block_id: int, tensor: torch.Tensor) -> None:  # kv_tiering.py:33-34
+        t = tensor.detach()
+        self.t2[block_id] = t if t.device.type == "cpu" else to_host(t)
+
+    def prefetch_to_t0(self, block_id: int, device: torch.device) -> torch.Tensor:  # :36-49
+        if block_id in self.t0:
+            self.t0.move_to_end(block_id)
+            return self.t0[block_id]
+        if block_id in self.t1:
+            cpu_tensor = self.t1.pop(block_id)
+        else:
+            cpu_tensor = self.t2[block_id]  # KeyError for an unknown block, as the reference
+        device = torch.device(device)
+        gpu_tensor = to_device(cpu_tensor, device) if device.type == "cuda" else cpu_tensor.to(device)
+        self.t0[block_id] = gpu_tensor
+        self._evict_t0_if_needed()
+        return gpu_tensor
+
+    def evict_from_t0(self, block_id: int) -> None:  # :51-55
+        tensor = self.t0.pop(block_id, None)
+        if tensor is not None:
+            self.t1[block_id] = to_host(tensor) if tensor.device.type == "cuda" else tensor.detach()
+            self._evict_t1_if_needed()
+
+    def _evict_t0_if_needed(self) -> None:  # :57-61, least recently used first
+        while len(self.t0) > self.t0_capacity:
+            old_block, old_tensor = self.t0.popitem(last=False)
+            self.t1[old_block] = to_host(old_tensor) if old_tensor.device.type == "cuda" else old_tensor.detach()
+            self._evict_t1_if_needed()
+
+    def _evict_t1_if_needed(self) -> None:  # :63-66
+        while len(self.t1) > self.t1_capacity:
+            old_block, old_tensor = self.t1.popitem(last=False)
+            self.t2[old_block] = old_tensor
+
+
+def build_ring_timeline(num_blocks: int) -> dict[str, list[int]]:
+    """Deterministic forward/backward access schedule for ring attention (kv_tiering.py:69-73)."""
+    forward = list(range(num_blocks))
+    backward = list(reversed(forward))
+    return {"forward": forward, "backward": backward}
+
+
+__all__ = ["KVTierManager", "KVBlockRef", "build_ring_timeline"]

@@ -1,0 +1,3 @@
+"""README-documented Phase-7/8 modules of zenyx, MI355X-native:
+``belayd_kv_cache_tiering`` (Belady KV tiering over a ring schedule) and
+``fp8_kv_quantization`` (per-head FP8 KV quantisation and a paged FP8 KV cache)."""

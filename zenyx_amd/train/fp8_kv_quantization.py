@@ -1,0 +1,116 @@
+"""FP8 KV quantisation (README.md:157-159, 329, 344: ``FP8KVQuantizer``; the module the
+README names, zenyx/train/fp8_kv_quantization.py, is absent from the reference tree, so
+its behaviour is defined here and in include/zenyx_kv.h).
+
+* ``FP8KVQuantizer`` -- e4m3fn codes with one fp32 scale per (layer, K/V, head):
+  scale = max(amax, 1e-8) / 448, code = e4m3fn_RNE(x / scale), dequant = bf16_RNE(code * scale).
+* ``PagedFP8KVCache`` -- a paged FP8 KV cache: page pool ``[L, n_pages, 2, H, P, D]``,
+  host-side page allocator and block tables, fused quantize+append of new tokens and
+  gather+dequant of whole sequences for decode.
+All arithmetic runs in libzenyx_kv.so on the HIP device.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import kv
+from .._native import ensure_gpu
+
+
+class FP8KVQuantizer:
+    """Per-(layer, kv, head) dynamic FP8 e4m3fn quantisation of a KV cache tensor."""
+
+    E4M3_MAX = 448.0
+    compression_ratio = 2.0  # bf16 -> fp8
+
+    def __init__(self, device: torch.device | None = None):
+        self.device = device
+
+    def quantize(self, kv_cache: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """kv_cache ``[L, 2, B, H, T, D]`` bf16 -> (codes uint8 same shape, scales ``[L, 2, H]`` fp32)."""
+        if kv_cache.dim() != 6 or kv_cache.shape[1] != 2:
+            raise ValueError("kv_cache must be [L, 2, B, H, T, D]")
+        dev = self.device or ensure_gpu()
+        x = kv_cache.to(dev).contiguous()
+        L, _, B, H, T, D = x.shape
+        codes, scales = kv.fp8_quant_heads(x.view(2 * L, B, H, T * D))
+        return codes.view(x.shape), scales.view(L, 2, H)
+
+    def dequantize(self, codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+        """Inverse of :meth:`quantize` -> bf16 ``[L, 2, B, H, T, D]``."""
+        if codes.dim() != 6 or codes.shape[1] != 2:
+            raise ValueError("codes must be [L, 2, B, H, T, D]")
+        L, _, B, H, T, D = codes.shape
+        y = kv.fp8_dequant_heads(codes.contiguous().view(2 * L, B, H, T * D),
+                                 scales.contiguous().view(2 * L, H))
+        return y.view(codes.shape)
+
+
+class PagedFP8KVCache:
+    """Paged FP8 KV cache with fused quantize+append and gather+dequant."""
+
+    def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, num_pages: int,
+                 page_size: int = 16, device: torch.device | None = None):
+        self.device = device or ensure_gpu()
+        self.L, self.H, self.D, self.P = num_layers, num_kv_heads, head_dim, page_size
+        self.num_pages = num_pages
+        self.pool = torch.zeros((num_layers, num_pages, 2, num_kv_heads, page_size, head_dim),
+                                dtype=torch.uint8, device=self.device)
+        self.scales = torch.ones((num_layers, 2, num_kv_heads), dtype=torch.float32, device=self.device)
+        self.has_scales = False
+        self._free = list(range(num_pages - 1, -1, -1))
+        self.pages: dict = {}    # seq id -> list of page ids
+        self.lengths: dict = {}  # seq id -> tokens stored
+
+    def _reserve(self, seq_id, new_len: int) -> None:
+        pages = self.pages.setdefault(seq_id, [])
+        need = -(-new_len // self.P)
+        while len(pages) < need:
+            if not self._free:
+                raise MemoryError("PagedFP8KVCache: out of pages")
+            pages.append(self._free.pop())
+
+    def _tables(self, seq_ids) -> torch.Tensor:
+        width = max(1, max(len(self.pages.get(s, [])) for s in seq_ids))
+        rows = [self.pages.get(s, []) + [-1] * (width - len(self.pages.get(s, []))) for s in seq_ids]
+        return torch.tensor(rows, dtype=torch.int32).to(self.device)
+
+    def append(self, x: torch.Tensor, seq_ids: list, lengths: list[int], dynamic_scales: bool | None = None):
+        """Append new tokens of several sequences.  x: ``[L, n_tok, 2, H, D]`` bf16, tokens of
+        sequence ``seq_ids[i]`` packed in order with ``lengths[i]`` tokens each.  Scales are
+        computed from this batch on the first append (or when ``dynamic_scales``) and reused
+        otherwise, so earlier pages keep decoding correctly."""
+        if sum(lengths) != x.shape[1]:
+            raise ValueError("sum(lengths) must equal x.shape[1]")
+        start = [self.lengths.get(s, 0) for s in seq_ids]
+        for s, st, n in zip(seq_ids, start, lengths):
+            self._reserve(s, st + n)
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + n)
+        dyn = (not self.has_scales) if dynamic_scales is None else dynamic_scales
+        kv.kv_quant_append(x.to(self.device), torch.tensor(cu, dtype=torch.int32).to(self.device),
+                           self._tables(seq_ids), self.pool, scales=self.scales,
+                           start_pos=torch.tensor(start, dtype=torch.int32).to(self.device),
+                           static_scales=not dyn)
+        self.has_scales = True
+        for s, st, n in zip(seq_ids, start, lengths):
+            self.lengths[s] = st + n
+        return self.scales
+
+    def gather(self, layer: int, seq_ids: list, out_len: int | None = None):
+        """bf16 ``(k, v)``, each ``[B, H, out_len, D]``, of one layer for decode; positions past a
+        sequence's length are zeros."""
+        lens = torch.tensor([self.lengths.get(s, 0) for s in seq_ids], dtype=torch.int32).to(self.device)
+        bt = self._tables(seq_ids)
+        if out_len is None:
+            out_len = max(1, max(self.lengths.get(s, 0) for s in seq_ids))
+        return kv.kv_gather_dequant(self.pool[layer], self.scales[layer].contiguous(), bt, lens, out_len)
+
+    def free(self, seq_id) -> None:
+        for p in self.pages.pop(seq_id, []):
+            self._free.append(p)
+        self.lengths.pop(seq_id, None)
+
+
+__all__ = ["FP8KVQuantizer", "PagedFP8KVCache"]
