@@ -31,8 +31,9 @@
 namespace zx {
 
 constexpr int BS_THREADS = 1024;
-constexpr int BS_IPT = 2;                     // trace positions per thread per window
-constexpr int BS_W = BS_THREADS * BS_IPT;     // window size
+constexpr int BS_IPT = 8;                     // trace positions per thread per window
+constexpr int BS_W = BS_THREADS * BS_IPT;     // largest window
+constexpr int BS_EMAX = 2048;                 // evictions and dynamic candidates per window
 constexpr int BS_BLOCK_BITS = 4096;           // bits per counted block
 constexpr int BS_MAX_BLOCKS = 8192;           // LDS block counters -> at most 2^25 bits
 constexpr int64_t BS_MAX_BITS = (int64_t)BS_MAX_BLOCKS * BS_BLOCK_BITS;
@@ -59,23 +60,8 @@ __device__ __forceinline__ int64_t item_idx(const SimArgs &a, int32_t page, int3
   return nu == ZX_NEVER ? (int64_t)page : (int64_t)a.n_pages + (a.n_total - 1 - nu);
 }
 
-// Byte of a flag array, read through to L2 (other waves of this workgroup wrote it in
-// earlier windows; the per-CU L1 is not kept coherent with those stores).
-__device__ __forceinline__ uint32_t ld_flag(const uint8_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 __device__ __forceinline__ unsigned long long ld_word(const unsigned long long *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void set_bit(const SimArgs &a, uint32_t *cnt, int64_t idx) {
-  atomicOr(&a.bits[idx >> 6], 1ull << (idx & 63));
-  atomicAdd(&cnt[idx / BS_BLOCK_BITS], 1u);
-}
-__device__ __forceinline__ void clear_bit(const SimArgs &a, uint32_t *cnt, int64_t idx) {
-  atomicAnd(&a.bits[idx >> 6], ~(1ull << (idx & 63)));
-  atomicSub(&cnt[idx / BS_BLOCK_BITS], 1u);
 }
 
 // Exclusive block-wide prefix sum of one value per thread; *total receives the sum.
@@ -106,22 +92,67 @@ __device__ __forceinline__ int block_scan(int v, int *total, int *ws /* [BS_THRE
 
 struct SimShared {
   uint32_t cnt[BS_MAX_BLOCKS];
-  int32_t s_idx[BS_W];    // first E set bits (static candidates), in order
-  int32_t d_idx[BS_W];    // dynamic candidates: idx, time (window offset), page
-  int32_t d_t[BS_W];
-  int32_t d_page[BS_W];
-  uint8_t d_taken[BS_W];
-  int32_t ev_t[BS_W];     // eviction events: window offset of the evicting miss
-  int32_t ev_vidx[BS_W];  // victim idx and page per event
-  int32_t ev_vpage[BS_W];
-  uint8_t ev_dyn[BS_W];
-  int32_t blk_list[BS_W];  // blocks holding the first E set bits, and their rank offsets
-  int32_t blk_before[BS_W];
+  int32_t s_idx[BS_EMAX];    // first E set bits (static candidates), in order
+  int32_t d_idx[BS_EMAX];    // dynamic candidates: idx, time (window offset), page
+  int32_t d_t[BS_EMAX];
+  int32_t d_page[BS_EMAX];
+  uint8_t d_taken[BS_EMAX];
+  int32_t ev_t[BS_EMAX];     // eviction events: window offset of the evicting miss
+  int32_t ev_vidx[BS_EMAX];  // victim idx and page per event
+  int32_t ev_vpage[BS_EMAX];
+  uint8_t ev_dyn[BS_EMAX];
+  int32_t blk_list[BS_EMAX];  // blocks holding the first E set bits, and their rank offsets
+  int32_t blk_before[BS_EMAX];
+  int32_t sort_key[BS_EMAX];  // dynamic candidates sorted by idx (key) -> candidate slot
+  int32_t sort_val[BS_EMAX];
+  unsigned long long win_bits[BS_W / 64 + 2];  // words of B covering the window's positions
+  unsigned long long win_clr[BS_W / 64 + 2];   // bits of those words cleared in this window
   int scan_ws[BS_THREADS / 64 + 1];
   int n_list;
+  int n_dyn_victims;
 };
 
-// First E set bits of B (E <= BS_W, at least E bits set) into sh.s_idx.
+// Sorts sh.sort_key[0, n) ascending with sh.sort_val as payload (bitonic; n <= BS_EMAX).
+__device__ void sort_candidates(SimShared &sh, int n) {
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  for (int i = n + threadIdx.x; i < n2; i += BS_THREADS) {
+    sh.sort_key[i] = 0x7FFFFFFF;
+    sh.sort_val[i] = -1;
+  }
+  __syncthreads();
+  for (int k = 2; k <= n2; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n2; i += BS_THREADS) {
+        const int p = i ^ j;
+        if (p > i) {
+          const bool up = (i & k) == 0;
+          const int ki = sh.sort_key[i], kp = sh.sort_key[p];
+          if ((ki > kp) == up) {
+            sh.sort_key[i] = kp;
+            sh.sort_key[p] = ki;
+            const int v = sh.sort_val[i];
+            sh.sort_val[i] = sh.sort_val[p];
+            sh.sort_val[p] = v;
+          }
+        }
+      }
+      __syncthreads();
+    }
+}
+
+// Number of entries of the ascending array a[0, n) that are < x.
+__device__ __forceinline__ int lower_bound(const int32_t *a, int n, int32_t x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] < x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// First E set bits of B (E <= BS_EMAX, at least E bits set) into sh.s_idx.
 __device__ void select_first(const SimArgs &a, SimShared &sh, int E) {
   const int per = (a.nblk + BS_THREADS - 1) / BS_THREADS;
   const int b0 = threadIdx.x * per;
@@ -162,6 +193,13 @@ __device__ void select_first(const SimArgs &a, SimShared &sh, int E) {
   __syncthreads();
 }
 
+// Makes this wave's global stores and atomics complete, then joins the workgroup, so
+// later reads by any wave of the workgroup observe them.
+__device__ __forceinline__ void sync_global() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
 __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
   __shared__ SimShared sh;
   __shared__ int64_t st[4];
@@ -169,89 +207,141 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
   if (threadIdx.x < 4) st[threadIdx.x] = a.state[threadIdx.x];
   __syncthreads();
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t top = (int64_t)a.n_pages + a.n_total - 1;  // idx of position 0
 
   int w_lim = BS_W;
   int64_t t0 = a.t_begin;
   while (t0 < a.t_end) {
     const int w = (int)((a.t_end - t0) < w_lim ? (a.t_end - t0) : w_lim);
     const int64_t t1 = t0 + w;
+    // A page whose first access in the window is at pos is resident iff its key is pos,
+    // i.e. iff bit idx(pos) is set: read the window's bits instead of per-page flags.
+    const int64_t wlo = (top - (t1 - 1)) >> 6, whi = (top - t0) >> 6;
+    for (int64_t q = wlo + threadIdx.x; q <= whi; q += BS_THREADS) {
+      sh.win_bits[q - wlo] = ld_word(&a.bits[q]);
+      sh.win_clr[q - wlo] = 0;
+    }
+    // thread-major items: thread tid owns window offsets [tid * BS_IPT, (tid + 1) * BS_IPT)
     int32_t p[BS_IPT], nu[BS_IPT];
-    bool live[BS_IPT], miss[BS_IPT], hitfirst[BS_IPT], last[BS_IPT];
-    int mcount = 0, hcount = 0;
+    bool first[BS_IPT];
+    const int i0 = threadIdx.x * BS_IPT;
 #pragma unroll
     for (int j = 0; j < BS_IPT; ++j) {
-      const int i = j * BS_THREADS + threadIdx.x;
-      live[j] = i < w;
+      const int i = i0 + j;
       p[j] = 0;
       nu[j] = ZX_NEVER;
-      miss[j] = hitfirst[j] = last[j] = false;
-      if (live[j]) {
-        const int64_t pos = t0 + i;
-        p[j] = a.trace[pos];
-        nu[j] = a.next_use[pos];
-        const bool first = a.prev_use[pos] < t0;
-        last[j] = nu[j] == ZX_NEVER || nu[j] >= t1;
-        if (first) {
-          const bool res = ld_flag(a.resident + p[j]) != 0;
-          miss[j] = !res;
-          hitfirst[j] = res;
-        }
+      first[j] = false;
+      if (i < w) {
+        p[j] = a.trace[t0 + i];
+        nu[j] = a.next_use[t0 + i];
+        first[j] = a.prev_use[t0 + i] < t0;
       }
-      mcount += miss[j];
-      hcount += hitfirst[j];
     }
-    // miss ranks in trace order (positions j * BS_THREADS + tid)
-    int m_rank[BS_IPT];
-    int M = 0;
+    __syncthreads();
+    uint32_t missm = 0, hitm = 0, lastm = 0;  // bit j: item j
+    int mc = 0, hc = 0;
 #pragma unroll
     for (int j = 0; j < BS_IPT; ++j) {
-      int tot;
-      m_rank[j] = M + block_scan(miss[j] ? 1 : 0, &tot, sh.scan_ws);
-      M += tot;
+      const int i = i0 + j;
+      if (i >= w) continue;
+      if (nu[j] == ZX_NEVER || nu[j] >= t1) lastm |= 1u << j;
+      if (first[j]) {
+        const int64_t idx = top - (t0 + i);
+        const bool res = (sh.win_bits[(idx >> 6) - wlo] >> (idx & 63)) & 1ull;
+        if (res) {
+          hitm |= 1u << j;
+          ++hc;
+        } else {
+          missm |= 1u << j;
+          ++mc;
+        }
+      }
     }
-    int Hf;
-    block_scan(hcount, &Hf, sh.scan_ws);
+    int tot;
+    const int pre = block_scan(mc | (hc << 16), &tot, sh.scan_ws);
+    const int m_base = pre & 0xFFFF, M = tot & 0xFFFF, Hf = tot >> 16;
     const int64_t count0 = st[0];
     const int64_t F = a.capacity - count0 > 0 ? a.capacity - count0 : 0;
     const int E = M > F ? (int)(M - F) : 0;
-    if (E > 0 && count0 - Hf < E) {  // not enough statics: smaller window
+    if (E > 0 && (count0 - Hf < E || E > BS_EMAX)) {  // not enough statics, or too many victims
       w_lim = w > 1 ? w / 2 : 1;
       continue;
     }
-    w_lim = w_lim < BS_W ? w_lim * 2 : BS_W;
 
-    int dpos[BS_IPT];
-#pragma unroll
-    for (int j = 0; j < BS_IPT; ++j) dpos[j] = -1;
+    uint32_t takenm = 0;  // bit j: item j's dynamic candidate was evicted
+    int dbase = 0;
     if (E > 0) {
       select_first(a, sh, E);
       const int32_t worst = sh.s_idx[E - 1];
       // dynamic candidates that can beat a needed static, in trace order
-      int nd = 0;
+      uint32_t candm = 0;
+      int dc = 0;
+#pragma unroll
+      for (int j = 0; j < BS_IPT; ++j)
+        if (((lastm >> j) & 1) && item_idx(a, p[j], nu[j]) < worst) {
+          candm |= 1u << j;
+          ++dc;
+        }
+      int nd;
+      dbase = block_scan(dc, &nd, sh.scan_ws);
+      if (nd > BS_EMAX) {
+        w_lim = w > 1 ? w / 2 : 1;
+        continue;
+      }
+      int r = dbase, mr = m_base;
 #pragma unroll
       for (int j = 0; j < BS_IPT; ++j) {
-        const bool cand = last[j] && item_idx(a, p[j], nu[j]) < worst;
-        int tot;
-        const int r = nd + block_scan(cand ? 1 : 0, &tot, sh.scan_ws);
-        if (cand) {
+        if ((candm >> j) & 1) {
           sh.d_idx[r] = (int32_t)item_idx(a, p[j], nu[j]);
-          sh.d_t[r] = j * BS_THREADS + threadIdx.x;
+          sh.d_t[r] = i0 + j;
           sh.d_page[r] = p[j];
           sh.d_taken[r] = 0;
-          dpos[j] = r;
+          ++r;
         }
-        nd += tot;
-        if (miss[j] && m_rank[j] >= F) sh.ev_t[m_rank[j] - F] = j * BS_THREADS + threadIdx.x;
+        if ((missm >> j) & 1) {
+          if (mr >= F) sh.ev_t[mr - F] = i0 + j;
+          ++mr;
+        }
       }
       __syncthreads();
+      if (threadIdx.x == 0) sh.n_dyn_victims = 0;
       if (nd == 0) {  // no dynamic candidate can beat a needed static: victims in order
         for (int k = threadIdx.x; k < E; k += BS_THREADS) {
           const int32_t sidx = sh.s_idx[k];
           sh.ev_vidx[k] = sidx;
-          sh.ev_vpage[k] = sidx < a.n_pages ? sidx : a.trace[a.n_total - 1 - ((int64_t)sidx - a.n_pages)];
+          sh.ev_vpage[k] = sidx < a.n_pages ? sidx : a.trace[top - sidx];
           sh.ev_dyn[k] = 0;
         }
-      } else if (wid == 0) {
+      } else if (sh.d_t[nd - 1] < sh.ev_t[0]) {
+        // Every dynamic candidate exists before the first eviction, so the victims are the
+        // E best of (dynamic candidates U statics): merge the two sorted lists by rank.
+        for (int q = threadIdx.x; q < nd; q += BS_THREADS) {
+          sh.sort_key[q] = sh.d_idx[q];
+          sh.sort_val[q] = q;
+        }
+        __syncthreads();
+        sort_candidates(sh, nd);
+        for (int q = threadIdx.x; q < nd; q += BS_THREADS) {
+          const int rank = q + lower_bound(sh.s_idx, E, sh.sort_key[q]);
+          if (rank < E) {
+            const int slot = sh.sort_val[q];
+            sh.ev_vidx[rank] = sh.sort_key[q];
+            sh.ev_vpage[rank] = sh.d_page[slot];
+            sh.ev_dyn[rank] = 1;
+            sh.d_taken[slot] = 1;
+            atomicAdd(&sh.n_dyn_victims, 1);
+          }
+        }
+        for (int k = threadIdx.x; k < E; k += BS_THREADS) {
+          const int32_t sidx = sh.s_idx[k];
+          const int rank = k + lower_bound(sh.sort_key, nd, sidx);
+          if (rank < E) {
+            sh.ev_vidx[rank] = sidx;
+            sh.ev_vpage[rank] = sidx < a.n_pages ? sidx : a.trace[top - sidx];
+            sh.ev_dyn[rank] = 0;
+          }
+        }
+      } else if (wid == 0) {  // candidates appear between evictions: one eviction at a time
         int sp = 0;
         for (int k = 0; k < E; ++k) {
           const int tau = sh.ev_t[k];
@@ -268,63 +358,115 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
               bj = oj;
             }
           }
+          const int32_t sidx = sh.s_idx[sp];
+          const bool dyn = bj >= 0 && best < sidx;
           if (lane == 0) {
-            const int32_t sidx = sh.s_idx[sp];
-            if (bj >= 0 && best < sidx) {
+            if (dyn) {
               sh.ev_vidx[k] = best;
               sh.ev_vpage[k] = sh.d_page[bj];
               sh.ev_dyn[k] = 1;
               sh.d_taken[bj] = 1;
+              ++sh.n_dyn_victims;
             } else {
               sh.ev_vidx[k] = sidx;
-              sh.ev_vpage[k] = sidx < a.n_pages ? sidx : a.trace[a.n_total - 1 - ((int64_t)sidx - a.n_pages)];
+              sh.ev_vpage[k] = sidx < a.n_pages ? sidx : a.trace[top - sidx];
               sh.ev_dyn[k] = 0;
             }
           }
-          if (!(bj >= 0 && best < sh.s_idx[sp])) ++sp;
+          if (!dyn) ++sp;
           __builtin_amdgcn_wave_barrier();
         }
       }
       __syncthreads();
+      int rr = dbase;
+#pragma unroll
+      for (int j = 0; j < BS_IPT; ++j)
+        if ((candm >> j) & 1) {
+          if (sh.d_taken[rr]) takenm |= 1u << j;
+          ++rr;
+        }
     }
-    // admissions and hits on pages resident since before the window
+    w_lim = w_lim < BS_W ? w_lim * 2 : BS_W;
+    // admissions, and hits on pages resident since before the window (their bits are
+    // cleared in the LDS copy first, then one atomic per word)
 #pragma unroll
     for (int j = 0; j < BS_IPT; ++j) {
-      if (!live[j]) continue;
-      const int64_t pos = t0 + j * BS_THREADS + threadIdx.x;
-      if (miss[j]) a.resident[p[j]] = 1;
-      if (hitfirst[j]) clear_bit(a, sh.cnt, item_idx(a, p[j], (int32_t)pos));
-      if (a.miss_flags) a.miss_flags[pos] = miss[j] ? 1 : 0;
+      const int i = i0 + j;
+      if (i >= w) continue;
+      if ((missm >> j) & 1) a.resident[p[j]] = 1;
+      if ((hitm >> j) & 1) {
+        const int64_t idx = top - (t0 + i);
+        atomicOr(&sh.win_clr[(idx >> 6) - wlo], 1ull << (idx & 63));
+        atomicSub(&sh.cnt[idx / BS_BLOCK_BITS], 1u);
+      }
+      if (a.miss_flags) a.miss_flags[t0 + i] = (missm >> j) & 1;
     }
     __syncthreads();
-    // evictions
+    for (int64_t q = wlo + threadIdx.x; q <= whi; q += BS_THREADS) {
+      const unsigned long long c = sh.win_clr[q - wlo];
+      if (c) atomicAnd(&a.bits[q], ~c);
+    }
+    // evictions: records, residency, and the static victims' bits -- those are exactly
+    // the first sp set bits of B, so every word up to the last one is cleared with a
+    // single atomic
     const int64_t ev0 = st[1];
+    const int sp = E - (E > 0 ? sh.n_dyn_victims : 0);
     for (int k = threadIdx.x; k < E; k += BS_THREADS) {
       const int32_t page = sh.ev_vpage[k];
       a.resident[page] = 0;
-      if (!sh.ev_dyn[k]) clear_bit(a, sh.cnt, sh.ev_vidx[k]);
       if (ev0 + k < a.evict_cap) {
         a.evict_pos[ev0 + k] = (int32_t)(t0 + sh.ev_t[k]);
         a.evict_page[ev0 + k] = page;
       }
     }
-    __syncthreads();
-    // pages still resident after their last access in the window get their new key
-#pragma unroll
-    for (int j = 0; j < BS_IPT; ++j) {
-      if (!live[j] || !last[j]) continue;
-      if (dpos[j] >= 0 && sh.d_taken[dpos[j]]) continue;
-      set_bit(a, sh.cnt, item_idx(a, p[j], nu[j]));
-      a.key[p[j]] = nu[j];
+    if (sp > 0) {
+      const int64_t bound = sh.s_idx[sp - 1];
+      for (int li = wid; li < sh.n_list; li += BS_THREADS / 64) {
+        if (sh.blk_before[li] >= sp) continue;
+        const int b = sh.blk_list[li];
+        const int64_t q = (int64_t)b * (BS_BLOCK_BITS / 64) + lane;
+        const int64_t lo = q * 64;
+        unsigned long long mask = 0;
+        if (lo <= bound && lo < a.nbits) mask = lo + 63 <= bound ? ~0ull : ((2ull << (bound - lo)) - 1);
+        int removed = 0;
+        if (mask) removed = __popcll(atomicAnd(&a.bits[q], ~mask) & mask);
+        for (int off = 32; off >= 1; off >>= 1) removed += __shfl_xor(removed, off, 64);
+        if (lane == 0 && removed) atomicSub(&sh.cnt[b], (uint32_t)removed);
+      }
     }
-    __syncthreads();
+    sync_global();
+    // pages still resident after their last access in the window get their new key; a
+    // thread's consecutive items often share a word, so their bits go out together
+    {
+      int64_t cur_w = -1;
+      unsigned long long cur_m = 0;
+#pragma unroll
+      for (int j = 0; j < BS_IPT; ++j) {
+        if (!((lastm >> j) & 1) || ((takenm >> j) & 1)) continue;
+        const int64_t idx = item_idx(a, p[j], nu[j]);
+        a.key[p[j]] = nu[j];
+        if ((idx >> 6) != cur_w) {
+          if (cur_w >= 0) {
+            atomicOr(&a.bits[cur_w], cur_m);
+            atomicAdd(&sh.cnt[(cur_w * 64) / BS_BLOCK_BITS], (uint32_t)__popcll(cur_m));
+          }
+          cur_w = idx >> 6;
+          cur_m = 0;
+        }
+        cur_m |= 1ull << (idx & 63);
+      }
+      if (cur_w >= 0) {
+        atomicOr(&a.bits[cur_w], cur_m);
+        atomicAdd(&sh.cnt[(cur_w * 64) / BS_BLOCK_BITS], (uint32_t)__popcll(cur_m));
+      }
+    }
     if (threadIdx.x == 0) {
       st[0] = count0 + M - E;
       st[1] = ev0 + E;
       st[2] += M;
       st[3] += w - M;
     }
-    __syncthreads();
+    sync_global();
     t0 = t1;
   }
   if (threadIdx.x < 4) a.state[threadIdx.x] = st[threadIdx.x];

@@ -128,6 +128,9 @@ class BeladyKVCacheTieringManager:
         concurrently.  Returns bytes moved and times."""
         dev = self.device or N.ensure_gpu()
         d2h, h2d = self.transfers(t_begin, t_end)
+        # batch the window's moves in page order: adjacent pages have adjacent slots on both
+        # sides, so zx_tier_copy_runs merges them into few large copies
+        d2h, h2d = np.sort(d2h), np.sort(h2d)
         pages = np.unique(np.concatenate([d2h, h2d]))
         slots = len(pages) if max_pool_pages is None else min(len(pages), max_pool_pages)
         slots = max(slots, 1)
