@@ -6,12 +6,13 @@ U[1k, 8k] tokens, 5% of each sequence's (layer, head) pairs x50), one step = one
 of every layer, inputs already resident in HBM.  Reported as algorithmic GB/s
 (3 bytes per KV element + scales + block tables) and as a fraction of the 8 TB/s HBM3E
 peak.  Also measured: configs[2] (paged gather + dequant, 64 x 32k decode, 300k-page
-pool) and, when built, configs[3] (Belady tiering trace).
+pool) and configs[3] (Belady tiering of a ring-attention trace: evictions/s, plus the
+pinned-host tier moves of one layer overlapped with compute).
 
 The CPU baseline is the C oracle (oracle/zx_oracle.c, one thread) timed on a bounded
 sample of the same workload on this machine's host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only append|gather]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only append|gather|belady|copy]
 """
 from __future__ import annotations
 
@@ -23,6 +24,10 @@ import time
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "KV quant+append & gather+dequant GB/s (% HBM peak); evictions/sec"
+# HBM bytes per launch of the dominant kernel, measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE and scaled by the same counters on a plain 4 GiB copy (profiles/*.md); keyed by
+# (workload, seed) because the append's size depends on the seed.
+MEASURED_TRAFFIC = {("append", 1): 14_824_469_511, ("gather", 2): 12_889_157_804}
 
 
 def parse():
@@ -31,7 +36,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
-    ap.add_argument("--only", choices=["append", "gather", "belady", "all"], default="all")
+    ap.add_argument("--only", choices=["append", "gather", "belady", "copy", "all"], default="all")
     ap.add_argument("--seed", type=int, default=1)
     return ap.parse_args()
 
@@ -257,6 +262,17 @@ def main():
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
            "data": "synthetic (seeded N(0,1) bf16 KV, random page tables)"}
 
+    if args.only == "copy":
+        # Counter calibration: one plain device-to-device copy of exactly 4 GiB per step, so
+        # rocprofv3's FETCH_SIZE / WRITE_SIZE per dispatch can be compared with known bytes.
+        src = torch.randint(0, 255, (4 << 30,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        ms_c, _, _ = time_steps(torch, lambda: dst.copy_(src), args.steps, args.warmup)
+        out.update({"value": round(2 * src.numel() / (ms_c * 1e-3) / 1e9, 2), "ms_per_step": round(ms_c, 4),
+                    "config": {"workload": "calibration: torch copy_ of 4 GiB (4 GiB read + 4 GiB written)"}})
+        print(json.dumps(out), flush=True)
+        return
+
     if args.only in ("append", "all"):
         log("building configs[1] append workload")
         W = make_append_workload(torch, dev, seed=args.seed)
@@ -276,8 +292,10 @@ def main():
                        "n_tok": W["T"], "elements": W["N"], "n_pages_per_layer": W["n_pages"],
                        "algorithmic_bytes_per_step": W["alg_bytes"], "seed": args.seed},
             "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                         "kernel": "zx_kv_quant_append (all kernels of one append, HIP events)"},
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                         "traffic": MEASURED_TRAFFIC.get(("append", args.seed)),
+                         "kernel": "kv_append_fused_kernel (HIP events around the whole zx_kv_quant_append "
+                                   "call: token offsets + fills + the fused kernel)"},
         })
         if not args.skip_cpu:
             log("CPU baseline (append)")
@@ -299,6 +317,7 @@ def main():
         gb_g = G["alg_bytes"] / (ms_g * 1e-3) / 1e9
         log(f"gather: {ms_g:.3f} ms/step, {gb_g:.1f} GB/s ({100 * gb_g / HBM_PEAK_GBPS:.1f}% of peak)")
         gather = {"GBps": round(gb_g, 2), "ms_per_step": round(ms_g, 4), "frac": round(gb_g / HBM_PEAK_GBPS, 4),
+                  "traffic": MEASURED_TRAFFIC.get(("gather", 2)),
                   "workload": "configs[2]: paged gather + dequant, 64 seqs x 32768, 300k-page pool, one layer K+V",
                   "algorithmic_bytes_per_step": G["alg_bytes"]}
         if not args.skip_cpu:

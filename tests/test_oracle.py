@@ -295,6 +295,38 @@ def test_belady_heap_matches_linear_scan_larger(seed):
     assert [tuple(map(int, e)) for e in zip(ep, eg)] == O.ref_belady_trace(trace, cap)
 
 
+def test_belady_argmax_matches_lexsort():
+    """belady.py:44-50 semantics (largest key > -1 among residents; ties to the smallest
+    slot) against numpy's lexsort on random inputs with many ties and negative keys."""
+    rng = np.random.default_rng(11)
+    for n in (1, 5, 64, 1000):
+        for _ in range(20):
+            keys = rng.integers(-3, 6, n).astype(np.int64)
+            res = (rng.random(n) < 0.5).astype(np.uint8)
+            ok = np.nonzero((res == 1) & (keys > -1))[0]
+            if ok.size == 0:
+                want = (-1, -1)
+            else:
+                order = np.lexsort((ok, -keys[ok]))  # key descending, then slot ascending
+                want = (int(ok[order[0]]), int(keys[ok[order[0]]]))
+            assert O.belady_argmax(keys, res) == want
+
+
+def test_next_use_matches_dictionary_scan():
+    rng = np.random.default_rng(12)
+    trace = rng.integers(0, 37, 5000).astype(np.int32)
+    nu, pu = O.next_use(trace, 37)
+    last, nxt = {}, [O.NEVER] * len(trace)
+    for i in range(len(trace) - 1, -1, -1):
+        nxt[i] = last.get(int(trace[i]), O.NEVER)
+        last[int(trace[i])] = i
+    prv, seen = [-1] * len(trace), {}
+    for i, p in enumerate(trace.tolist()):
+        prv[i] = seen.get(p, -1)
+        seen[p] = i
+    assert nu.tolist() == nxt and pu.tolist() == prv
+
+
 def test_next_use_closed_form():
     trace = np.array([3, 1, 3, 3, 0, 1], np.int32)
     nu, pu = O.next_use(trace, 4)
