@@ -116,8 +116,10 @@ size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32
 
 /* Paged append with fused FP8 quantisation.  Without
  * ZX_APPEND_STATIC_SCALES the scales are computed from this batch (amax over all
- * of its tokens) and written to `scales`.  Rows whose page id is out of range are
- * skipped and flagged in *err (device int32, may be NULL). */
+ * of its tokens) and written to `scales`.  Static scales may be normal fp32 numbers of
+ * either sign, +-inf (treated as +inf) or NaN; zero and subnormal static scales are
+ * outside the contract (dynamic scales are always >= 1e-8/448).  Rows whose page id is
+ * out of range are skipped and flagged in *err (device int32, may be NULL). */
 int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
                        int64_t n_tok, int32_t n_heads, int32_t head_dim,
                        const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,

@@ -222,6 +222,74 @@ def test_kv_quant_append_fused_and_two_pass_bit_exact(dev, two_pass, L, H, D, P,
     np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
 
 
+@pytest.mark.parametrize("two_pass", [False, True])
+def test_kv_quant_append_special_slabs(dev, two_pass):
+    """Slabs whose scale is clamped (all zero), +inf (holds +-inf), NaN (holds NaNs of both
+    signs), and subnormal inputs, through the single-pass and the two-pass kernels."""
+    L, H, D, P = 3, 4, 128, 16
+    lens = [5, 40, 300, 77]
+    x, cu, bt, n_pages, _ = make_append_case(L, H, D, P, lens, seed=21)
+    x[0, :, 0, 0] = 0.0
+    x[1, 7, 1, 1, 3] = float("inf")
+    x[1, 100, 1, 1, 9] = -float("inf")
+    xi = x.view(torch.int16)
+    xi[2, 50, 0, 2, 11] = 0x7FC1
+    xi[2, 51, 0, 2, 12] = -63  # 0xFFC1, a negative NaN
+    x[2, :, 1, 3] = (torch.arange(x.shape[1] * D, dtype=torch.float32).reshape(-1, D) % 97 - 48) * 2.0 ** -133
+    pool = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8)
+    wpool = pool.numpy().copy()
+    wsc, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, P)
+    assert werr == 0
+    assert np.isinf(wsc[1, 1, 1]) and np.isnan(wsc[2, 0, 2])
+    pool_d = pool.to(dev)
+    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+    np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
+
+
+def test_kv_quant_append_static_special_scales(dev):
+    """Given scales of both signs, +-inf and NaN (inputs include +-inf)."""
+    L, H, D, P = 1, 4, 64, 16
+    lens = [33, 64]
+    x, cu, bt, n_pages, _ = make_append_case(L, H, D, P, lens, seed=22)
+    x[0, 3, 0, 1, 5] = float("inf")
+    x[0, 4, 1, 2, 6] = -float("inf")
+    scales = torch.tensor([[[0.02, -0.03, float("inf"), float("nan")],
+                            [-float("inf"), 0.5, 1e-3, -7.0]]], dtype=torch.float32)
+    pool = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8)
+    wpool = pool.numpy().copy()
+    _, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, P, scales=scales.numpy())
+    assert werr == 0
+    pool_d = pool.to(dev)
+    kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, scales=scales.to(dev), static_scales=True,
+                       check=True)
+    np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
+
+
+@pytest.mark.parametrize("two_pass", [False, True])
+def test_kv_quant_append_pool_layer_over_2gib(dev, two_pass):
+    """A pool layer of 2.3 GB (70,000 pages of 32 KiB): pages past 2 GiB take the 64-bit
+    store path.  The oracle runs on a compact pool with the same pages renumbered."""
+    L, H, D, P = 1, 8, 128, 16
+    lens = [100, 37, 250]
+    x, cu, bt_small, n_small, _ = make_append_case(L, H, D, P, lens, seed=23, extra_pages=0)
+    n_big = 70_000
+    g = torch.Generator().manual_seed(24)
+    big_ids = (n_big - 1 - torch.randperm(4000, generator=g)[:n_small]).to(torch.int32)  # > 2 GiB offsets
+    bt_big = torch.where(bt_small >= 0, big_ids[bt_small.clamp(min=0).long()], bt_small)
+    wpool = np.zeros((L, n_small, 2, H, P, D), np.uint8)
+    wsc, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt_small.numpy(), wpool, P)
+    assert werr == 0
+    pool_d = torch.zeros((L, n_big, 2, H, P, D), dtype=torch.uint8, device=dev)
+    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt_big.to(dev), pool_d, check=True, two_pass=two_pass)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+    got = pool_d[:, big_ids.long().to(dev)].cpu().numpy()
+    np.testing.assert_array_equal(got, wpool)
+    touched = int(pool_d[:, big_ids.long().to(dev)].sum(dtype=torch.int64))
+    assert int(pool_d.sum(dtype=torch.int64)) == touched  # nothing written elsewhere
+    del pool_d
+
+
 def test_kv_quant_append_repeated_calls_reset_state(dev):
     """The single-pass kernel's counters live in the per-call workspace and start at zero:
     two appends in a row (second one smaller) both match the oracle."""

@@ -18,6 +18,8 @@
 // registers hold are re-read from memory (both for the max and for the encode).
 // Every wait is bounded in wall time; a timeout raises a global abort flag that
 // releases every other waiter, so all waves always exit.
+#include <type_traits>
+
 #include "zx_internal.h"
 
 namespace zx {
@@ -65,23 +67,32 @@ __device__ __forceinline__ uint32_t ld_lds(const uint32_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-__device__ __forceinline__ void nt_store8(uint8_t *p, uint2 v) {
-  typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-  v2u w = {v.x, v.y};
-  __builtin_nontemporal_store(w, reinterpret_cast<v2u *>(p));
+// Buffer resources (raw, stride 0) let the hardware drop what a lane must not touch: a
+// load whose offset is at or past num_records returns zeros, such a store is discarded.
+// Lanes past the share, and rows without a page, get offset FA_OOB; a padding step
+// stores through a resource with num_records = 0.
+constexpr uint32_t FA_OOB = 0x80000000u;
+constexpr int FA_RANGE = 0x7FFFFFF0;  // num_records of a live resource (offsets < 2^31 - 16)
+typedef unsigned int zx_v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int zx_v2u __attribute__((ext_vector_type(2)));
+constexpr int FA_NT = 2;  // cache policy: nontemporal (each byte is moved exactly once)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, int num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, num_records, 0x00020000);
 }
 
 // Per-thread constants of the register part.  Vector k of a data thread is index
 // v = k * FA_DATA_THREADS + tid of the share (token v >> vpt_log2, 16-byte chunk
-// v & mask).  dst[k] is the offset of its 8 codes inside a layer's pool minus the slab
-// term, or -1 (the store then goes to a dummy workspace slot).  Lanes past the share
-// read the share's first vector (always valid) and leave it out of the max.  Keeping
-// the data path free of per-lane branches lets the compiler count outstanding loads
-// exactly (s_waitcnt vmcnt(N) instead of vmcnt(0)), so later slabs' loads stay in flight.
-template <int K> struct ThreadMap {
-  int64_t dst[K];
-  uint32_t live;  // bit k: vector k is part of the share
-  int nreg;       // vectors of the share held in registers (whole workgroup)
+// v & mask).  src[k] is its byte offset from the share's first row (FA_OOB past the
+// share); dst[k] is the offset of its 8 codes inside a layer's pool minus the slab term
+// (FA_OOB, or -1 when WIDE, for a row without a page).  WIDE pools (a layer of 2 GiB or
+// more) store through 64-bit addresses, a row without a page then writes a dummy
+// workspace slot.  The data path has no per-lane branch, so the compiler counts
+// outstanding loads exactly (s_waitcnt vmcnt(N) instead of vmcnt(0)) and later slabs'
+// loads stay in flight.
+template <int K, bool WIDE> struct ThreadMap {
+  uint32_t src[K];
+  typename std::conditional<WIDE, int64_t, uint32_t>::type dst[K];
+  int nreg;  // vectors of the share held in registers (whole workgroup)
 };
 
 __device__ __forceinline__ int64_t vec_src(const FusedArgs &a, int v) {
@@ -101,52 +112,60 @@ __device__ __forceinline__ uint8_t *slab_dst(const FusedArgs &a, int s) {
   return a.pool + (int64_t)l * a.pool_layer_stride + (int64_t)j * a.page_size * a.head_dim;
 }
 
-template <int K>
-__device__ __forceinline__ void load_share(const FusedArgs &a, const ThreadMap<K> &m, int s, int64_t t_base,
+template <int K, bool WIDE>
+__device__ __forceinline__ void load_share(const FusedArgs &a, const ThreadMap<K, WIDE> &m, int s, int64_t t_base,
                                            uint4 (&r)[K]) {
-  const char *base = slab_src(a, s, t_base);
+  const __amdgpu_buffer_rsrc_t rs = rsrc(slab_src(a, s, t_base), FA_RANGE);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const int v = k * FA_DATA_THREADS + (int)threadIdx.x;
-    // nontemporal: the input is read exactly once (2% faster at configs[1] on MI355X)
-    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-    const v4u q = __builtin_nontemporal_load(
-        reinterpret_cast<const v4u *>(base + ((m.live >> k) & 1 ? vec_src(a, v) : 0)));
+    const zx_v4u q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)m.src[k], 0, FA_NT);
     r[k] = make_uint4(q.x, q.y, q.z, q.w);
   }
 }
 
-template <int K, bool SPILL>
-__device__ __forceinline__ uint32_t share_max(const FusedArgs &a, const ThreadMap<K> &m, int s, int64_t t_lo,
+template <int K, bool SPILL, bool WIDE>
+__device__ __forceinline__ uint32_t share_max(const FusedArgs &a, const ThreadMap<K, WIDE> &m, int s, int64_t t_lo,
                                               int nv, const uint4 (&r)[K]) {
-  uint32_t mx = 0;
+  uint32_t mx = 0;  // two packed 16-bit maxes; lanes past the share loaded zeros
 #pragma unroll
-  for (int k = 0; k < K; ++k) mx = max(mx, (m.live >> k) & 1 ? absmax8(r[k]) : 0u);
+  for (int k = 0; k < K; ++k) mx = absmax_acc(mx, r[k]);
   if (SPILL && nv > m.nreg) {
     const char *base = slab_src(a, s, t_lo);
     for (int v = m.nreg + threadIdx.x; v < nv; v += FA_DATA_THREADS)
-      mx = max(mx, absmax8(*reinterpret_cast<const uint4 *>(base + vec_src(a, v))));
+      mx = absmax_acc(mx, *reinterpret_cast<const uint4 *>(base + vec_src(a, v)));
   }
-  return mx;
+  return fold16(mx);
 }
 
-// dst: the slab's base in the pool, or nullptr for a padding step (every store then
-// goes to the dummy slot).
-template <int K, bool SPILL>
-__device__ __forceinline__ void encode_share(const FusedArgs &a, const ThreadMap<K> &m, int s, int64_t t_lo,
+__device__ __forceinline__ void nt_store8(uint8_t *p, uint2 v) {
+  zx_v2u w = {v.x, v.y};
+  __builtin_nontemporal_store(w, reinterpret_cast<zx_v2u *>(p));
+}
+
+// dst: the slab's base in the pool, or nullptr for a padding step (nothing is stored).
+template <int K, bool SPILL, bool WIDE>
+__device__ __forceinline__ void encode_share(const FusedArgs &a, const ThreadMap<K, WIDE> &m, int s, int64_t t_lo,
                                              int nv, const uint4 (&r)[K], float sc, uint8_t *dst,
                                              uint8_t *dummy) {
-  const int mode = scale_mode(sc);
-  const float rcp = 1.0f / sc;
+  const QuantScale q = quant_scale(sc);
+  if constexpr (WIDE) {
 #pragma unroll
-  for (int k = 0; k < K; ++k)
-    nt_store8(dst && m.dst[k] >= 0 ? dst + m.dst[k] : dummy, quant8(r[k], sc, rcp, mode));
+    for (int k = 0; k < K; ++k) nt_store8(dst && m.dst[k] >= 0 ? dst + m.dst[k] : dummy, quant8(r[k], q));
+  } else {
+    const __amdgpu_buffer_rsrc_t rd = rsrc(dst ? dst : a.pool, dst ? FA_RANGE : 0);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const uint2 c = quant8(r[k], q);
+      const zx_v2u w = {c.x, c.y};
+      __builtin_amdgcn_raw_buffer_store_b64(w, rd, (int)m.dst[k], 0, FA_NT);
+    }
+  }
   if (SPILL && dst && nv > m.nreg) {
     const char *base = slab_src(a, s, t_lo);
     for (int v = m.nreg + threadIdx.x; v < nv; v += FA_DATA_THREADS) {
       const int64_t off = a.tok_off[t_lo + (v >> a.vpt_log2)];
-      const uint4 q = *reinterpret_cast<const uint4 *>(base + vec_src(a, v));
-      if (off >= 0) nt_store8(dst + off + (v & ((1 << a.vpt_log2) - 1)) * 8, quant8(q, sc, rcp, mode));
+      const uint4 x = *reinterpret_cast<const uint4 *>(base + vec_src(a, v));
+      if (off >= 0) nt_store8(dst + off + (v & ((1 << a.vpt_log2) - 1)) * 8, quant8(x, q));
     }
   }
 }
@@ -246,7 +265,7 @@ __device__ __forceinline__ bool control_loop(const FusedArgs &a, FusedShared &sh
 // (the data waves run NB - 1 slabs ahead of the oldest unresolved one).
 // SPILL: some share holds more vectors than the registers (extra loops re-read them);
 // without it the data path is straight-line code between waits.
-template <int K, int NB, bool SPILL>
+template <int K, int NB, bool SPILL, bool WIDE>
 __global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArgs a) {
   static_assert(NB + 1 <= FA_SLOTS, "slot ring too small");
   __shared__ FusedShared sh;
@@ -272,18 +291,19 @@ __global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArg
     return;
   }
 
-  ThreadMap<K> m;
+  ThreadMap<K, WIDE> m;
   m.nreg = nv < K * FA_DATA_THREADS ? nv : K * FA_DATA_THREADS;
-  m.live = 0;
-  // a workgroup with an empty share reads token 0 of the slab (valid: n_tok >= 1)
+  // a workgroup with an empty share bases its (all out-of-range) loads at token 0
   const int64_t t_base = nv > 0 ? t_lo : 0;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int v = k * FA_DATA_THREADS + threadIdx.x;
     const bool live = v < m.nreg;
-    m.live |= (uint32_t)live << k;
+    m.src[k] = live ? (uint32_t)vec_src(a, v) : FA_OOB;
     const int64_t off = live ? a.tok_off[t_lo + (v >> a.vpt_log2)] : -1;
-    m.dst[k] = off < 0 ? -1 : off + (v & ((1 << a.vpt_log2) - 1)) * 8;
+    const int64_t d = off < 0 ? -1 : off + (v & ((1 << a.vpt_log2) - 1)) * 8;
+    if constexpr (WIDE) m.dst[k] = d;
+    else m.dst[k] = d < 0 ? FA_OOB : (uint32_t)d;
   }
   uint8_t *dummy = reinterpret_cast<uint8_t *>(a.abort_flag) + 64 + 8 * (threadIdx.x & 15);
 
@@ -292,25 +312,30 @@ __global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArg
   auto clamp = [&](int s) { return s < S ? s : S - 1; };
   uint4 buf[NB][K];
 #pragma unroll
-  for (int i = 0; i < NB; ++i) load_share<K>(a, m, clamp(i), t_base, buf[i]);
+  for (int i = 0; i < NB; ++i) load_share<K, WIDE>(a, m, clamp(i), t_base, buf[i]);
 #pragma unroll
-  for (int i = 0; i + 1 < NB; ++i) contribute(sh, i, share_max<K, SPILL>(a, m, clamp(i), t_lo, nv, buf[i]), i < S);
+  for (int i = 0; i + 1 < NB; ++i)
+    contribute(sh, i, share_max<K, SPILL, WIDE>(a, m, clamp(i), t_lo, nv, buf[i]), i < S);
 
-  // step s (buffer i = s % NB): encode s, refill the buffer with s + NB, reduce s + NB - 1.
-  // The slab count is padded to a multiple of NB so every unrolled step is unconditional
-  // (padded steps encode into the dummy slot; the control wave marks them ready at the
-  // end); an aborted wait leaves the kernel directly.
+  // step s (buffer i = s % NB): reduce s + NB - 1 (loaded during step s - 1), wait for
+  // slab s's scale, encode s, refill the buffer with s + NB.  Reducing first hands the
+  // max to the control wave before this wave blocks on a scale, so the device-wide round
+  // trip of slab s + NB - 1 starts as early as its data allows.  The slab count is padded
+  // to a multiple of NB so every unrolled step is unconditional (padded steps encode into
+  // the dummy slot; the control wave marks them ready at the end); an aborted wait leaves
+  // the kernel directly.
   const int S_pad = (int)ceil_div(S, NB) * NB;
   for (int s0 = 0; s0 < S_pad; s0 += NB) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int s = s0 + i;
+      const int j = (i + NB - 1) % NB;  // constant after unrolling
+      contribute(sh, s + NB - 1, share_max<K, SPILL, WIDE>(a, m, clamp(s + NB - 1), t_lo, nv, buf[j]),
+                 s + NB - 1 < S);
       float sc;
       if (!wait_ready(sh, s, sc)) return;
-      encode_share<K, SPILL>(a, m, s, t_lo, nv, buf[i], sc, s < S ? slab_dst(a, s) : nullptr, dummy);
-      load_share<K>(a, m, clamp(s + NB), t_base, buf[i]);
-      const int j = (i + NB - 1) % NB;  // constant after unrolling
-      contribute(sh, s + NB - 1, share_max<K, SPILL>(a, m, clamp(s + NB - 1), t_lo, nv, buf[j]), s + NB - 1 < S);
+      encode_share<K, SPILL, WIDE>(a, m, s, t_lo, nv, buf[i], sc, s < S ? slab_dst(a, s) : nullptr, dummy);
+      load_share<K, WIDE>(a, m, clamp(s + NB), t_base, buf[i]);
     }
   }
 }
@@ -324,7 +349,7 @@ __global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArg
 #define FA_NB_CHOICE 4
 #endif
 constexpr int FA_K = FA_K_CHOICE;
-#define FA_KERNEL(spill) kv_append_fused_kernel<FA_K, FA_NB_CHOICE, spill>
+#define FA_KERNEL(spill, wide) kv_append_fused_kernel<FA_K, FA_NB_CHOICE, spill, wide>
 
 static int fused_supported() {
   static int cached[64] = {0};
@@ -332,12 +357,18 @@ static int fused_supported() {
   ZX_TRY_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= 64) return fail(ZX_ERR_UNSUPPORTED, "device index out of range");
   if (!cached[dev]) {
-    int coop = 0, per_cu = 0;
+    int coop = 0, fits = 1;
     ZX_TRY_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
-    int per_cu2 = 0;
-    ZX_TRY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, FA_KERNEL(false), FA_THREADS, 0));
-    ZX_TRY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu2, FA_KERNEL(true), FA_THREADS, 0));
-    cached[dev] = (coop && per_cu >= 1 && per_cu2 >= 1) ? 1 : -1;
+    const void *fns[4] = {reinterpret_cast<const void *>(FA_KERNEL(false, false)),
+                          reinterpret_cast<const void *>(FA_KERNEL(true, false)),
+                          reinterpret_cast<const void *>(FA_KERNEL(false, true)),
+                          reinterpret_cast<const void *>(FA_KERNEL(true, true))};
+    for (const void *fn : fns) {
+      int per_cu = 0;
+      ZX_TRY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, FA_THREADS, 0));
+      fits = fits && per_cu >= 1;
+    }
+    cached[dev] = (coop && fits) ? 1 : -1;
   }
   if (cached[dev] < 0) return fail(ZX_ERR_UNSUPPORTED, "device cannot co-schedule the single-pass append");
   return ZX_OK;
@@ -357,6 +388,9 @@ int append_fused(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, in
   const int G = num_cus();
   if (ceil_div(n_tok, G) * (head_dim / 8) >= (1LL << 30))
     return fail(ZX_ERR_UNSUPPORTED, "fused append: share too large");
+  // source offsets of the register part are 32-bit buffer offsets
+  if ((int64_t)(FA_K * FA_DATA_THREADS / (head_dim / 8) + 1) * 4 * n_heads * head_dim > FA_RANGE)
+    return fail(ZX_ERR_UNSUPPORTED, "fused append: token rows too long");
   const int64_t S = (int64_t)n_layers * 2 * n_heads;
   char *w = static_cast<char *>(ws);
   FusedArgs a;
@@ -382,8 +416,11 @@ int append_fused(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, in
   if ((rc = fill_u32(a.slots, S * G, FA_EMPTY, st))) return rc;
   void *args[] = {&a};
   const bool spill = ceil_div(n_tok, G) * (head_dim / 8) > (int64_t)FA_K * FA_DATA_THREADS;
-  const void *fn = spill ? reinterpret_cast<const void *>(FA_KERNEL(true))
-                         : reinterpret_cast<const void *>(FA_KERNEL(false));
+  const bool wide = pool_layer_stride > FA_RANGE;  // pool offsets beyond 32-bit buffer offsets
+  const void *fn = spill ? (wide ? reinterpret_cast<const void *>(FA_KERNEL(true, true))
+                                 : reinterpret_cast<const void *>(FA_KERNEL(true, false)))
+                         : (wide ? reinterpret_cast<const void *>(FA_KERNEL(false, true))
+                                 : reinterpret_cast<const void *>(FA_KERNEL(false, false)));
   ZX_TRY_HIP(hipLaunchCooperativeKernel(fn, dim3(G), dim3(FA_THREADS), args, 0, st));
   return check_launch("kv_append_fused");
 }

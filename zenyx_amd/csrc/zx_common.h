@@ -54,7 +54,9 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // Four fp32 -> four OCP e4m3fn codes (byte k holds value k), nearest-even, via
 // v_cvt_pk_fp8_f32.  Callers guarantee |v| <= 464 or handle larger values themselves.
 __device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  // the first conversion fills bytes 0-1 and keeps 2-3 of its `old` operand, which the
+  // second one overwrites: any register will do, so no zero has to be materialised
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
 }
@@ -87,88 +89,73 @@ __device__ __forceinline__ float scale_from_amax_bits(uint32_t bits) {
   return a / 448.0f;
 }
 
-// Slab mode from its scale: 0 finite (normal path), 1 +inf, 2 NaN.
-__device__ __forceinline__ int scale_mode(float s) {
-  uint32_t b = __float_as_uint(s) & 0x7FFFFFFFu;
-  return b < 0x7F800000u ? 0 : (b == 0x7F800000u ? 1 : 2);
+// Encode parameters of one slab (uniform across the slab).  A finite scale s encodes
+// RN_e4m3(RN(x / s)) through div_by_scale(x, s, r = RN(1/s)).  The other cases follow
+// the torch evaluation of x / s -> e4m3fn:
+//   * s = +-inf (the slab holds an infinity and no NaN): a finite x gives a zero with
+//     the sign of x, +-inf gives inf/inf = NaN -> 0x7F.  The same arithmetic with s' = 1,
+//     r' = 0 gives exactly the signed zeros, and a NaN for +-inf;
+//   * s = NaN (the slab holds a NaN): every code is 0x7F; s' = r' = NaN make every
+//     value a NaN.
+// In those two cases the NaN codes that come out (0x7F or 0xFF: the sign of a NaN result
+// depends on the operands) are set to 0x7F by nan_codes_positive.  With a finite scale
+// the fix-up is switched off (an overflowing negative quotient keeps its 0xFF), so every
+// slab takes the same branch-free path.
+struct QuantScale {
+  float s, r;
+  uint32_t nan_fix;  // 0x80808080 for a non-finite scale, else 0
+};
+__device__ __forceinline__ QuantScale quant_scale(float sc) {
+  const uint32_t b = __float_as_uint(sc) & 0x7FFFFFFFu;
+  QuantScale q;
+  q.s = b == 0x7F800000u ? 1.0f : sc;
+  q.r = b == 0x7F800000u ? 0.0f : 1.0f / sc;
+  q.nan_fix = b >= 0x7F800000u ? 0x80808080u : 0u;
+  return q;
 }
 
-// Code of one value in a slab whose scale is not finite (mode 1 or 2).
-__device__ __forceinline__ uint32_t code_nonfinite(uint32_t xbits16, int mode) {
-  if (mode == 2) return 0x7Fu;
-  uint32_t mag = xbits16 & 0x7FFFu;
-  if (mag >= 0x7F80u) return 0x7Fu;  // +-inf or NaN input: inf/inf or NaN
-  return (xbits16 >> 8) & 0x80u;     // finite / inf = signed zero
+// Four e4m3 codes of a non-finite-scale slab (each 0x00, 0x80, 0x7F or 0xFF): with
+// fix = 0x80808080 clears bit 7 of every byte whose bit 6 is set, i.e. 0xFF -> 0x7F;
+// with fix = 0 returns c.  (c << 1) moves each byte's bit 6 to its bit 7; the whole
+// expression is one v_bitop3_b32 after the shift.
+__device__ __forceinline__ uint32_t nan_codes_positive(uint32_t c, uint32_t fix) {
+  return c & ~((c << 1) & fix);
+}
+
+// Four bf16 (two 32-bit words) -> four e4m3 codes.
+__device__ __forceinline__ uint32_t quant4(uint32_t u0, uint32_t u1, const QuantScale &q) {
+  return nan_codes_positive(e4m3x4(div_by_scale(bf_lo(u0), q.s, q.r), div_by_scale(bf_hi(u0), q.s, q.r),
+                                   div_by_scale(bf_lo(u1), q.s, q.r), div_by_scale(bf_hi(u1), q.s, q.r)),
+                            q.nan_fix);
 }
 
 // 16 bf16 values (two 16-byte words) -> 16 e4m3 codes (one 16-byte word).
-__device__ __forceinline__ uint4 quant16(uint4 a, uint4 b, float s, float r, int mode) {
-  uint4 out;
-  if (mode == 0) {
-    uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint32_t u0 = w[2 * k], u1 = w[2 * k + 1];
-      o[k] = e4m3x4(div_by_scale(bf_lo(u0), s, r), div_by_scale(bf_hi(u0), s, r),
-                    div_by_scale(bf_lo(u1), s, r), div_by_scale(bf_hi(u1), s, r));
-    }
-    out = make_uint4(o[0], o[1], o[2], o[3]);
-  } else {
-    uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      uint32_t u0 = w[2 * k], u1 = w[2 * k + 1];
-      o[k] = code_nonfinite(u0 & 0xFFFFu, mode) | (code_nonfinite(u0 >> 16, mode) << 8) |
-             (code_nonfinite(u1 & 0xFFFFu, mode) << 16) | (code_nonfinite(u1 >> 16, mode) << 24);
-    }
-    out = make_uint4(o[0], o[1], o[2], o[3]);
-  }
-  return out;
+__device__ __forceinline__ uint4 quant16(uint4 a, uint4 b, const QuantScale &q) {
+  return make_uint4(quant4(a.x, a.y, q), quant4(a.z, a.w, q), quant4(b.x, b.y, q), quant4(b.z, b.w, q));
 }
 
-// 8 bf16 values (one 16-byte word) -> 8 e4m3 codes (one 8-byte word).  Branch-free:
-// the non-finite-scale codes are computed alongside and selected, so callers that keep
-// several loads in flight see straight-line code.
-__device__ __forceinline__ uint2 quant8(uint4 a, float s, float r, int mode) {
-  uint32_t w[4] = {a.x, a.y, a.z, a.w};
-  uint32_t o[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    uint32_t u0 = w[2 * k], u1 = w[2 * k + 1];
-    uint32_t fin = e4m3x4(div_by_scale(bf_lo(u0), s, r), div_by_scale(bf_hi(u0), s, r),
-                          div_by_scale(bf_lo(u1), s, r), div_by_scale(bf_hi(u1), s, r));
-    uint32_t nf = code_nonfinite(u0 & 0xFFFFu, mode) | (code_nonfinite(u0 >> 16, mode) << 8) |
-                  (code_nonfinite(u1 & 0xFFFFu, mode) << 16) | (code_nonfinite(u1 >> 16, mode) << 24);
-    o[k] = mode == 0 ? fin : nf;
-  }
-  return make_uint2(o[0], o[1]);
+// 8 bf16 values (one 16-byte word) -> 8 e4m3 codes (one 8-byte word).
+__device__ __forceinline__ uint2 quant8(uint4 a, const QuantScale &q) {
+  return make_uint2(quant4(a.x, a.y, q), quant4(a.z, a.w, q));
 }
 
-// Largest |bf16| bit pattern among 8 values.
-__device__ __forceinline__ uint32_t absmax8(uint4 q) {
-  uint32_t m = 0;
-  uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    uint32_t u = w[k] & 0x7FFF7FFFu;
-    m = max(m, max(u & 0xFFFFu, u >> 16));
-  }
-  return m;
+// |bf16| bit patterns, two per word, folded into a running packed max (v_pk_max_u16);
+// fold16 gives the largest of the two halves.  A NaN pattern (> 0x7F80) wins over
+// every number, as torch's amax propagates NaN.
+typedef unsigned short zx_u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pkmax(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(zx_u16x2, a),
+                                                                 __builtin_bit_cast(zx_u16x2, b)));
 }
+__device__ __forceinline__ uint32_t absmax_acc(uint32_t acc, uint4 q) {
+  const uint32_t m = 0x7FFF7FFFu;
+  return pkmax(pkmax(acc, pkmax(q.x & m, q.y & m)), pkmax(q.z & m, q.w & m));
+}
+__device__ __forceinline__ uint32_t fold16(uint32_t p) { return max(p & 0xFFFFu, p >> 16); }
 
-// Largest |bf16| bit pattern among 16 values (as a 16-bit magnitude in a uint32).
-__device__ __forceinline__ uint32_t absmax16(uint4 a, uint4 b) {
-  uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  uint32_t m = 0;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    uint32_t u = w[k] & 0x7FFF7FFFu;
-    m = max(m, max(u & 0xFFFFu, u >> 16));
-  }
-  return m;
-}
+// Largest |bf16| bit pattern among 8 / 16 values (a 16-bit magnitude in a uint32).
+__device__ __forceinline__ uint32_t absmax8(uint4 q) { return fold16(absmax_acc(0u, q)); }
+__device__ __forceinline__ uint32_t absmax16(uint4 a, uint4 b) { return fold16(absmax_acc(absmax_acc(0u, a), b)); }
 
 // 16 e4m3 codes (one 16-byte word) -> 16 bf16 values (two 16-byte words).
 __device__ __forceinline__ void dequant16(uint4 c, float s, uint4 &o0, uint4 &o1) {

@@ -161,15 +161,13 @@ __global__ void __launch_bounds__(QH_THREADS)
 heads_quant_kernel(const uint4 *x, HeadsGeom g, const float *scales, uint4 *codes) {
   int64_t run_idx, chunk, slab;
   g.locate(blockIdx.x, run_idx, chunk, slab);
-  const float s = scales[slab];
-  const int mode = scale_mode(s);
-  const float r = 1.0f / s;
+  const QuantScale q = quant_scale(scales[slab]);
   const uint4 *src = x + run_idx * g.vec_per_run * 2;
   uint4 *dst = codes + run_idx * g.vec_per_run;
 #pragma unroll
   for (int k = 0; k < QH_VEC_PER_THREAD; ++k) {
     int64_t v = chunk * QH_CHUNK_VEC + k * QH_THREADS + threadIdx.x;
-    if (v < g.vec_per_run) dst[v] = quant16(src[2 * v], src[2 * v + 1], s, r, mode);
+    if (v < g.vec_per_run) dst[v] = quant16(src[2 * v], src[2 * v + 1], q);
   }
 }
 
@@ -313,9 +311,7 @@ kv_quant_append_kernel(const uint16_t *x, RowGeom g, const int64_t *tok_off, con
   const int c = t % g.vpr, rg = t / g.vpr;
   const int slab = c / g.vec_per_d;
   const int layer = blockIdx.y;
-  const float s = scales[(int64_t)layer * g.n_slabs + slab];
-  const int mode = scale_mode(s);
-  const float rcp = 1.0f / s;
+  const QuantScale q = quant_scale(scales[(int64_t)layer * g.n_slabs + slab]);
   const uint4 *xl = reinterpret_cast<const uint4 *>(x + (int64_t)layer * g.x_layer_stride);
   uint8_t *pl = pool + (int64_t)layer * pool_layer_stride +
                 (int64_t)slab * page_size * head_dim + (c % g.vec_per_d) * 16;
@@ -336,7 +332,7 @@ kv_quant_append_kernel(const uint16_t *x, RowGeom g, const int64_t *tok_off, con
     }
 #pragma unroll
     for (int k = 0; k < KV_UNROLL; ++k)
-      if (off[k] >= 0) *reinterpret_cast<uint4 *>(pl + off[k]) = quant16(a[k], b[k], s, rcp, mode);
+      if (off[k] >= 0) *reinterpret_cast<uint4 *>(pl + off[k]) = quant16(a[k], b[k], q);
   }
 }
 
