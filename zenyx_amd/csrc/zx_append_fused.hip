@@ -5,15 +5,19 @@
 // them can be encoded.  Instead of reading the input twice (amax pass + quant pass), one
 // cooperative persistent launch keeps each workgroup's share of a slab on chip:
 //   * workgroup w (one per CU) owns tokens [w*T/G, (w+1)*T/G) of every slab;
-//   * 15 data waves stream the share of slab s+3 from HBM into registers (three register
-//     buffers per lane) while encoding slab s and reducing the max of slab s+2, so loads
-//     stay in flight continuously and no block-wide barrier is ever taken;
+//   * 15 data waves keep NB = 4 slabs of their share in registers.  At step s a wave
+//     reduces the max of slab s+3 (loaded during step s-1), hands it to the workgroup,
+//     waits for slab s's scale, encodes slab s and refills that buffer with slab s+4, so
+//     loads stay in flight continuously and no block-wide barrier is ever taken;
 //   * a wave's max goes to an LDS slot (ds_max + arrival count); the control wave (the
 //     16th) stores the workgroup's max into its own device-coherent slot of slab s
 //     (slots start as a sentinel), reads all G slots of a slab with one wave-wide load
 //     until none is the sentinel, and broadcasts the finished scale through LDS.  It
-//     publishes slab s+1 while still polling slab s, so two slabs' round trips overlap,
+//     publishes later slabs while still polling slab s, so their round trips overlap,
 //     and the data waves keep streaming throughout.
+// Loads and stores go through buffer resources, whose range check drops the lanes that
+// have nothing to move (past the share, rows without a page, padding steps), so the
+// data path has no per-lane branch or select.
 // HBM traffic is 2 B read + 1 B written per element.  Tokens of a share beyond what the
 // registers hold are re-read from memory (both for the max and for the encode).
 // Every wait is bounded in wall time; a timeout raises a global abort flag that
@@ -90,9 +94,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, int num
 // outstanding loads exactly (s_waitcnt vmcnt(N) instead of vmcnt(0)) and later slabs'
 // loads stay in flight.
 template <int K, bool WIDE> struct ThreadMap {
-  uint32_t src[K];
+  uint32_t src;  // offset of vector 0 from its row block's first row
   typename std::conditional<WIDE, int64_t, uint32_t>::type dst[K];
-  int nreg;  // vectors of the share held in registers (whole workgroup)
+  int nreg;         // vectors of the share held in registers (whole workgroup)
+  int64_t blk_bytes;  // bytes between row blocks k and k + 1 (FA_DATA_THREADS vectors)
+  int range[K];     // bytes of row block k inside the register part (0 if none)
 };
 
 __device__ __forceinline__ int64_t vec_src(const FusedArgs &a, int v) {
@@ -112,13 +118,17 @@ __device__ __forceinline__ uint8_t *slab_dst(const FusedArgs &a, int s) {
   return a.pool + (int64_t)l * a.pool_layer_stride + (int64_t)j * a.page_size * a.head_dim;
 }
 
+// Vector k*FA_DATA_THREADS + tid lies FA_DATA_THREADS / vpt rows after vector tid, in
+// the same column, so one per-lane offset serves every k: row block k gets a resource
+// of its own whose num_records ends at the last row of the register part.
 template <int K, bool WIDE>
 __device__ __forceinline__ void load_share(const FusedArgs &a, const ThreadMap<K, WIDE> &m, int s, int64_t t_base,
                                            uint4 (&r)[K]) {
-  const __amdgpu_buffer_rsrc_t rs = rsrc(slab_src(a, s, t_base), FA_RANGE);
+  const char *base = slab_src(a, s, t_base);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const zx_v4u q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)m.src[k], 0, FA_NT);
+    const __amdgpu_buffer_rsrc_t rs = rsrc(base + k * m.blk_bytes, m.range[k]);
+    const zx_v4u q = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)m.src, 0, FA_NT);
     r[k] = make_uint4(q.x, q.y, q.z, q.w);
   }
 }
@@ -295,11 +305,21 @@ __global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArg
   m.nreg = nv < K * FA_DATA_THREADS ? nv : K * FA_DATA_THREADS;
   // a workgroup with an empty share bases its (all out-of-range) loads at token 0
   const int64_t t_base = nv > 0 ? t_lo : 0;
+  {
+    const int64_t row_bytes = 4LL * a.n_heads * a.head_dim;
+    const int rows_blk = FA_DATA_THREADS >> a.vpt_log2, rows_reg = m.nreg >> a.vpt_log2;
+    m.src = (uint32_t)vec_src(a, threadIdx.x);
+    m.blk_bytes = rows_blk * row_bytes;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int rows = rows_reg - k * rows_blk;
+      m.range[k] = rows > 0 ? (int)(rows * row_bytes) : 0;
+    }
+  }
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int v = k * FA_DATA_THREADS + threadIdx.x;
     const bool live = v < m.nreg;
-    m.src[k] = live ? (uint32_t)vec_src(a, v) : FA_OOB;
     const int64_t off = live ? a.tok_off[t_lo + (v >> a.vpt_log2)] : -1;
     const int64_t d = off < 0 ? -1 : off + (v & ((1 << a.vpt_log2) - 1)) * 8;
     if constexpr (WIDE) m.dst[k] = d;
