@@ -112,7 +112,11 @@ size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32
 #define ZX_APPEND_STATIC_SCALES 1 /* flag: use `scales` as given instead of computing them */
 #define ZX_APPEND_TWO_PASS 2      /* flag: compute dynamic scales in a separate amax pass
                                      instead of the single-pass cooperative kernel (same
-                                     results; for devices without cooperative launch) */
+                                     results).  Without the flag the library picks: one
+                                     pass while a CU's share of a (layer, kv, head) slab
+                                     fits about twice its registers (~150k tokens at
+                                     D = 128 on MI355X), two passes beyond that or on
+                                     devices without cooperative launch. */
 
 /* Paged append with fused FP8 quantisation.  Without
  * ZX_APPEND_STATIC_SCALES the scales are computed from this batch (amax over all

@@ -206,8 +206,9 @@ def test_kv_gather_dequant_nan_codes_and_bad_pages(dev):
 
 @pytest.mark.parametrize("two_pass", [False, True])
 @pytest.mark.parametrize("L,H,D,P,lens", [
-    (2, 8, 128, 16, [1000, 17, 2048, 511]),   # single-pass kernel: every share fits in LDS
-    (1, 1, 256, 16, [30000, 20001]),          # share larger than an LDS buffer: spill path
+    (2, 8, 128, 16, [1000, 17, 2048, 511]),   # single pass: every share fits in registers
+    (1, 1, 256, 16, [30000, 20001]),          # share beyond the registers: spill path
+    (1, 1, 256, 16, [60000, 41000]),          # share beyond twice the registers: two passes
     (3, 4, 64, 32, [3, 1, 2]),                # fewer tokens than workgroups
 ])
 def test_kv_quant_append_fused_and_two_pass_bit_exact(dev, two_pass, L, H, D, P, lens):

@@ -394,6 +394,10 @@ static int fused_supported() {
   return ZX_OK;
 }
 
+bool append_fused_preferred(int64_t n_tok, int32_t head_dim) {
+  return ceil_div(n_tok, num_cus()) * (head_dim / 8) <= 2LL * FA_K * FA_DATA_THREADS;
+}
+
 // workspace: abort flag (+ 60 B pad) | dummy store slots (128 B) | slots [S][G]
 size_t append_fused_workspace_bytes(int32_t n_layers, int32_t n_heads) {
   const size_t S = (size_t)n_layers * 2 * n_heads;
