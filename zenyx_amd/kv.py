@@ -12,6 +12,8 @@ Layouts:
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _native as N
@@ -334,3 +336,28 @@ class BeladyTraceSim:
         """(positions, pages) of the stored victims as CPU int32 tensors."""
         k = min(self.n_evicted, self.evict_cap)
         return self.evict_pos[:k].cpu(), self.evict_page[:k].cpu()
+
+
+def tier_copy_runs(dst: torch.Tensor, src: torch.Tensor, dst_offs, src_offs, run_bytes: int,
+                   stream: torch.cuda.Stream | None = None) -> None:
+    """Enqueue run copies ``dst[dst_offs[i] : +run_bytes] = src[src_offs[i] : +run_bytes]``
+    (byte offsets into the two tensors' storage) on ``stream`` (default: the current one).
+    One side is a device tensor, the other device or pinned host memory; adjacent runs are
+    merged into one copy.  Replaces the ``.to(device)`` / ``.cpu()`` moves of
+    kv_tiering.py:46, 54, 60."""
+    import numpy as np
+
+    d = np.ascontiguousarray(dst_offs, dtype=np.int64)
+    s = np.ascontiguousarray(src_offs, dtype=np.int64)
+    if d.shape != s.shape or d.ndim != 1:
+        raise ValueError("dst_offs and src_offs must be 1-D of equal length")
+    nb_d, nb_s = dst.numel() * dst.element_size(), src.numel() * src.element_size()
+    if len(d) and (d.min() < 0 or s.min() < 0 or d.max() + run_bytes > nb_d or s.max() + run_bytes > nb_s):
+        raise ValueError("run outside a buffer")
+    if not (dst.is_contiguous() and src.is_contiguous()):
+        raise ValueError("dst and src must be contiguous")
+    dev = dst.device if dst.is_cuda else src.device
+    st = stream if stream is not None else torch.cuda.current_stream(dev)
+    lib = N.load()
+    N.check(lib.zx_tier_copy_runs(N.ptr(dst), N.ptr(src), d.ctypes.data, s.ctypes.data, len(d), run_bytes,
+                                  ctypes.c_void_p(st.cuda_stream), None), "tier_copy_runs")
