@@ -30,7 +30,7 @@ METRIC = "KV quant+append & gather+dequant GB/s (% HBM peak); evictions/sec"
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE and scaled by the same counters on a plain 4 GiB copy (profiles/*.md); keyed by
 # (workload, seed) because the append's size depends on the seed.
-MEASURED_TRAFFIC = {("append", 1): 14_824_469_511, ("gather", 2): 12_889_157_804}
+MEASURED_TRAFFIC = {("append", 1): 14_804_340_633, ("gather", 2): 12_889_463_193}
 
 
 def parse():
