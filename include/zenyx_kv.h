@@ -142,6 +142,25 @@ int zx_kv_gather_dequant(const uint8_t *pool, int64_t n_pages, int32_t n_heads, 
                          int32_t out_len, uint16_t *k_out, uint16_t *v_out, int32_t *err,
                          zx_stream_t stream);
 
+/* Decode attention straight from the FP8 pages (the attention that consumes FP8 pages
+ * directly: QuantizedRingAttention, README.md:344, whose code is absent; defined here).
+ * q: [n_seqs][n_q_heads][head_dim] bf16, one query token per sequence; query head i reads
+ * kv head i / (n_q_heads / n_kv_heads).  For positions t < seq_lens[b]:
+ *   s_t = sm_scale * sum_d q[d] * K_t[d],   K_t[d] = decode(code) * scales[0][h]
+ *   out = sum_t softmax(s)_t * V_t,         V_t[d] = decode(code) * scales[1][h]
+ * computed in fp32 (exp2-domain online softmax, split over positions) and rounded once to
+ * bf16: within 1 bf16 ulp of the same expression evaluated exactly.  A sequence of length
+ * 0 gives zeros; rows with an out-of-range page id or a position past max_blocks*P are
+ * left out and flagged in *err.  out: [n_seqs][n_q_heads][head_dim] bf16.  workspace:
+ * zx_paged_attention_decode_workspace_bytes() device bytes (per-split partial results). */
+size_t zx_paged_attention_decode_workspace_bytes(int32_t n_seqs, int32_t n_q_heads, int32_t head_dim,
+                                                 int32_t max_blocks, int32_t page_size);
+int zx_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, const uint8_t *pool, int64_t n_pages,
+                              int32_t n_kv_heads, int32_t head_dim, int32_t page_size, const float *scales,
+                              const int32_t *block_tables, int32_t max_blocks, const int32_t *seq_lens,
+                              int32_t n_seqs, float sm_scale, uint16_t *out, int32_t *err,
+                              void *workspace, size_t workspace_bytes, zx_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Belady victim selection.  Replaces zenyx/streaming/belady.py:39-51: among slots
  * with resident[i] != 0, pick the largest keys[i] that is > -1; ties go to the

@@ -56,6 +56,7 @@ def lib() -> ctypes.CDLL:
             "zxo_next_use": (None, [P, i64, i32, P, P]),
             "zxo_belady_simulate": (i64, [P, i64, i32, i64, P, P, i64, P, P]),
             "zxo_ring_trace": (None, [i32, i32, i32, P]),
+            "zxo_paged_attention_decode": (i32, [P, i32, P, i64, i32, i32, i32, P, P, i32, P, i32, f32, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -180,6 +181,21 @@ def kv_gather_dequant(pool_layer, scales_layer, block_tables, seq_lens, out_len)
 # ------------------------------------------------------------------ legacy int8
 
 _DT = {"bf16": 0, "f16": 1, "f32": 2}
+
+
+def paged_attention_decode(q_bits, pool_layer, scales_layer, block_tables, seq_lens, sm_scale):
+    """q_bits [B, Hq, D] bf16 bits; pool_layer [n_pages, 2, Hkv, P, D] -> (out bits [B, Hq, D], err)."""
+    q_bits = np.ascontiguousarray(q_bits, dtype=np.uint16)
+    pool_layer = np.ascontiguousarray(pool_layer, dtype=np.uint8)
+    n_pages, _, Hkv, P, D = pool_layer.shape
+    B, Hq, _ = q_bits.shape
+    sc = np.ascontiguousarray(scales_layer, dtype=np.float32)
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    out = np.empty((B, Hq, D), np.uint16)
+    err = lib().zxo_paged_attention_decode(_p(q_bits), Hq, _p(pool_layer), n_pages, Hkv, D, P, _p(sc), _p(bt),
+                                           bt.shape[1], _p(sl), B, float(sm_scale), _p(out))
+    return out, int(err)
 
 
 def int8_legacy_quant(x: np.ndarray, dtype: str):

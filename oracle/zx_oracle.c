@@ -257,6 +257,69 @@ int32_t zxo_kv_gather_dequant(const uint8_t *pool, int64_t n_pages, int32_t n_he
   return err;
 }
 
+/* ------------------------------------------------------ paged decode attention */
+
+/* One query token per sequence attending to its paged FP8 K/V (the attention that
+ * consumes FP8 pages directly, QuantizedRingAttention README.md:344; semantics defined
+ * by include/zenyx_kv.h).  q [B][Hq][D] bf16; kv head of query head hq = hq / (Hq/Hkv);
+ *   s_t = sm_scale * sum_d q[d] * K[t][d],  K = decode(code) * scale_k, t < seq_len
+ *   out = sum_t softmax(s)_t * V[t],        V = decode(code) * scale_v
+ * evaluated in double and rounded once to bf16 (via fp32); a sequence of length 0
+ * gives zeros.  Returns the error bits of zxo_kv_gather_dequant (such rows are skipped). */
+int32_t zxo_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, const uint8_t *pool,
+                                   int64_t n_pages, int32_t n_kv_heads, int32_t head_dim,
+                                   int32_t page_size, const float *scales, const int32_t *block_tables,
+                                   int32_t max_blocks, const int32_t *seq_lens, int32_t n_seqs,
+                                   float sm_scale, uint16_t *out) {
+  int32_t err = 0;
+  const int32_t grp = n_q_heads / n_kv_heads;
+  const int64_t page_bytes = 2LL * n_kv_heads * page_size * head_dim;
+  double *s = NULL, *acc = malloc(sizeof(double) * head_dim);
+  int64_t *pg = NULL, cap = 0;
+  for (int32_t b = 0; b < n_seqs; ++b)
+    for (int32_t hq = 0; hq < n_q_heads; ++hq) {
+      const int32_t h = hq / grp;
+      const uint16_t *qv = q + ((int64_t)b * n_q_heads + hq) * head_dim;
+      uint16_t *o = out + ((int64_t)b * n_q_heads + hq) * head_dim;
+      const int64_t len = seq_lens[b] > 0 ? seq_lens[b] : 0;
+      if (len > cap) {
+        cap = len;
+        s = realloc(s, sizeof(double) * (size_t)cap);
+        pg = realloc(pg, sizeof(int64_t) * (size_t)cap);
+      }
+      double m = -INFINITY;
+      for (int64_t t = 0; t < len; ++t) {  /* scores; pg[t] < 0 marks a skipped row */
+        pg[t] = -1;
+        if (t / page_size >= max_blocks) { err |= 2; continue; }
+        const int64_t page = block_tables[(int64_t)b * max_blocks + t / page_size];
+        if (page < 0 || page >= n_pages) { err |= 1; continue; }
+        pg[t] = page;
+        const uint8_t *kr = pool + page * page_bytes + ((int64_t)h * page_size + t % page_size) * head_dim;
+        double dot = 0.0;
+        for (int32_t d = 0; d < head_dim; ++d)
+          dot += (double)zxo_bf16_to_f32(qv[d]) * ((double)zxo_e4m3_decode(kr[d]) * (double)scales[h]);
+        s[t] = dot * (double)sm_scale;
+        if (s[t] > m) m = s[t];
+      }
+      double l = 0.0;
+      for (int32_t d = 0; d < head_dim; ++d) acc[d] = 0.0;
+      for (int64_t t = 0; t < len; ++t) {
+        if (pg[t] < 0) continue;
+        const double p = exp(s[t] - m);
+        const uint8_t *vr = pool + pg[t] * page_bytes +
+                            ((int64_t)(n_kv_heads + h) * page_size + t % page_size) * head_dim;
+        l += p;
+        for (int32_t d = 0; d < head_dim; ++d)
+          acc[d] += p * ((double)zxo_e4m3_decode(vr[d]) * (double)scales[n_kv_heads + h]);
+      }
+      for (int32_t d = 0; d < head_dim; ++d) o[d] = l > 0.0 || isnan(l) ? zxo_bf16_rne((float)(acc[d] / l)) : 0;
+    }
+  free(s);
+  free(pg);
+  free(acc);
+  return err;
+}
+
 /* ---------------------------------------------------------------- legacy int8 */
 
 /* Round a float to the storage dtype and back (0 bf16, 1 f16, 2 f32), as torch stores

@@ -353,3 +353,40 @@ def test_ring_trace_structure():
     one = O.ring_trace(1, 1, 5)
     ref = O.ref_ring_timeline(5)
     assert one.tolist() == ref["forward"] + ref["backward"]
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,P,seed", [(8, 2, 64, 16, 0), (4, 4, 128, 5, 1), (8, 1, 256, 32, 2)])
+def test_paged_attention_oracle_matches_torch_sdpa(Hq, Hkv, D, P, seed):
+    """The oracle's decode attention against torch's float64 softmax(qK^T)V on K/V built by
+    plain numpy indexing of the pool (codes decoded, times the per-head scale), including
+    an empty sequence, a one-token one and a partial last page."""
+    rng = np.random.default_rng(seed)
+    lens = np.array([0, 1, 3 * P + 2, 50], np.int32)
+    B, n_pages = len(lens), 64
+    max_blocks = (int(lens.max()) + P - 1) // P
+    pool = rng.integers(0, 256, (n_pages, 2, Hkv, P, D), dtype=np.uint8)
+    pool[(pool & 0x7F) == 0x7F] = 0x12  # no NaN codes
+    bt = np.stack([rng.permutation(n_pages)[:max_blocks] for _ in range(B)]).astype(np.int32)
+    scales = rng.uniform(1e-3, 0.05, (2, Hkv)).astype(np.float32)
+    q = torch.randn((B, Hq, D), dtype=torch.float32).to(torch.bfloat16)
+    qb = q.view(torch.int16).numpy().view(np.uint16)
+    sm = 1.0 / np.sqrt(D)
+    got, err = O.paged_attention_decode(qb, pool, scales, bt, lens, sm)
+    assert err == 0
+    dec = O.e4m3_decode(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    grp = Hq // Hkv
+    for b in range(B):
+        t = np.arange(lens[b])
+        pages = bt[b, t // P]
+        for hq in range(Hq):
+            h = hq // grp
+            K = torch.from_numpy(dec[pool[pages, 0, h, t % P, :]] * float(scales[0, h]))
+            V = torch.from_numpy(dec[pool[pages, 1, h, t % P, :]] * float(scales[1, h]))
+            qd = q[b, hq].double()
+            if lens[b] == 0:
+                want = torch.zeros(D, dtype=torch.bfloat16)
+            else:
+                p = torch.softmax((K @ qd) * sm, dim=0)
+                want = (p @ V).float().to(torch.bfloat16)
+            w = want.view(torch.int16).numpy().view(np.uint16)
+            np.testing.assert_array_equal(got[b, hq], w)

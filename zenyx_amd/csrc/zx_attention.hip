@@ -1,0 +1,330 @@
+// zx_attention.hip -- decode attention straight from the paged FP8 pool.
+//
+// One query token per sequence attends to its K/V pages without materialising bf16 K/V
+// (the attention that consumes FP8 pages directly, QuantizedRingAttention README.md:344):
+//   s_t = sm_scale * q . K_t,  K_t = decode(code) * scale_k     (t < seq_len)
+//   out = sum_t softmax(s)_t V_t,  V_t = decode(code) * scale_v
+// HBM traffic is 1 B per K/V element (the gather + dequant path moves 3 B and then the
+// attention reads 2 B more).
+//
+// Split-K flash decoding.  Pass 1 (paged_decode_partial_kernel): a block owns one
+// (sequence, kv head, group of G query heads, split of ATT_SPLIT positions); lane l of a
+// wave owns 16 channels (dc = l % LPT, LPT = D / 16 lanes per token) of token slot
+// l / LPT, so K and V rows are read as 16-byte loads that cover whole page rows.  Scale
+// factors fold into q (q * scale_k * sm_scale * log2 e) and into the end (scale_v), so
+// the inner loop works on decoded codes.  Each wave keeps an online softmax (running max
+// m, sum l, accumulator acc[G][16] per lane, exp2 domain) over steps of ATT_U passes;
+// at the end the token slots and the block's 4 waves are combined and the partial
+// (m, l, acc[D]) per query head is written to the workspace.  Pass 2
+// (paged_decode_combine_kernel) merges the splits of a (sequence, query head) and writes
+// bf16.
+#include "zx_common.h"
+
+namespace zx {
+
+constexpr int ATT_THREADS = 256;  // 4 waves
+constexpr int ATT_WAVES = ATT_THREADS / 64;
+constexpr int ATT_U = 4;          // passes per online-softmax step
+constexpr int ATT_SPLIT = 1024;   // positions per block
+constexpr float ATT_LOG2E = 1.4426950408889634f;
+
+struct AttnGeom {
+  int32_t n_q_heads, n_kv_heads, head_dim, page_size, max_blocks, n_seqs;
+  int32_t n_splits;
+  int64_t n_pages;
+  float sm_scale;
+};
+
+// 16 e4m3 codes -> 16 fp32 values (exact).
+__device__ __forceinline__ void decode16(uint4 c, float (&f)[16]) {
+  e4m3x4_decode(c.x, f[0], f[1], f[2], f[3]);
+  e4m3x4_decode(c.y, f[4], f[5], f[6], f[7]);
+  e4m3x4_decode(c.z, f[8], f[9], f[10], f[11]);
+  e4m3x4_decode(c.w, f[12], f[13], f[14], f[15]);
+}
+
+__device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
+__device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
+
+// Partial layout in the workspace: [B][Hq][n_splits][2 + D] fp32 = (m, l, acc[D]) with m
+// in the exp2 domain; a split without valid positions writes m = -inf, l = 0, acc = 0.
+template <int G, int D>
+__global__ void __launch_bounds__(ATT_THREADS)
+paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8_t *__restrict__ pool,
+                            const float *__restrict__ scales, const int32_t *__restrict__ block_tables,
+                            const int32_t *__restrict__ seq_lens, float *__restrict__ part, int32_t *err) {
+  constexpr int LPT = D / 16;   // lanes per token
+  constexpr int TPW = 64 / LPT;  // token slots per wave pass
+  const int split = blockIdx.x;
+  const int grp_blocks = g.n_q_heads / g.n_kv_heads / G;  // query-head groups per kv head
+  const int h = blockIdx.y / grp_blocks;
+  const int hq0 = h * (g.n_q_heads / g.n_kv_heads) + (blockIdx.y % grp_blocks) * G;
+  const int b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ts = lane / LPT, dc = lane % LPT;
+  const int32_t len = seq_lens[b];
+  const int64_t t_begin = (int64_t)split * ATT_SPLIT;
+  const int64_t t_end = min(min((int64_t)len, (int64_t)g.max_blocks * g.page_size), t_begin + ATT_SPLIT);
+  const int64_t page_bytes = 2LL * g.n_kv_heads * g.page_size * D;
+  const uint8_t *kbase = pool + (int64_t)h * g.page_size * D + dc * 16;
+  const uint8_t *vbase = kbase + (int64_t)g.n_kv_heads * g.page_size * D;
+  const int32_t *bt = block_tables + (int64_t)b * g.max_blocks;
+
+  // q' = q * scale_k * sm_scale * log2(e) for this lane's 16 channels
+  float qf[G][16];
+  const float qs = scales[h] * g.sm_scale * ATT_LOG2E;
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    const uint4 *qp = reinterpret_cast<const uint4 *>(q + ((int64_t)b * g.n_q_heads + hq0 + j) * D + dc * 16);
+    const uint4 a = qp[0], c = qp[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      qf[j][2 * i] = bf_lo(w[i]) * qs;
+      qf[j][2 * i + 1] = bf_hi(w[i]) * qs;
+    }
+  }
+
+  float m[G], l[G], acc[G][16];
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[j][i] = 0.0f;
+  }
+  // positions past the block table are not attended to, and flagged once per sequence
+  int32_t e = split == 0 && threadIdx.x == 0 && blockIdx.y == 0 && (int64_t)len > (int64_t)g.max_blocks * g.page_size
+                  ? ZX_KERR_POS_RANGE : 0;
+
+  // wave w takes steps w, w + 4, ...; a step is ATT_U passes of TPW consecutive positions
+  for (int64_t t0 = t_begin + (int64_t)wave * ATT_U * TPW; t0 < t_end; t0 += (int64_t)ATT_WAVES * ATT_U * TPW) {
+    uint4 kc[ATT_U], vc[ATT_U];
+    bool ok[ATT_U];
+#pragma unroll
+    for (int u = 0; u < ATT_U; ++u) {
+      const int64_t t = t0 + u * TPW + ts;
+      ok[u] = false;
+      kc[u] = vc[u] = make_uint4(0, 0, 0, 0);
+      if (t < t_end) {
+        const int64_t bi = t / g.page_size;
+        if (bi >= g.max_blocks) {
+          e |= ZX_KERR_POS_RANGE;
+        } else {
+          const int64_t page = bt[bi];
+          if (page < 0 || page >= g.n_pages) {
+            e |= ZX_KERR_PAGE_RANGE;
+          } else {
+            const int64_t off = page * page_bytes + (t - bi * g.page_size) * D;
+            kc[u] = *reinterpret_cast<const uint4 *>(kbase + off);
+            vc[u] = *reinterpret_cast<const uint4 *>(vbase + off);
+            ok[u] = true;
+          }
+        }
+      }
+    }
+    // scores (exp2 domain), reduced over the LPT lanes of each token
+    float s[ATT_U][G];
+#pragma unroll
+    for (int u = 0; u < ATT_U; ++u) {
+      float k[16];
+      decode16(kc[u], k);
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a = __builtin_fmaf(qf[j][i], k[i], a);
+#pragma unroll
+        for (int mk = 1; mk < LPT; mk <<= 1) a = xor_sum(a, mk);
+        s[u][j] = ok[u] ? a : -INFINITY;
+      }
+    }
+    // online softmax update per query head
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      float mx = s[0][j];
+#pragma unroll
+      for (int u = 1; u < ATT_U; ++u) mx = fmaxf(mx, s[u][j]);
+#pragma unroll
+      for (int mk = LPT; mk < 64; mk <<= 1) mx = xor_max(mx, mk);
+      const float m_new = fmaxf(m[j], mx);
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[j] - m_new);
+      m[j] = m_new;
+      l[j] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[j][i] *= alpha;
+#pragma unroll
+      for (int u = 0; u < ATT_U; ++u) s[u][j] = m_new == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[u][j] - m_new);
+    }
+#pragma unroll
+    for (int u = 0; u < ATT_U; ++u) {
+      float v[16];
+      decode16(vc[u], v);
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        l[j] += s[u][j];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[j][i] = __builtin_fmaf(s[u][j], v[i], acc[j][i]);
+      }
+    }
+  }
+
+  // token slots of the wave -> one value per (head, channel) in every lane of slot 0
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+#pragma unroll
+    for (int mk = LPT; mk < 64; mk <<= 1) {
+      l[j] = xor_sum(l[j], mk);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[j][i] = xor_sum(acc[j][i], mk);
+    }
+  }
+  // combine the block's waves through LDS
+  __shared__ float sm_m[ATT_WAVES][G], sm_l[ATT_WAVES][G];
+  __shared__ float sm_acc[ATT_WAVES][G][D];
+  if (ts == 0) {
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sm_acc[wave][j][dc * 16 + i] = acc[j][i];
+      if (dc == 0) {
+        sm_m[wave][j] = m[j];
+        sm_l[wave][j] = l[j];
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += ATT_THREADS) {
+    const int j = idx / D, d = idx % D;
+    float M = sm_m[0][j];
+#pragma unroll
+    for (int w = 1; w < ATT_WAVES; ++w) M = fmaxf(M, sm_m[w][j]);
+    float a = 0.0f, ll = 0.0f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) {
+      const float f = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm_m[w][j] - M);
+      a += f * sm_acc[w][j][d];
+      ll += f * sm_l[w][j];
+    }
+    float *pp = part + (((int64_t)b * g.n_q_heads + hq0 + j) * g.n_splits + split) * (2 + D);
+    pp[2 + d] = a;
+    if (d == 0) {
+      pp[0] = M;
+      pp[1] = ll;
+    }
+  }
+  if (e && err) atomicOr(err, e);
+}
+
+// Pass 2: out[b][hq][:] = scale_v * sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s.
+__global__ void __launch_bounds__(256)
+paged_decode_combine_kernel(const float *__restrict__ part, AttnGeom g, const float *__restrict__ scales,
+                            uint16_t *__restrict__ out) {
+  const int64_t row = blockIdx.x;  // b * Hq + hq
+  const int hq = (int)(row % g.n_q_heads);
+  const int h = hq / (g.n_q_heads / g.n_kv_heads);
+  const int D = g.head_dim;
+  const float *pp = part + row * g.n_splits * (2 + D);
+  __shared__ float w_s[256];
+  __shared__ float l_sum;
+  float M = -INFINITY;
+  for (int s = 0; s < g.n_splits; ++s) M = fmaxf(M, pp[s * (2 + D)]);
+  if (threadIdx.x == 0) {
+    float ll = 0.0f;
+    for (int s = 0; s < g.n_splits; ++s)
+      ll += M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pp[s * (2 + D)] - M) * pp[s * (2 + D) + 1];
+    l_sum = ll;
+  }
+  for (int s = threadIdx.x; s < g.n_splits && s < 256; s += blockDim.x)
+    w_s[s] = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pp[s * (2 + D)] - M);
+  __syncthreads();
+  const float sv = scales[g.n_kv_heads + h];
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float a = 0.0f;
+    for (int s = 0; s < g.n_splits; ++s) {
+      const float f = s < 256 ? w_s[s] : (M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pp[s * (2 + D)] - M));
+      a += f * pp[s * (2 + D) + 2 + d];
+    }
+    // a sequence without positions (l = 0) gives zeros
+    const float o = l_sum == 0.0f ? 0.0f : a / l_sum * sv;
+    out[row * D + d] = (uint16_t)(pack_bf16(o, 0.0f) & 0xFFFFu);
+  }
+}
+
+}  // namespace zx
+
+using namespace zx;
+
+static int64_t att_splits(int32_t max_blocks, int32_t page_size) {
+  return ceil_div((int64_t)max_blocks * page_size, ATT_SPLIT);
+}
+
+extern "C" size_t zx_paged_attention_decode_workspace_bytes(int32_t n_seqs, int32_t n_q_heads, int32_t head_dim,
+                                                            int32_t max_blocks, int32_t page_size) {
+  if (n_seqs <= 0 || n_q_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || page_size <= 0) return 0;
+  return (size_t)n_seqs * n_q_heads * att_splits(max_blocks, page_size) * (2 + head_dim) * sizeof(float);
+}
+
+template <int G, int D>
+static int launch_partial(dim3 grid, hipStream_t st, const uint16_t *q, const AttnGeom &g, const uint8_t *pool,
+                          const float *scales, const int32_t *bt, const int32_t *sl, float *part, int32_t *err) {
+  paged_decode_partial_kernel<G, D><<<grid, ATT_THREADS, 0, st>>>(q, g, pool, scales, bt, sl, part, err);
+  return check_launch("paged_decode_partial");
+}
+
+template <int D>
+static int launch_g(int G, dim3 grid, hipStream_t st, const uint16_t *q, const AttnGeom &g, const uint8_t *pool,
+                    const float *scales, const int32_t *bt, const int32_t *sl, float *part, int32_t *err) {
+  switch (G) {
+    case 1: return launch_partial<1, D>(grid, st, q, g, pool, scales, bt, sl, part, err);
+    case 2: return launch_partial<2, D>(grid, st, q, g, pool, scales, bt, sl, part, err);
+    default: return launch_partial<4, D>(grid, st, q, g, pool, scales, bt, sl, part, err);
+  }
+}
+
+extern "C" int zx_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, const uint8_t *pool, int64_t n_pages,
+                                         int32_t n_kv_heads, int32_t head_dim, int32_t page_size,
+                                         const float *scales, const int32_t *block_tables, int32_t max_blocks,
+                                         const int32_t *seq_lens, int32_t n_seqs, float sm_scale, uint16_t *out,
+                                         int32_t *err, void *workspace,
+                                         size_t workspace_bytes, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(q && pool && scales && block_tables && seq_lens && out, "paged_attention_decode: null pointer");
+  ZX_REQUIRE(n_q_heads > 0 && n_kv_heads > 0 && n_pages > 0 && page_size > 0 && max_blocks > 0 && n_seqs > 0,
+             "paged_attention_decode: sizes must be positive");
+  ZX_REQUIRE(n_q_heads % n_kv_heads == 0, "paged_attention_decode: n_q_heads must be a multiple of n_kv_heads");
+  if (!(head_dim == 64 || head_dim == 128 || head_dim == 256))
+    return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: head_dim %d not in {64, 128, 256}", head_dim);
+  if (n_seqs > 65535) return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: more than 65535 sequences");
+  const size_t need = zx_paged_attention_decode_workspace_bytes(n_seqs, n_q_heads, head_dim, max_blocks, page_size);
+  if (!workspace || workspace_bytes < need)
+    return fail(ZX_ERR_WORKSPACE, "paged_attention_decode: workspace %zu < %zu bytes", workspace_bytes, need);
+  const int grp = n_q_heads / n_kv_heads;
+  const int G = grp % 4 == 0 ? 4 : (grp % 2 == 0 ? 2 : 1);  // query heads per block
+  AttnGeom g;
+  g.n_q_heads = n_q_heads;
+  g.n_kv_heads = n_kv_heads;
+  g.head_dim = head_dim;
+  g.page_size = page_size;
+  g.max_blocks = max_blocks;
+  g.n_seqs = n_seqs;
+  const int64_t n_splits = att_splits(max_blocks, page_size);
+  if (n_splits >= (1LL << 31)) return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: sequences too long");
+  g.n_splits = (int32_t)n_splits;
+  g.n_pages = n_pages;
+  g.sm_scale = sm_scale;
+  const int64_t gy = (int64_t)n_kv_heads * (grp / G);
+  if (gy > 65535) return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: too many heads");
+  hipStream_t st = as_stream(stream);
+  float *part = static_cast<float *>(workspace);
+  const dim3 grid((unsigned)g.n_splits, (unsigned)gy, (unsigned)n_seqs);
+  int rc;
+  switch (head_dim) {
+    case 64: rc = launch_g<64>(G, grid, st, q, g, pool, scales, block_tables, seq_lens, part, err); break;
+    case 128: rc = launch_g<128>(G, grid, st, q, g, pool, scales, block_tables, seq_lens, part, err); break;
+    default: rc = launch_g<256>(G, grid, st, q, g, pool, scales, block_tables, seq_lens, part, err); break;
+  }
+  if (rc) return rc;
+  paged_decode_combine_kernel<<<(unsigned)((int64_t)n_seqs * n_q_heads), 256, 0, st>>>(part, g, scales, out);
+  return check_launch("paged_decode_combine");
+}

@@ -244,6 +244,50 @@ def kv_gather_dequant(pool_layer: torch.Tensor, scales_layer: torch.Tensor, bloc
     return k, v
 
 
+def paged_attention_decode(q: torch.Tensor, pool_layer: torch.Tensor, scales_layer: torch.Tensor,
+                           block_tables: torch.Tensor, seq_lens: torch.Tensor, sm_scale: float | None = None,
+                           out: torch.Tensor | None = None, check: bool = False) -> torch.Tensor:
+    """Decode attention straight from the FP8 pages: q ``[B, Hq, D]`` bf16 (one token per
+    sequence), pool ``[n_pages, 2, Hkv, P, D]`` uint8, scales ``[2, Hkv]`` fp32 ->
+    ``[B, Hq, D]`` bf16 = softmax(sm_scale * q K^T) V over positions < seq_lens[b], with
+    K, V = decoded codes times their head's scale (query head i reads kv head
+    i // (Hq / Hkv)).  ``sm_scale`` defaults to 1/sqrt(D)."""
+    N.ensure_gpu()
+    if pool_layer.dim() != 5 or pool_layer.dtype != torch.uint8 or pool_layer.shape[1] != 2:
+        raise ValueError("pool_layer must be uint8 [n_pages, 2, Hkv, P, D]")
+    n_pages, _, Hkv, P, D = pool_layer.shape
+    if q.dim() != 3 or q.dtype != torch.bfloat16 or q.shape[2] != D:
+        raise ValueError(f"q must be bf16 [B, Hq, {D}]")
+    B, Hq, _ = q.shape
+    if Hq % Hkv:
+        raise ValueError("the number of query heads must be a multiple of the number of kv heads")
+    if scales_layer.shape != (2, Hkv) or scales_layer.dtype != torch.float32:
+        raise ValueError(f"scales_layer must be float32 [2, {Hkv}]")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32 or block_tables.dim() != 2:
+        raise ValueError("block_tables [B, max_blocks] and seq_lens [B] must be int32")
+    if block_tables.shape[0] != B or seq_lens.numel() != B:
+        raise ValueError("block_tables and seq_lens need one row per sequence")
+    q = q.contiguous()
+    for name, t in (("q", q), ("pool_layer", pool_layer), ("scales_layer", scales_layer),
+                    ("block_tables", block_tables), ("seq_lens", seq_lens)):
+        N.require_device(t, name)
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=q.device)
+    elif out.shape != (B, Hq, D) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous bf16 {(B, Hq, D)}")
+    lib = N.load()
+    mb = block_tables.shape[1]
+    ws = _workspace(lib.zx_paged_attention_decode_workspace_bytes(B, Hq, D, mb, P), q.device)
+    err = _err_word(q.device)
+    N.check(lib.zx_paged_attention_decode(
+        N.ptr(q), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer), N.ptr(block_tables), mb,
+        N.ptr(seq_lens), B, float(D ** -0.5 if sm_scale is None else sm_scale), N.ptr(out), N.ptr(err), N.ptr(ws),
+        ws.numel(), N.stream_ptr(q.device)), "paged_attention_decode")
+    if check:
+        _raise_kernel_error(err, "paged_attention_decode")
+    return out
+
+
 # ------------------------------------------------------------------ Belady
 
 def belady_argmax(keys: torch.Tensor, resident: torch.Tensor) -> torch.Tensor:
