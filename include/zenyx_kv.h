@@ -153,8 +153,8 @@ int zx_kv_gather_dequant(const uint8_t *pool, int64_t n_pages, int32_t n_heads, 
  * 0 gives zeros; rows with an out-of-range page id or a position past max_blocks*P are
  * left out and flagged in *err.  out: [n_seqs][n_q_heads][head_dim] bf16.  workspace:
  * zx_paged_attention_decode_workspace_bytes() device bytes (per-split partial results). */
-size_t zx_paged_attention_decode_workspace_bytes(int32_t n_seqs, int32_t n_q_heads, int32_t head_dim,
-                                                 int32_t max_blocks, int32_t page_size);
+size_t zx_paged_attention_decode_workspace_bytes(int32_t n_seqs, int32_t n_q_heads, int32_t n_kv_heads,
+                                                 int32_t head_dim, int32_t max_blocks, int32_t page_size);
 int zx_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, const uint8_t *pool, int64_t n_pages,
                               int32_t n_kv_heads, int32_t head_dim, int32_t page_size, const float *scales,
                               const int32_t *block_tables, int32_t max_blocks, const int32_t *seq_lens,

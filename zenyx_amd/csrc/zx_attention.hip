@@ -8,7 +8,7 @@
 // attention reads 2 B more).
 //
 // Split-K flash decoding.  Pass 1 (paged_decode_partial_kernel): a block owns one
-// (sequence, kv head, group of G query heads, split of ATT_SPLIT positions); lane l of a
+// (sequence, kv head, group of G query heads, split of positions); lane l of a
 // wave owns 16 channels (dc = l % LPT, LPT = D / 16 lanes per token) of token slot
 // l / LPT, so K and V rows are read as 16-byte loads that cover whole page rows.  Scale
 // factors fold into q (q * scale_k * sm_scale * log2 e) and into the end (scale_v), so
@@ -25,15 +25,21 @@ namespace zx {
 constexpr int ATT_THREADS = 256;  // 4 waves
 constexpr int ATT_WAVES = ATT_THREADS / 64;
 constexpr int ATT_U = 4;          // passes per online-softmax step
-constexpr int ATT_SPLIT = 1024;   // positions per block
+constexpr int ATT_SPLIT_MIN = 1024;  // positions per block: a multiple of this, chosen per call
 constexpr float ATT_LOG2E = 1.4426950408889634f;
 
 struct AttnGeom {
   int32_t n_q_heads, n_kv_heads, head_dim, page_size, max_blocks, n_seqs;
-  int32_t n_splits;
+  int32_t n_splits, split_len;  // blocks per (sequence, head group), positions per block
+  uint32_t p_magic;  // t / page_size = (t * p_magic) >> (31 + p_shift) for t < 2^31
+  int32_t p_shift;
   int64_t n_pages;
   float sm_scale;
 };
+
+__device__ __forceinline__ uint32_t page_of(const AttnGeom &g, uint32_t t) {
+  return (uint32_t)(((uint64_t)t * g.p_magic) >> (31 + g.p_shift));
+}
 
 // 16 e4m3 codes -> 16 fp32 values (exact).
 __device__ __forceinline__ void decode16(uint4 c, float (&f)[16]) {
@@ -43,47 +49,92 @@ __device__ __forceinline__ void decode16(uint4 c, float (&f)[16]) {
   e4m3x4_decode(c.w, f[12], f[13], f[14], f[15]);
 }
 
-__device__ __forceinline__ float xor_sum(float v, int mask) { return v + __shfl_xor(v, mask, 64); }
-__device__ __forceinline__ float xor_max(float v, int mask) { return fmaxf(v, __shfl_xor(v, mask, 64)); }
+typedef __bf16 att_bf2 __attribute__((ext_vector_type(2)));
+// 16 e4m3 codes -> 8 bf16 pairs (exact: every e4m3 value is a bf16 value).
+__device__ __forceinline__ void decode16_bf16(uint4 c, uint32_t (&b)[8]) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    b[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[i], 1.0f, false));
+    b[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[i], 1.0f, true));
+  }
+}
+
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// Sum over aligned groups of N lanes inside a 16-lane row, by DPP (quad_perm swaps, then
+// half-row and row mirrors, which pair groups whose lanes already agree; every lane of a
+// group ends with the result).
+template <int N> __device__ __forceinline__ float group_sum(float v) {
+  if (N >= 2) v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (N >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (N >= 8) v += dpp<0x141>(v);  // row_half_mirror
+  if (N >= 16) v += dpp<0x140>(v); // row_mirror
+  return v;
+}
+// Across 16-lane rows: the lane 16 and 32 positions away (ds_bpermute).  (The
+// v_permlane16/32_swap builtins return one of their two outputs twice with this
+// compiler, so they are not used.)
+__device__ __forceinline__ float rows_sum(float v) {
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
+__device__ __forceinline__ float rows_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+// Max / sum over the token slots of a wave for each channel group: lanes l, l + LPT,
+// l + 2 LPT, ... (row_ror by 4 and 8 inside a 16-lane row keeps l % LPT, then the row
+// pairs).
+template <int LPT> __device__ __forceinline__ float slots_max(float v) {
+  if (LPT <= 4) v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
+  if (LPT <= 8) v = fmaxf(v, dpp<0x128>(v));  // row_ror:8
+  return rows_max(v);
+}
+template <int LPT> __device__ __forceinline__ float slots_sum(float v) {
+  if (LPT <= 4) v += dpp<0x124>(v);
+  if (LPT <= 8) v += dpp<0x128>(v);
+  return rows_sum(v);
+}
 
 // Partial layout in the workspace: [B][Hq][n_splits][2 + D] fp32 = (m, l, acc[D]) with m
 // in the exp2 domain; a split without valid positions writes m = -inf, l = 0, acc = 0.
-template <int G, int D>
+template <int G, int D, bool FAST>
 __global__ void __launch_bounds__(ATT_THREADS)
 paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8_t *__restrict__ pool,
                             const float *__restrict__ scales, const int32_t *__restrict__ block_tables,
                             const int32_t *__restrict__ seq_lens, float *__restrict__ part, int32_t *err) {
   constexpr int LPT = D / 16;   // lanes per token
   constexpr int TPW = 64 / LPT;  // token slots per wave pass
+  constexpr int STEP = ATT_U * TPW;
   const int split = blockIdx.x;
   const int grp_blocks = g.n_q_heads / g.n_kv_heads / G;  // query-head groups per kv head
   const int h = blockIdx.y / grp_blocks;
   const int hq0 = h * (g.n_q_heads / g.n_kv_heads) + (blockIdx.y % grp_blocks) * G;
   const int b = blockIdx.z;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar addressing
   const int ts = lane / LPT, dc = lane % LPT;
   const int32_t len = seq_lens[b];
-  const int64_t t_begin = (int64_t)split * ATT_SPLIT;
-  const int64_t t_end = min(min((int64_t)len, (int64_t)g.max_blocks * g.page_size), t_begin + ATT_SPLIT);
+  const int64_t t_begin = (int64_t)split * g.split_len;
+  const int64_t t_end = min(min((int64_t)len, (int64_t)g.max_blocks * g.page_size), t_begin + g.split_len);
   const int64_t page_bytes = 2LL * g.n_kv_heads * g.page_size * D;
   const uint8_t *kbase = pool + (int64_t)h * g.page_size * D + dc * 16;
-  const uint8_t *vbase = kbase + (int64_t)g.n_kv_heads * g.page_size * D;
+  const int64_t v_off = (int64_t)g.n_kv_heads * g.page_size * D;
   const int32_t *bt = block_tables + (int64_t)b * g.max_blocks;
 
-  // q' = q * scale_k * sm_scale * log2(e) for this lane's 16 channels
-  float qf[G][16];
-  const float qs = scales[h] * g.sm_scale * ATT_LOG2E;
+  // q as bf16 pairs for this lane's 16 channels; the score scale (scale_k * sm_scale *
+  // log2 e) multiplies the reduced dot product
+  uint32_t qb[G][8];
 #pragma unroll
   for (int j = 0; j < G; ++j) {
     const uint4 *qp = reinterpret_cast<const uint4 *>(q + ((int64_t)b * g.n_q_heads + hq0 + j) * D + dc * 16);
     const uint4 a = qp[0], c = qp[1];
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      qf[j][2 * i] = bf_lo(w[i]) * qs;
-      qf[j][2 * i + 1] = bf_hi(w[i]) * qs;
-    }
+    qb[j][0] = a.x; qb[j][1] = a.y; qb[j][2] = a.z; qb[j][3] = a.w;
+    qb[j][4] = c.x; qb[j][5] = c.y; qb[j][6] = c.z; qb[j][7] = c.w;
   }
+  const float qs = scales[h] * g.sm_scale * ATT_LOG2E;
 
   float m[G], l[G], acc[G][16];
 #pragma unroll
@@ -97,56 +148,77 @@ paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const ui
   int32_t e = split == 0 && threadIdx.x == 0 && blockIdx.y == 0 && (int64_t)len > (int64_t)g.max_blocks * g.page_size
                   ? ZX_KERR_POS_RANGE : 0;
 
-  // wave w takes steps w, w + 4, ...; a step is ATT_U passes of TPW consecutive positions
-  for (int64_t t0 = t_begin + (int64_t)wave * ATT_U * TPW; t0 < t_end; t0 += (int64_t)ATT_WAVES * ATT_U * TPW) {
-    uint4 kc[ATT_U], vc[ATT_U];
-    bool ok[ATT_U];
+  // K/V of one step (ATT_U passes of TPW positions) into registers.  FAST (page size a
+  // multiple of TPW): the TPW positions of a pass share one page, so the page id is a
+  // scalar load and the loads go through a resource whose num_records ends at the last
+  // valid row; otherwise every lane looks its page up.  ok marks positions with data.
+  auto load_step = [&](int64_t t0, uint4 (&kc)[ATT_U], uint4 (&vc)[ATT_U], bool (&ok)[ATT_U]) {
 #pragma unroll
     for (int u = 0; u < ATT_U; ++u) {
-      const int64_t t = t0 + u * TPW + ts;
-      ok[u] = false;
-      kc[u] = vc[u] = make_uint4(0, 0, 0, 0);
-      if (t < t_end) {
-        const int64_t bi = t / g.page_size;
-        if (bi >= g.max_blocks) {
-          e |= ZX_KERR_POS_RANGE;
-        } else {
+      if constexpr (FAST) {
+        const int64_t tp = t0 + u * TPW;  // uniform
+        const int64_t rows = min((int64_t)TPW, t_end - tp);
+        int nrec = 0;
+        const uint8_t *src = pool;
+        if (rows > 0) {
+          const uint32_t bi = page_of(g, (uint32_t)tp);
           const int64_t page = bt[bi];
-          if (page < 0 || page >= g.n_pages) {
-            e |= ZX_KERR_PAGE_RANGE;
-          } else {
-            const int64_t off = page * page_bytes + (t - bi * g.page_size) * D;
-            kc[u] = *reinterpret_cast<const uint4 *>(kbase + off);
-            vc[u] = *reinterpret_cast<const uint4 *>(vbase + off);
-            ok[u] = true;
+          if (page < 0 || page >= g.n_pages) e |= ZX_KERR_PAGE_RANGE;
+          else {
+            src = pool + page * page_bytes + (int64_t)h * g.page_size * D + (tp - (int64_t)bi * g.page_size) * D;
+            nrec = (int)rows * D;
           }
         }
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src), (short)0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src + (nrec ? v_off : 0)), (short)0, nrec, 0x00020000);
+        typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+        const v4u a = __builtin_amdgcn_raw_buffer_load_b128(rk, ts * D + dc * 16, 0, 2);
+        const v4u c = __builtin_amdgcn_raw_buffer_load_b128(rv, ts * D + dc * 16, 0, 2);
+        kc[u] = make_uint4(a.x, a.y, a.z, a.w);
+        vc[u] = make_uint4(c.x, c.y, c.z, c.w);
+        ok[u] = ts * D < nrec;
+      } else {
+        const int64_t t = t0 + u * TPW + ts;
+        int64_t off = -1;
+        if (t < t_end) {
+          const uint32_t bi = page_of(g, (uint32_t)t);
+          const int64_t page = bt[bi];
+          if (page < 0 || page >= g.n_pages) e |= ZX_KERR_PAGE_RANGE;
+          else off = page * page_bytes + (t - (int64_t)bi * g.page_size) * D;
+        }
+        ok[u] = off >= 0;
+        const uint8_t *kp = kbase + (off >= 0 ? off : 0);
+        kc[u] = ok[u] ? *reinterpret_cast<const uint4 *>(kp) : make_uint4(0, 0, 0, 0);
+        vc[u] = ok[u] ? *reinterpret_cast<const uint4 *>(kp + v_off) : make_uint4(0, 0, 0, 0);
       }
     }
-    // scores (exp2 domain), reduced over the LPT lanes of each token
+  };
+
+  auto compute_step = [&](const uint4 (&kc)[ATT_U], const uint4 (&vc)[ATT_U], const bool (&ok)[ATT_U]) {
     float s[ATT_U][G];
 #pragma unroll
     for (int u = 0; u < ATT_U; ++u) {
-      float k[16];
-      decode16(kc[u], k);
+      uint32_t kb[8];
+      decode16_bf16(kc[u], kb);
 #pragma unroll
       for (int j = 0; j < G; ++j) {
         float a = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) a = __builtin_fmaf(qf[j][i], k[i], a);
-#pragma unroll
-        for (int mk = 1; mk < LPT; mk <<= 1) a = xor_sum(a, mk);
-        s[u][j] = ok[u] ? a : -INFINITY;
+        for (int i = 0; i < 8; ++i)
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(att_bf2, qb[j][i]), __builtin_bit_cast(att_bf2, kb[i]),
+                                              a, false);
+        a = group_sum<LPT>(a);
+        s[u][j] = ok[u] ? a * qs : -INFINITY;
       }
     }
-    // online softmax update per query head
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       float mx = s[0][j];
 #pragma unroll
       for (int u = 1; u < ATT_U; ++u) mx = fmaxf(mx, s[u][j]);
-#pragma unroll
-      for (int mk = LPT; mk < 64; mk <<= 1) mx = xor_max(mx, mk);
+      mx = slots_max<LPT>(mx);
       const float m_new = fmaxf(m[j], mx);
       const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[j] - m_new);
       m[j] = m_new;
@@ -167,17 +239,31 @@ paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const ui
         for (int i = 0; i < 16; ++i) acc[j][i] = __builtin_fmaf(s[u][j], v[i], acc[j][i]);
       }
     }
+  };
+
+  // wave w takes steps w, w + 4, ...; the next step's loads are issued before the
+  // current step is computed
+  const int64_t stride = (int64_t)ATT_WAVES * STEP;
+  int64_t t0 = t_begin + (int64_t)wave * STEP;
+  uint4 ka[ATT_U], va[ATT_U], kb2[ATT_U], vb2[ATT_U];
+  bool oka[ATT_U], okb[ATT_U];
+  if (t0 < t_end) load_step(t0, ka, va, oka);
+  while (t0 < t_end) {
+    if (t0 + stride < t_end) load_step(t0 + stride, kb2, vb2, okb);
+    compute_step(ka, va, oka);
+    t0 += stride;
+    if (t0 >= t_end) break;
+    if (t0 + stride < t_end) load_step(t0 + stride, ka, va, oka);
+    compute_step(kb2, vb2, okb);
+    t0 += stride;
   }
 
   // token slots of the wave -> one value per (head, channel) in every lane of slot 0
 #pragma unroll
   for (int j = 0; j < G; ++j) {
+    l[j] = slots_sum<LPT>(l[j]);
 #pragma unroll
-    for (int mk = LPT; mk < 64; mk <<= 1) {
-      l[j] = xor_sum(l[j], mk);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[j][i] = xor_sum(acc[j][i], mk);
-    }
+    for (int i = 0; i < 16; ++i) acc[j][i] = slots_sum<LPT>(acc[j][i]);
   }
   // combine the block's waves through LDS
   __shared__ float sm_m[ATT_WAVES][G], sm_l[ATT_WAVES][G];
@@ -255,20 +341,41 @@ paged_decode_combine_kernel(const float *__restrict__ part, AttnGeom g, const fl
 
 using namespace zx;
 
-static int64_t att_splits(int32_t max_blocks, int32_t page_size) {
-  return ceil_div((int64_t)max_blocks * page_size, ATT_SPLIT);
+// Positions per block: a multiple of ATT_SPLIT_MIN, as long as the grid still has about
+// two blocks per CU (long sequences in small batches get more, shorter splits).
+static void att_splits(int32_t n_seqs, int32_t head_groups, int32_t max_blocks, int32_t page_size,
+                       int64_t &n_splits, int64_t &split_len) {
+  const int64_t max_len = (int64_t)max_blocks * page_size;
+  const int64_t most = ceil_div(max_len, ATT_SPLIT_MIN);
+  int64_t want = ceil_div(2LL * num_cus(), (int64_t)n_seqs * head_groups);
+  want = want < 1 ? 1 : (want > most ? most : want);
+  split_len = ceil_div(ceil_div(max_len, want), ATT_SPLIT_MIN) * ATT_SPLIT_MIN;
+  n_splits = ceil_div(max_len, split_len);
 }
 
-extern "C" size_t zx_paged_attention_decode_workspace_bytes(int32_t n_seqs, int32_t n_q_heads, int32_t head_dim,
-                                                            int32_t max_blocks, int32_t page_size) {
-  if (n_seqs <= 0 || n_q_heads <= 0 || head_dim <= 0 || max_blocks <= 0 || page_size <= 0) return 0;
-  return (size_t)n_seqs * n_q_heads * att_splits(max_blocks, page_size) * (2 + head_dim) * sizeof(float);
+static int32_t att_group(int32_t n_q_heads, int32_t n_kv_heads) {  // query heads per block
+  const int grp = n_q_heads / n_kv_heads;
+  return grp % 4 == 0 ? 4 : (grp % 2 == 0 ? 2 : 1);
+}
+
+extern "C" size_t zx_paged_attention_decode_workspace_bytes(int32_t n_seqs, int32_t n_q_heads, int32_t n_kv_heads,
+                                                            int32_t head_dim, int32_t max_blocks, int32_t page_size) {
+  if (n_seqs <= 0 || n_q_heads <= 0 || n_kv_heads <= 0 || n_q_heads % n_kv_heads || head_dim <= 0 ||
+      max_blocks <= 0 || page_size <= 0)
+    return 0;
+  int64_t n_splits, split_len;
+  att_splits(n_seqs, n_q_heads / att_group(n_q_heads, n_kv_heads), max_blocks, page_size, n_splits, split_len);
+  return (size_t)n_seqs * n_q_heads * n_splits * (2 + head_dim) * sizeof(float);
 }
 
 template <int G, int D>
 static int launch_partial(dim3 grid, hipStream_t st, const uint16_t *q, const AttnGeom &g, const uint8_t *pool,
                           const float *scales, const int32_t *bt, const int32_t *sl, float *part, int32_t *err) {
-  paged_decode_partial_kernel<G, D><<<grid, ATT_THREADS, 0, st>>>(q, g, pool, scales, bt, sl, part, err);
+  constexpr int TPW = 64 / (D / 16);
+  if (g.page_size % TPW == 0)
+    paged_decode_partial_kernel<G, D, true><<<grid, ATT_THREADS, 0, st>>>(q, g, pool, scales, bt, sl, part, err);
+  else
+    paged_decode_partial_kernel<G, D, false><<<grid, ATT_THREADS, 0, st>>>(q, g, pool, scales, bt, sl, part, err);
   return check_launch("paged_decode_partial");
 }
 
@@ -296,11 +403,12 @@ extern "C" int zx_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, c
   if (!(head_dim == 64 || head_dim == 128 || head_dim == 256))
     return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: head_dim %d not in {64, 128, 256}", head_dim);
   if (n_seqs > 65535) return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: more than 65535 sequences");
-  const size_t need = zx_paged_attention_decode_workspace_bytes(n_seqs, n_q_heads, head_dim, max_blocks, page_size);
+  const size_t need =
+      zx_paged_attention_decode_workspace_bytes(n_seqs, n_q_heads, n_kv_heads, head_dim, max_blocks, page_size);
   if (!workspace || workspace_bytes < need)
     return fail(ZX_ERR_WORKSPACE, "paged_attention_decode: workspace %zu < %zu bytes", workspace_bytes, need);
   const int grp = n_q_heads / n_kv_heads;
-  const int G = grp % 4 == 0 ? 4 : (grp % 2 == 0 ? 2 : 1);  // query heads per block
+  const int G = att_group(n_q_heads, n_kv_heads);
   AttnGeom g;
   g.n_q_heads = n_q_heads;
   g.n_kv_heads = n_kv_heads;
@@ -308,11 +416,20 @@ extern "C" int zx_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, c
   g.page_size = page_size;
   g.max_blocks = max_blocks;
   g.n_seqs = n_seqs;
-  const int64_t n_splits = att_splits(max_blocks, page_size);
-  if (n_splits >= (1LL << 31)) return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: sequences too long");
+  int64_t n_splits, split_len;
+  att_splits(n_seqs, n_q_heads / G, max_blocks, page_size, n_splits, split_len);
+  if (n_splits >= (1LL << 31) || split_len >= (1LL << 31))
+    return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: sequences too long");
   g.n_splits = (int32_t)n_splits;
+  g.split_len = (int32_t)split_len;
   g.n_pages = n_pages;
   g.sm_scale = sm_scale;
+  {  // magic division by the page size for positions below 2^31
+    int sh = 0;
+    while ((1LL << sh) < page_size) ++sh;
+    g.p_shift = sh;
+    g.p_magic = (uint32_t)(((1ULL << (31 + sh)) + (uint64_t)page_size - 1) / (uint64_t)page_size);
+  }
   const int64_t gy = (int64_t)n_kv_heads * (grp / G);
   if (gy > 65535) return fail(ZX_ERR_UNSUPPORTED, "paged_attention_decode: too many heads");
   hipStream_t st = as_stream(stream);

@@ -277,7 +277,7 @@ def paged_attention_decode(q: torch.Tensor, pool_layer: torch.Tensor, scales_lay
         raise ValueError(f"out must be contiguous bf16 {(B, Hq, D)}")
     lib = N.load()
     mb = block_tables.shape[1]
-    ws = _workspace(lib.zx_paged_attention_decode_workspace_bytes(B, Hq, D, mb, P), q.device)
+    ws = _workspace(lib.zx_paged_attention_decode_workspace_bytes(B, Hq, Hkv, D, mb, P), q.device)
     err = _err_word(q.device)
     N.check(lib.zx_paged_attention_decode(
         N.ptr(q), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer), N.ptr(block_tables), mb,
