@@ -6,7 +6,7 @@ U[1k, 8k] tokens, 5% of each sequence's (layer, head) pairs x50), one step = one
 of every layer, inputs already resident in HBM.  Reported as algorithmic GB/s
 (3 bytes per KV element + scales + block tables) and as a fraction of the 8 TB/s HBM3E
 peak.  Also measured: configs[2] (paged gather + dequant, 64 x 32k decode, 300k-page
-pool), configs[3] (Belady tiering of a ring-attention trace: evictions/s, plus the
+pool; plus decode attention computed straight from those FP8 pages), configs[3] (Belady tiering of a ring-attention trace: evictions/s, plus the
 pinned-host tier moves of one layer overlapped with compute) and configs[4] (80-layer
 70B-shape share streamed through 60 HBM layer slots and pinned DRAM: per-kernel append
 and gather GB/s, D2H / H2D GB/s).
@@ -453,6 +453,24 @@ def main():
         if not args.skip_cpu:
             log("CPU baseline (gather)")
             gather["cpu_baseline"] = cpu_baseline_gather(G)
+        # decode attention straight from the same FP8 pages (one query token per sequence,
+        # 32 query heads over the 8 KV heads, as Llama-3-8B)
+        Hq = 32
+        qd = torch.randn((G["B"], Hq, G["D"]), device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+        qd = qd.to(torch.bfloat16)
+        od = torch.empty_like(qd)
+        astep = lambda: kv.paged_attention_decode(qd, G["pool"], sc, G["bt"], G["seq_lens"], out=od)
+        ms_a, _, _ = time_steps(torch, astep, args.steps, args.warmup)
+        alg_a = G["N"] + 4 * G["B"] * (G["T"] // G["P"]) + 4 * 2 * G["H"] + 2 * 2 * G["B"] * Hq * G["D"]
+        gb_a = alg_a / (ms_a * 1e-3) / 1e9
+        log(f"attention decode from FP8 pages: {ms_a:.3f} ms/step, {gb_a:.1f} GB/s ({100 * gb_a / HBM_PEAK_GBPS:.1f}% "
+            f"of peak)")
+        gather["attention_decode"] = {
+            "GBps": round(gb_a, 2), "ms_per_step": round(ms_a, 4), "frac": round(gb_a / HBM_PEAK_GBPS, 4),
+            "algorithmic_bytes_per_step": alg_a,
+            "workload": "paged_decode_partial/combine: 64 seqs x 32768 positions, 32 query heads over 8 KV heads, "
+                        "D=128, reading the configs[2] pool (1 B per K/V element)"}
+        del qd, od
         out["gather_dequant"] = gather
         if "value" not in out:
             out.update({"value": round(gb_g, 2), "ms_per_step": round(ms_g, 4),
