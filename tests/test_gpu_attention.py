@@ -77,6 +77,8 @@ def make_case(Hq, Hkv, D, P, lens, seed, n_pages=None, nan_codes=False):
     (8, 8, 64, 16, [5, 64, 2100]),                                  # no grouping, D = 64
     (12, 4, 256, 32, [700, 31, 2049]),                              # groups of 3 (one head per block)
     (16, 8, 128, 5, [1, 333, 1500]),                                # page size 5, pairs of heads
+    (8, 8, 128, 32, [40, 1, 2222]),                                 # matrix-core variant, one head
+    (16, 8, 128, 16, [17, 4000]),                                   # matrix-core variant, pairs
 ])
 def test_paged_attention_decode_matches_oracle(dev, Hq, Hkv, D, P, lens):
     q, pool, scales, bt, lens = make_case(Hq, Hkv, D, P, lens, seed=Hq + D + P)
@@ -100,9 +102,11 @@ def test_paged_attention_decode_large_scores_and_custom_scale(dev):
     assert_within_one_ulp(bits16(got), want, v_colmax(pool, scales, bt, lens, 32))
 
 
-def test_paged_attention_decode_nan_codes_and_bad_pages(dev):
-    """NaN codes make the affected heads NaN; an out-of-range page id is skipped and flagged."""
-    q, pool, scales, bt, lens = make_case(8, 2, 64, 16, [100, 200, 50], seed=6)
+@pytest.mark.parametrize("D", [64, 128])
+def test_paged_attention_decode_nan_codes_and_bad_pages(dev, D):
+    """NaN codes make the affected heads NaN; an out-of-range page id is skipped and flagged
+    (D = 64: VALU kernel, D = 128: matrix-core kernel)."""
+    q, pool, scales, bt, lens = make_case(8, 2, D, 16, [100, 200, 50], seed=6)
     pool[bt[1, 3], 0, 1, 4, 7] = 0x7F  # a NaN code in sequence 1, kv head 1
     bt_bad = bt.copy()
     bt_bad[2, 1] = pool.shape[0] + 10

@@ -213,20 +213,34 @@ paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const ui
         s[u][j] = ok[u] ? a * qs : -INFINITY;
       }
     }
+    // running max per head (the same in every lane); the accumulators are rescaled only
+    // on the steps where some head's max grew (a scalar branch: rare after the first
+    // steps of a split)
+    float m_new[G];
+    bool grew = false;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       float mx = s[0][j];
 #pragma unroll
       for (int u = 1; u < ATT_U; ++u) mx = fmaxf(mx, s[u][j]);
       mx = slots_max<LPT>(mx);
-      const float m_new = fmaxf(m[j], mx);
-      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[j] - m_new);
-      m[j] = m_new;
-      l[j] *= alpha;
+      m_new[j] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fmaxf(m[j], mx))));
+      grew = grew || m_new[j] > m[j];
+    }
+    if (grew) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[j][i] *= alpha;
+      for (int j = 0; j < G; ++j) {
+        const float alpha = m_new[j] == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[j] - m_new[j]);
+        m[j] = m_new[j];
+        l[j] *= alpha;
 #pragma unroll
-      for (int u = 0; u < ATT_U; ++u) s[u][j] = m_new == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[u][j] - m_new);
+        for (int i = 0; i < 16; ++i) acc[j][i] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+#pragma unroll
+      for (int u = 0; u < ATT_U; ++u) s[u][j] = m[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[u][j] - m[j]);
     }
 #pragma unroll
     for (int u = 0; u < ATT_U; ++u) {
@@ -274,6 +288,274 @@ paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const ui
 #pragma unroll
       for (int i = 0; i < 16; ++i) sm_acc[wave][j][dc * 16 + i] = acc[j][i];
       if (dc == 0) {
+        sm_m[wave][j] = m[j];
+        sm_l[wave][j] = l[j];
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += ATT_THREADS) {
+    const int j = idx / D, d = idx % D;
+    float M = sm_m[0][j];
+#pragma unroll
+    for (int w = 1; w < ATT_WAVES; ++w) M = fmaxf(M, sm_m[w][j]);
+    float a = 0.0f, ll = 0.0f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; ++w) {
+      const float f = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm_m[w][j] - M);
+      a += f * sm_acc[w][j][d];
+      ll += f * sm_l[w][j];
+    }
+    float *pp = part + (((int64_t)b * g.n_q_heads + hq0 + j) * g.n_splits + split) * (2 + D);
+    pp[2 + d] = a;
+    if (d == 0) {
+      pp[0] = M;
+      pp[1] = ll;
+    }
+  }
+  if (e && err) atomicOr(err, e);
+}
+
+// Matrix-core variant of pass 1 for D = 128 and page sizes that are a multiple of 16:
+// q.K^T and P.V run on v_mfma_f32_16x16x32_bf16 with the (up to 4) query heads of the
+// block as the M rows (padded to 16).  A wave takes steps of 32 positions (two 16-token
+// tiles, each inside one page).  Lane l loads, for token l % 16 of a tile, the 32 K and V
+// codes of channels 32 (l / 16) ..+32, converts them to bf16 exactly and
+//   * uses the K codes directly as the B operand of q.K^T (k = channel, any consistent
+//     permutation of the channels works since the product sums over them);
+//   * writes the V values transposed into LDS (V^T[channel][token], bf16, 80-byte rows,
+//     16-byte token chunks XOR-swizzled by channel / 32 so the four lane groups of a
+//     store hit different banks), from where each lane reads the 8 consecutive tokens
+//     of one channel that the B operand of P.V needs.
+// P goes through LDS as fp32 into the A-operand layout and is split into bf16 hi + lo
+// (two MFMAs), which keeps the products at ~2^-17 relative error.  Scores land in the C
+// layout: lanes 0-15 hold heads 0-3 of token l % 16, so the softmax bookkeeping is a
+// 16-lane DPP reduction; the O accumulators (8 tiles of 16 channels) live in MFMA
+// results, rows = heads.
+typedef __bf16 att_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float att_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int att_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int AM_VROW = 80;                 // bytes per channel row of V^T (64 + 16 pad)
+constexpr int AM_VBYTES = 128 * AM_VROW;    // one wave's V^T (32 tokens)
+constexpr int AM_PBYTES = 4 * 32 * 4;       // one wave's P (4 heads x 32 tokens fp32)
+
+__device__ __forceinline__ float row16_max(float v) {  // max over lanes 0-15 of each row
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  return fmaxf(v, dpp<0x140>(v));
+}
+
+template <int G>
+__global__ void __launch_bounds__(ATT_THREADS)
+paged_decode_mfma_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8_t *__restrict__ pool,
+                         const float *__restrict__ scales, const int32_t *__restrict__ block_tables,
+                         const int32_t *__restrict__ seq_lens, float *__restrict__ part, int32_t *err) {
+  constexpr int D = 128;
+  const int split = blockIdx.x;
+  const int grp_blocks = g.n_q_heads / g.n_kv_heads / G;
+  const int h = blockIdx.y / grp_blocks;
+  const int hq0 = h * (g.n_q_heads / g.n_kv_heads) + (blockIdx.y % grp_blocks) * G;
+  const int b = blockIdx.z;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, kg = lane >> 4;  // MFMA column / k-group
+  const int32_t len = seq_lens[b];
+  const int64_t t_begin = (int64_t)split * g.split_len;
+  const int64_t t_end = min(min((int64_t)len, (int64_t)g.max_blocks * g.page_size), t_begin + g.split_len);
+  const int64_t page_bytes = 2LL * g.n_kv_heads * g.page_size * D;
+  const int64_t head_off = (int64_t)h * g.page_size * D;
+  const int64_t v_off = (int64_t)g.n_kv_heads * g.page_size * D;
+  const int32_t *bt = block_tables + (int64_t)b * g.max_blocks;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[ATT_WAVES][AM_VBYTES + AM_PBYTES];
+  uint8_t *vt = lds[wave];
+  float *pl = reinterpret_cast<float *>(lds[wave] + AM_VBYTES);
+
+  // q rows (heads) as the A operand: lane l holds head n, channels 32 kg + 8 c .. +8
+  att_bf16x8 qa[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    att_u32x4 w = {0u, 0u, 0u, 0u};
+    if (n < G) {
+      const uint4 x = *reinterpret_cast<const uint4 *>(q + ((int64_t)b * g.n_q_heads + hq0 + n) * D + kg * 32 + c * 8);
+      w = att_u32x4{x.x, x.y, x.z, x.w};
+    }
+    qa[c] = __builtin_bit_cast(att_bf16x8, w);
+  }
+  const float qs = scales[h] * g.sm_scale * ATT_LOG2E;
+
+  att_f32x4 o[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) o[t] = att_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m[4], l[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.0f;
+  }
+  int32_t e = split == 0 && threadIdx.x == 0 && blockIdx.y == 0 && (int64_t)len > (int64_t)g.max_blocks * g.page_size
+                  ? ZX_KERR_POS_RANGE : 0;
+
+  // one 16-token tile: K and V codes of token tp + n, channels 32 kg ..+32; rows = valid tokens
+  auto load_tile = [&](int64_t tp, uint4 (&kc)[2], uint4 (&vc)[2], int &rows) {
+    rows = (int)max((int64_t)0, min((int64_t)16, t_end - tp));
+    int nrec = 0;
+    const uint8_t *src = pool;
+    if (rows > 0) {
+      const uint32_t bi = page_of(g, (uint32_t)tp);
+      const int64_t page = bt[bi];
+      if (page < 0 || page >= g.n_pages) {
+        e |= ZX_KERR_PAGE_RANGE;
+        rows = 0;
+      } else {
+        src = pool + page * page_bytes + head_off + (tp - (int64_t)bi * g.page_size) * D;
+        nrec = rows * D;
+      }
+    }
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src), (short)0, nrec,
+                                                                        0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(src + (nrec ? v_off : 0)), (short)0, nrec, 0x00020000);
+    const int off = n * D + kg * 32;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const att_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16 * i, 0, 2);
+      const att_u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(rv, off + 16 * i, 0, 2);
+      kc[i] = make_uint4(a.x, a.y, a.z, a.w);
+      vc[i] = make_uint4(c.x, c.y, c.z, c.w);
+    }
+  };
+
+  auto compute_step = [&](const uint4 (&kc)[2][2], const uint4 (&vc)[2][2], const int (&rows)[2]) {
+    // scores: S[head][token] for both tiles
+    float sv[2][4];
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+      uint32_t kb[16];
+      uint32_t (&k0)[8] = *reinterpret_cast<uint32_t (*)[8]>(&kb[0]);
+      uint32_t (&k1)[8] = *reinterpret_cast<uint32_t (*)[8]>(&kb[8]);
+      decode16_bf16(kc[T][0], k0);
+      decode16_bf16(kc[T][1], k1);
+      att_f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            qa[c], __builtin_bit_cast(att_bf16x8, att_u32x4{kb[4 * c], kb[4 * c + 1], kb[4 * c + 2], kb[4 * c + 3]}),
+            sc, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sv[T][j] = (kg == 0 && j < G && n < rows[T]) ? sc[j] * qs : -INFINITY;
+    }
+    float m_new[4];
+    bool grew = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float mx = row16_max(fmaxf(sv[0][j], sv[1][j]));
+      m_new[j] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fmaxf(m[j], mx))));
+      grew = grew || m_new[j] > m[j];
+    }
+    if (grew) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float alpha = m_new[j] == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[j] - m_new[j]);
+        m[j] = m_new[j];
+        l[j] *= alpha;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t][j] *= alpha;
+      }
+    }
+    // P (fp32) into LDS as [head][token]
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = m[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[T][j] - m[j]);
+        l[j] += p;
+        if (kg == 0) pl[j * 32 + T * 16 + n] = p;
+      }
+    // V^T into LDS: token t = 16 T + n, channels 32 kg + 2 i, +1
+#pragma unroll
+    for (int T = 0; T < 2; ++T) {
+      uint32_t vb[16];
+      uint32_t (&v0)[8] = *reinterpret_cast<uint32_t (*)[8]>(&vb[0]);
+      uint32_t (&v1)[8] = *reinterpret_cast<uint32_t (*)[8]>(&vb[8]);
+      decode16_bf16(vc[T][0], v0);
+      decode16_bf16(vc[T][1], v1);
+      const int t = T * 16 + n;
+      const int base = (((t >> 3) ^ kg) << 4) + (t & 7) * 2;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        uint8_t *row = vt + (kg * 32 + 2 * i) * AM_VROW + base;
+        *reinterpret_cast<uint16_t *>(row) = (uint16_t)(vb[i] & 0xFFFFu);
+        *reinterpret_cast<uint16_t *>(row + AM_VROW) = (uint16_t)(vb[i] >> 16);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // A operand: P[head n][tokens 8 kg ..+8], split into bf16 hi + lo
+    att_bf16x8 ah, al;
+    {
+      float pr[8];
+      if (n < G) {
+        const float4 a = *reinterpret_cast<const float4 *>(pl + n * 32 + kg * 8);
+        const float4 c = *reinterpret_cast<const float4 *>(pl + n * 32 + kg * 8 + 4);
+        pr[0] = a.x; pr[1] = a.y; pr[2] = a.z; pr[3] = a.w; pr[4] = c.x; pr[5] = c.y; pr[6] = c.z; pr[7] = c.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ah[i] = (__bf16)pr[i];
+        al[i] = (__bf16)(pr[i] - (float)ah[i]);
+      }
+    }
+    // B operand per 16-channel tile: V^T[channel 16 jt + n][tokens 8 kg ..+8]
+#pragma unroll
+    for (int jt = 0; jt < 8; ++jt) {
+      const int ch = 16 * jt + n;
+      const att_u32x4 w = *reinterpret_cast<const att_u32x4 *>(vt + ch * AM_VROW + ((kg ^ (ch >> 5)) << 4));
+      const att_bf16x8 bv = __builtin_bit_cast(att_bf16x8, w);
+      o[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv, o[jt], 0, 0, 0);
+      o[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv, o[jt], 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // steps of 32 positions: wave w takes steps w, w + 4, ...; loads one step ahead
+  constexpr int STEP = 32;
+  const int64_t stride = (int64_t)ATT_WAVES * STEP;
+  int64_t t0 = t_begin + (int64_t)wave * STEP;
+  uint4 ka[2][2], va[2][2], kb2[2][2], vb2[2][2];
+  int ra[2], rb[2];
+  auto load_step = [&](int64_t ts0, uint4 (&kc)[2][2], uint4 (&vc)[2][2], int (&rows)[2]) {
+    load_tile(ts0, kc[0], vc[0], rows[0]);
+    load_tile(ts0 + 16, kc[1], vc[1], rows[1]);
+  };
+  if (t0 < t_end) load_step(t0, ka, va, ra);
+  while (t0 < t_end) {
+    if (t0 + stride < t_end) load_step(t0 + stride, kb2, vb2, rb);
+    compute_step(ka, va, ra);
+    t0 += stride;
+    if (t0 >= t_end) break;
+    if (t0 + stride < t_end) load_step(t0 + stride, ka, va, ra);
+    compute_step(kb2, vb2, rb);
+    t0 += stride;
+  }
+
+  // l over the 16 token lanes; then the block's waves merge through LDS
+#pragma unroll
+  for (int j = 0; j < 4; ++j) l[j] = group_sum<16>(l[j]);
+  __shared__ float sm_m[ATT_WAVES][4], sm_l[ATT_WAVES][4];
+  __shared__ float sm_acc[ATT_WAVES][4][D];
+  if (kg == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) sm_acc[wave][j][16 * t + n] = o[t][j];
+      if (n == 0) {
         sm_m[wave][j] = m[j];
         sm_l[wave][j] = l[j];
       }
@@ -379,9 +661,23 @@ static int launch_partial(dim3 grid, hipStream_t st, const uint16_t *q, const At
   return check_launch("paged_decode_partial");
 }
 
+template <int G>
+static int launch_mfma(dim3 grid, hipStream_t st, const uint16_t *q, const AttnGeom &g, const uint8_t *pool,
+                       const float *scales, const int32_t *bt, const int32_t *sl, float *part, int32_t *err) {
+  paged_decode_mfma_kernel<G><<<grid, ATT_THREADS, 0, st>>>(q, g, pool, scales, bt, sl, part, err);
+  return check_launch("paged_decode_mfma");
+}
+
 template <int D>
 static int launch_g(int G, dim3 grid, hipStream_t st, const uint16_t *q, const AttnGeom &g, const uint8_t *pool,
                     const float *scales, const int32_t *bt, const int32_t *sl, float *part, int32_t *err) {
+  if (D == 128 && g.page_size % 16 == 0) {  // matrix-core variant
+    switch (G) {
+      case 1: return launch_mfma<1>(grid, st, q, g, pool, scales, bt, sl, part, err);
+      case 2: return launch_mfma<2>(grid, st, q, g, pool, scales, bt, sl, part, err);
+      default: return launch_mfma<4>(grid, st, q, g, pool, scales, bt, sl, part, err);
+    }
+  }
   switch (G) {
     case 1: return launch_partial<1, D>(grid, st, q, g, pool, scales, bt, sl, part, err);
     case 2: return launch_partial<2, D>(grid, st, q, g, pool, scales, bt, sl, part, err);
