@@ -7,7 +7,8 @@ of every layer, inputs already resident in HBM.  Reported as algorithmic GB/s
 (3 bytes per KV element + scales + block tables) and as a fraction of the 8 TB/s HBM3E
 peak.  Also measured: configs[2] (paged gather + dequant, 64 x 32k decode, 300k-page
 pool; plus decode attention computed straight from those FP8 pages), configs[3] (Belady tiering of a ring-attention trace: evictions/s, plus the
-pinned-host tier moves of one layer overlapped with compute) and configs[4] (80-layer
+pinned-host tier moves of one layer overlapped with compute; and the same schedule over three
+tiers, HBM / pinned DRAM / a file, planned on the GPU and replayed for three windows) and configs[4] (80-layer
 70B-shape share streamed through 60 HBM layer slots and pinned DRAM: per-kernel append
 and gather GB/s, D2H / H2D GB/s).
 
@@ -15,7 +16,7 @@ The CPU baseline is the C oracle (oracle/zx_oracle.c, one thread) timed on a bou
 sample of the same workload on this machine's host cores.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-                    [--only append|gather|belady|configs4|copy|all]
+                    [--only append|gather|belady|tiers|configs4|copy|all]
 """
 from __future__ import annotations
 
@@ -39,7 +40,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
-    ap.add_argument("--only", choices=["append", "gather", "belady", "configs4", "copy", "all"], default="all")
+    ap.add_argument("--only", choices=["append", "gather", "belady", "tiers", "configs4", "copy", "all"],
+                    default="all")
     ap.add_argument("--seed", type=int, default=1)
     return ap.parse_args()
 
@@ -244,6 +246,76 @@ def belady_leg(torch, dev, skip_cpu):
             k += 1
         out["reference_linear_scan_evictions_per_s"] = round(k / (time.perf_counter() - t0), 3)
     del m
+    return out
+
+
+def tiers_leg(torch, dev):
+    """configs[3]'s schedule over three tiers (README.md:150-154: HBM / DRAM / NVMe): T0 =
+    the 64 GB HBM budget, T1 = 32 GiB of pinned host DRAM, T2 = a file.  The whole trace
+    is planned on the GPU (two Belady runs + the plan kernel, then host slot bookkeeping);
+    three windows are replayed with real page bytes, each overlapped with 20 paged
+    gather+dequant kernels on the compute stream: the forward of layer 50 (T0 -> T1 and
+    T1 -> T2 moves), the backward of layer 40 (T1 -> T0) and the backward of layer 20
+    (T2 -> T0; its pages are written to the file first, untimed)."""
+    import shutil
+
+    import numpy as np
+
+    from zenyx_amd import kv
+    from zenyx_amd.train.belady_tiers import ThreeTierPlan, ThreeTierReplay
+    from zenyx_amd.train.belayd_kv_cache_tiering import BeladyKVCacheTieringManager
+
+    m = BeladyKVCacheTieringManager(num_devices=8, context_length=2**20, num_layers=80, num_kv_heads=8,
+                                    head_dim=128, page_tokens=64, hbm_budget_bytes=64e9, device=dev)
+    spare = 4096
+    t1_pages = (32 << 30) // m.page_bytes - spare  # T1 pool (with spare slots) = 32 GiB
+    trace = m.sequence.trace(dev)
+    ThreeTierPlan(trace[:65536].contiguous(), m.n_pages, 1024, 1024, spare=64)  # warm-up
+    plan = ThreeTierPlan(trace, m.n_pages, m.capacity, t1_pages, spare=spare)
+    st = plan.stats()
+    log(f"three tiers: plan {st['gpu_plan_s'] * 1e3:.0f} ms on the GPU + {st['host_slots_s']:.2f} s of host slots; "
+        f"{st['from_t1']} pages back from DRAM, {st['from_t2']} from the file")
+    out = {"workload": "configs[3] schedule over T0 = 64 GB HBM, T1 = 32 GiB pinned DRAM, T2 = file",
+           "t0_pages": m.capacity, "t1_pages": t1_pages, "spare_slots": spare, "plan": st}
+    tmpdir = os.environ.get("TMPDIR", "/tmp")
+    if shutil.disk_usage(tmpdir).free < (12 << 30):
+        out["replay"] = f"skipped: less than 12 GiB free under {tmpdir}"
+        return out
+    path = os.path.join(tmpdir, f"zx_t2_{os.getpid()}.bin")
+    pool = torch.randint(0, 126, (8192, 2, 8, 16, 128), dtype=torch.uint8, device=dev)
+    bt = torch.randperm(8192, device=dev)[:64 * 128].to(torch.int32).view(64, 128)
+    sl = torch.full((64,), 2048, dtype=torch.int32, device=dev)
+    sc = torch.full((2, 8), 0.01, dtype=torch.float32, device=dev)
+
+    def compute():
+        for _ in range(20):
+            kv.kv_gather_dequant(pool, sc, bt, sl, 2048)
+
+    n = plan.trace.size
+    per_layer = n // 2 // 80
+    windows = {"forward_layer50": (50 * per_layer, 51 * per_layer),
+               "backward_layer40": (n // 2 + 39 * per_layer, n // 2 + 40 * per_layer),
+               "backward_layer20": (n // 2 + 59 * per_layer, n // 2 + 60 * per_layer)}
+    rep = ThreeTierReplay(plan, m.page_bytes, path, device=dev)
+    try:
+        a, b = windows["backward_layer20"]
+        pages = plan.moves(a, b)["t2_t0"][0]
+        if len(pages):  # the window reads these pages from the file: put them there first
+            rep._pwrite(rep._t1_np, (np.arange(len(pages)) % (plan.c1 + spare)) * m.page_bytes, pages)
+        a, b = windows["backward_layer40"]
+        rep.run(a, a + 8192)  # warm-up: staging buffers, copy engines
+        res = {}
+        for name, (a, b) in windows.items():
+            r = rep.run(a, b, compute=compute)
+            keep = ("batches", "wall_s", "t0_t1_pages", "t1_t0_pages", "t2_t0_pages", "t1_t2_pages", "t0_t2_pages",
+                    "d2h_GBps", "h2d_GBps", "disk_write_GBps", "disk_read_GBps", "direct_io")
+            res[name] = {k: (round(r[k], 3) if isinstance(r[k], float) else r[k]) for k in keep}
+            log(f"three tiers {name}: " + ", ".join(f"{k} {res[name][k]}" for k in keep))
+        out["replay"] = res
+        out["overlapped_with"] = "20 paged gather+dequant kernels on the compute stream per window"
+    finally:
+        rep.close()
+        os.remove(path)
     return out
 
 
@@ -485,6 +557,18 @@ def main():
             out.update({"value": b["evictions_per_s"], "unit": "evictions/s",
                         "ms_per_step": b["simulate_ms"], "config": {"workload": b["workload"]}})
 
+    if args.only == "tiers":
+        out["three_tier"] = tiers_leg(torch, dev)
+    elif args.only == "all":
+        # in a child process: 64 GB of T0 slots and 32 GiB of pinned T1 slots
+        import subprocess
+
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", "tiers", "--skip-cpu"],
+                           stdout=subprocess.PIPE, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"three-tier leg failed with exit code {r.returncode}")
+        out["three_tier"] = json.loads(r.stdout.strip().splitlines()[-1])["three_tier"]
+
     if args.only == "configs4":
         out["configs4"] = configs4_leg(torch, dev)
     elif args.only == "all":
@@ -497,6 +581,11 @@ def main():
         if r.returncode != 0:
             raise RuntimeError(f"configs[4] leg failed with exit code {r.returncode}")
         out["configs4"] = json.loads(r.stdout.strip().splitlines()[-1])["configs4"]
+    if args.only == "tiers" and "value" not in out:
+        t = out["three_tier"]
+        out.update({"value": round(t["plan"]["accesses"] / (t["plan"]["gpu_plan_s"] + t["plan"]["host_slots_s"]), 1),
+                    "unit": "accesses planned/s", "ms_per_step": round(1e3 * t["plan"]["gpu_plan_s"], 3),
+                    "config": {"workload": t["workload"]}})
     if args.only in ("configs4", "all"):
         if "value" not in out:
             c = out["configs4"]

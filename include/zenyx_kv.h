@@ -213,6 +213,34 @@ int zx_belady_simulate(const int32_t *trace, const int32_t *next_use, const int3
 int zx_tier_copy_runs(void *dst, const void *src, const int64_t *dst_off, const int64_t *src_off,
                       int64_t n_runs, int64_t run_bytes, zx_stream_t stream, void *done);
 
+/* Scattered page moves of a tier (replaces the per-block .to(device) / .cpu() copies of
+ * kv_tiering.py:46, 54, 60): page i goes from src + src_off[i] to dst + dst_off[i], each
+ * page_bytes (a multiple of 16) long, by one kernel that reads and writes device memory
+ * or pinned host memory directly (dst/src 16-byte aligned; pinned host memory must come
+ * from hipHostMalloc).  dst_off / src_off hold n_pages int64 byte offsets in memory the
+ * device can read (device or pinned host), and must stay valid until the copy is done.
+ * A page whose range leaves [0, dst_bytes) or [0, src_bytes) is skipped and sets
+ * ZX_KERR_PAGE_RANGE in *err (may be NULL).  max_workgroups <= 0 picks 32 (enough to
+ * keep PCIe Gen5 x16 busy on MI355X; more only takes compute units from other work). */
+int zx_tier_move_pages(void *dst, int64_t dst_bytes, const void *src, int64_t src_bytes,
+                       const int64_t *dst_off, const int64_t *src_off, int64_t n_pages,
+                       int64_t page_bytes, int32_t max_workgroups, int32_t *err, zx_stream_t stream);
+
+/* Three-tier Belady plan (README.md:150-154: HBM / DRAM / NVMe tiers with offline-optimal
+ * replacement; replaces the LRU spill of kv_tiering.py:57-66).  Inputs are two runs of
+ * zx_belady_simulate over the same trace with miss flags: capacity c0 (T0) and c0 + c1
+ * (T0 and T1 together), plus the trace's prev_use table.  Per position i writes
+ *   src[i]: 0 hit in T0, 1 brought from T1, 2 brought from T2 (seen before), 3 new;
+ *   v0[i]:  the page T0 evicts at i (to T1, or to T2 when v1[i] == v0[i]), or -1;
+ *   v1[i]:  the page T1 evicts to T2 at i, or -1.
+ * Equal to the explicit hierarchy in which T0 sends its farthest page to T1 and T1 its
+ * farthest to T2 (Belady MIN is a stack algorithm).  A victim position outside [0, n)
+ * sets ZX_KERR_POS_RANGE in *err (may be NULL) and is skipped. */
+int zx_belady_tier_plan(const int32_t *prev_use, const uint8_t *miss0, const uint8_t *miss01, int64_t n,
+                        const int32_t *e0_pos, const int32_t *e0_page, int64_t n_e0,
+                        const int32_t *e01_pos, const int32_t *e01_page, int64_t n_e01, uint8_t *src,
+                        int32_t *v0, int32_t *v1, int32_t *err, zx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

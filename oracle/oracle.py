@@ -55,6 +55,7 @@ def lib() -> ctypes.CDLL:
             "zxo_belady_argmax": (None, [P, P, i64, P]),
             "zxo_next_use": (None, [P, i64, i32, P, P]),
             "zxo_belady_simulate": (i64, [P, i64, i32, i64, P, P, i64, P, P]),
+            "zxo_belady_tiers": (i64, [P, i64, i32, i64, i64, P, P, P]),
             "zxo_ring_trace": (None, [i32, i32, i32, P]),
             "zxo_paged_attention_decode": (i32, [P, i32, P, i64, i32, i32, i32, P, P, i32, P, i32, f32, P]),
         }
@@ -247,6 +248,18 @@ def belady_simulate(trace: np.ndarray, n_pages: int, capacity: int, evict_cap: i
     out = (ep[:k].copy(), eg[:k].copy(), {"evictions": int(n_ev), "misses": int(stats[0]),
                                           "hits": int(stats[1]), "resident": int(stats[2])})
     return out + (mf,) if miss_flags else out
+
+
+def belady_tiers(trace: np.ndarray, n_pages: int, c0: int, c1: int):
+    """Explicit three-tier Belady hierarchy (two heaps); returns (src uint8, v0 int32,
+    v1 int32, T0 misses): per access the tier the page came from (0 hit in T0, 1 from T1,
+    2 from T2, 3 new), the page T0 evicted to T1 and the page T1 evicted to T2 (-1: none)."""
+    trace = np.ascontiguousarray(trace, dtype=np.int32)
+    src = np.empty(trace.size, np.uint8)
+    v0 = np.empty(trace.size, np.int32)
+    v1 = np.empty(trace.size, np.int32)
+    m = lib().zxo_belady_tiers(_p(trace), trace.size, n_pages, c0, c1, _p(src), _p(v0), _p(v1))
+    return src, v0, v1, int(m)
 
 
 def ring_trace(n_layers: int, ring: int, shard_pages: int) -> np.ndarray:

@@ -484,6 +484,86 @@ int64_t zxo_belady_simulate(const int32_t *trace, int64_t n, int32_t n_pages, in
   return ev;
 }
 
+/* Three-tier Belady hierarchy (README.md:150-154: HBM / DRAM / NVMe, offline-optimal
+ * replacement; the reference's T0/T1/T2 manager kv_tiering.py:18-66 with the policy made
+ * Belady), simulated explicitly with one heap per tier.  T0 holds at most c0 pages, T1 at
+ * most c1; T2 holds everything else.  Access of page p at position i:
+ *   * p in T0: hit (src 0), its key becomes its next use;
+ *   * otherwise p comes from T1 (src 1, leaving T1), from T2 (src 2: seen before) or is
+ *     new (src 3: first access).  If T0 is full, its farthest page r (ties: smallest id)
+ *     goes to T1 (v0[i] = r); if T1 then holds more than c1 pages, its farthest page q
+ *     (possibly r itself) goes to T2 (v1[i] = q).  p enters T0.
+ * src, v0, v1 have n entries (v0/v1 = -1 where nothing moves).  Returns the number of
+ * T0 misses.  The hierarchy is exclusive: a page is in exactly one tier. */
+int64_t zxo_belady_tiers(const int32_t *trace, int64_t n, int32_t n_pages, int64_t c0, int64_t c1,
+                         uint8_t *src, int32_t *v0, int32_t *v1) {
+  int32_t *next_use = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n ? n : 1));
+  int32_t *prev_use = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n ? n : 1));
+  int32_t *key = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  uint8_t *seen = (uint8_t *)calloc((size_t)n_pages, 1);
+  zxo_heap H0, H1;
+  H0.h = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  H0.pos = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  H1.h = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  H1.pos = (int32_t *)malloc(sizeof(int32_t) * (size_t)n_pages);
+  H0.key = H1.key = key;
+  H0.size = H1.size = 0;
+  zxo_next_use(trace, n, n_pages, next_use, prev_use);
+  for (int32_t p = 0; p < n_pages; ++p) { H0.pos[p] = H1.pos[p] = -1; key[p] = -1; }
+  int64_t misses = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int32_t p = trace[i];
+    v0[i] = v1[i] = -1;
+    if (H0.pos[p] >= 0) {
+      src[i] = 0;
+      key[p] = next_use[i];
+      heap_up(&H0, H0.pos[p]);
+      heap_down(&H0, H0.pos[p]);
+      continue;
+    }
+    ++misses;
+    if (H1.pos[p] >= 0) { /* leaves T1: move the last heap entry into its place */
+      int64_t at = H1.pos[p];
+      heap_swap(&H1, at, H1.size - 1);
+      H1.size--;
+      H1.pos[p] = -1;
+      if (at < H1.size) { heap_up(&H1, at); heap_down(&H1, at); }
+      src[i] = 1;
+    } else {
+      src[i] = seen[p] ? 2 : 3;
+    }
+    seen[p] = 1;
+    if (H0.size >= c0) {
+      const int32_t r = H0.h[0];
+      heap_swap(&H0, 0, H0.size - 1);
+      H0.size--;
+      H0.pos[r] = -1;
+      if (H0.size) heap_down(&H0, 0);
+      v0[i] = r;
+      H1.h[H1.size] = r; /* r keeps its key (its next use) */
+      H1.pos[r] = (int32_t)H1.size;
+      H1.size++;
+      heap_up(&H1, H1.size - 1);
+      if (H1.size > c1) {
+        const int32_t q = H1.h[0];
+        heap_swap(&H1, 0, H1.size - 1);
+        H1.size--;
+        H1.pos[q] = -1;
+        if (H1.size) heap_down(&H1, 0);
+        v1[i] = q;
+      }
+    }
+    key[p] = next_use[i];
+    H0.h[H0.size] = p;
+    H0.pos[p] = (int32_t)H0.size;
+    H0.size++;
+    heap_up(&H0, H0.size - 1);
+  }
+  free(next_use); free(prev_use); free(key); free(seen);
+  free(H0.h); free(H0.pos); free(H1.h); free(H1.pos);
+  return misses;
+}
+
 /* Ring-attention access schedule of degree `ring` on one GPU (kv_tiering.py:69-73
  * generalised).  Layer l owns pages [l*ring*shard_pages, (l+1)*ring*shard_pages), split
  * into `ring` shards of shard_pages pages.  Forward: for each layer, for step s, for each

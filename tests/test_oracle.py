@@ -368,9 +368,10 @@ def test_paged_attention_oracle_matches_torch_sdpa(Hq, Hkv, D, P, seed):
     pool[(pool & 0x7F) == 0x7F] = 0x12  # no NaN codes
     bt = np.stack([rng.permutation(n_pages)[:max_blocks] for _ in range(B)]).astype(np.int32)
     scales = rng.uniform(1e-3, 0.05, (2, Hkv)).astype(np.float32)
-    q = torch.randn((B, Hq, D), dtype=torch.float32).to(torch.bfloat16)
+    q = torch.randn((B, Hq, D), dtype=torch.float32, generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16)
     qb = q.view(torch.int16).numpy().view(np.uint16)
-    sm = 1.0 / np.sqrt(D)
+    # the softmax scale crosses the C ABI as a float: the float64 reference uses the same value
+    sm = float(np.float32(1.0 / np.sqrt(D)))
     got, err = O.paged_attention_decode(qb, pool, scales, bt, lens, sm)
     assert err == 0
     dec = O.e4m3_decode(np.arange(256, dtype=np.uint8)).astype(np.float64)

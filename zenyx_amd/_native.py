@@ -56,6 +56,8 @@ SIGNATURES = {
     "zx_paged_attention_decode_workspace_bytes": (ctypes.c_size_t, [_I32, _I32, _I32, _I32, _I32, _I32]),
     "zx_paged_attention_decode": (_INT, [_P, _I32, _P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32,
                                          ctypes.c_float, _P, _P, _P, ctypes.c_size_t, _P]),
+    "zx_tier_move_pages": (_INT, [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I32, _P, _P]),
+    "zx_belady_tier_plan": (_INT, [_P, _P, _P, _I64, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P]),
 }
 
 _lib = None

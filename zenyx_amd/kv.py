@@ -382,6 +382,61 @@ class BeladyTraceSim:
         return self.evict_pos[:k].cpu(), self.evict_page[:k].cpu()
 
 
+def tier_move_pages(dst: torch.Tensor, src: torch.Tensor, dst_offs: torch.Tensor, src_offs: torch.Tensor,
+                    page_bytes: int, stream: torch.cuda.Stream | None = None, max_workgroups: int = 0,
+                    err: torch.Tensor | None = None) -> None:
+    """Enqueue ``dst[dst_offs[i] : +page_bytes] = src[src_offs[i] : +page_bytes]`` for every
+    i with one kernel (zx_tier_move_pages).  ``dst``/``src`` are contiguous device or pinned
+    host tensors; the offset tensors are int64, on the device or pinned, and must stay
+    alive until the copy has run."""
+    for t, name in ((dst_offs, "dst_offs"), (src_offs, "src_offs")):
+        if t.dtype != torch.int64 or t.dim() != 1 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous 1-D int64 tensor")
+        if not (t.is_cuda or t.is_pinned()):
+            raise ValueError(f"{name} must be on the device or in pinned host memory")
+    if dst_offs.numel() != src_offs.numel():
+        raise ValueError("dst_offs and src_offs differ in length")
+    for t, name in ((dst, "dst"), (src, "src")):
+        if not t.is_contiguous() or not (t.is_cuda or t.is_pinned()):
+            raise ValueError(f"{name} must be a contiguous device or pinned host tensor")
+    dev = dst.device if dst.is_cuda else src.device
+    st = stream if stream is not None else torch.cuda.current_stream(dev)
+    N.check(N.load().zx_tier_move_pages(
+        N.ptr(dst), dst.numel() * dst.element_size(), N.ptr(src), src.numel() * src.element_size(),
+        N.ptr(dst_offs), N.ptr(src_offs), dst_offs.numel(), int(page_bytes), int(max_workgroups), N.ptr(err),
+        ctypes.c_void_p(st.cuda_stream)), "tier_move_pages")
+
+
+def belady_tier_plan(sim0: "BeladyTraceSim", sim01: "BeladyTraceSim", check: bool = False):
+    """Three-tier schedule from two Belady runs over one trace (zx_belady_tier_plan):
+    ``sim0`` with the T0 capacity, ``sim01`` with T0 + T1, both run to the end with
+    ``record_misses=True``.  Returns device tensors (src uint8, v0 int32, v1 int32): per
+    position the tier the accessed page came from (0 hit in T0, 1 from T1, 2 from T2,
+    3 new), the page T0 evicts (-1: none; it goes to T1 unless v1 names it too) and the
+    page T1 evicts to T2 (-1: none)."""
+    for s in (sim0, sim01):
+        if s.miss_flags is None or s.t != s.n_total:
+            raise ValueError("both simulations must be run to the end with record_misses=True")
+        if s.n_evicted > s.evict_cap:
+            raise ValueError("an eviction list overflowed its capacity")
+    if sim0.trace.data_ptr() != sim01.trace.data_ptr() or sim0.capacity > sim01.capacity:
+        raise ValueError("sim0 and sim01 must share one trace, with sim0's capacity <= sim01's")
+    dev = sim0.trace.device
+    n = sim0.n_total
+    src = torch.empty(n, dtype=torch.uint8, device=dev)
+    v0 = torch.empty(n, dtype=torch.int32, device=dev)
+    v1 = torch.empty(n, dtype=torch.int32, device=dev)
+    err = _err_word(dev)
+    N.check(N.load().zx_belady_tier_plan(
+        N.ptr(sim0.prev_use), N.ptr(sim0.miss_flags), N.ptr(sim01.miss_flags), n,
+        N.ptr(sim0.evict_pos), N.ptr(sim0.evict_page), sim0.n_evicted,
+        N.ptr(sim01.evict_pos), N.ptr(sim01.evict_page), sim01.n_evicted,
+        N.ptr(src), N.ptr(v0), N.ptr(v1), N.ptr(err), N.stream_ptr(dev)), "belady_tier_plan")
+    if check:
+        _raise_kernel_error(err, "belady_tier_plan")
+    return src, v0, v1
+
+
 def tier_copy_runs(dst: torch.Tensor, src: torch.Tensor, dst_offs, src_offs, run_bytes: int,
                    stream: torch.cuda.Stream | None = None) -> None:
     """Enqueue run copies ``dst[dst_offs[i] : +run_bytes] = src[src_offs[i] : +run_bytes]``

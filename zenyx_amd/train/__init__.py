@@ -1,3 +1,4 @@
 """README-documented Phase-7/8 modules of zenyx, MI355X-native:
-``belayd_kv_cache_tiering`` (Belady KV tiering over a ring schedule) and
+``belayd_kv_cache_tiering`` (Belady KV tiering over a ring schedule), ``belady_tiers``
+(the three-tier HBM / DRAM / NVMe hierarchy with Belady at both levels) and
 ``fp8_kv_quantization`` (per-head FP8 KV quantisation and a paged FP8 KV cache)."""
