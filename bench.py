@@ -219,6 +219,7 @@ def belady_leg(torch, dev, skip_cpu):
                          "wall_ms": round(r["wall_ms"], 3)}
     log(f"tier moves: {r['d2h_pages']} D2H pages at {r['d2h_GBps']:.1f} GB/s, {r['h2d_pages']} H2D pages at "
         f"{r['h2d_GBps']:.1f} GB/s")
+    out["curriculum"] = curriculum_leg(torch, dev, skip_cpu)
     if not skip_cpu:
         import numpy as np
 
@@ -246,6 +247,54 @@ def belady_leg(torch, dev, skip_cpu):
             k += 1
         out["reference_linear_scan_evictions_per_s"] = round(k / (time.perf_counter() - t0), 3)
     del m
+    return out
+
+
+def curriculum_leg(torch, dev, skip_cpu):
+    """A ring curriculum across two phase changes (RingDegreeScheduler, README.md:162-165):
+    one training step each at degree 2 / 256k tokens, 4 / 512k and 8 / 1M, 80 layers,
+    FP8 pages of 64 tokens, the 64 GB HBM budget of configs[3].  The page trace is built
+    on the GPU, then next-use tables and the Belady schedule over the whole run."""
+    from zenyx_amd import kv
+    from zenyx_amd.train.dynamic_ring_curriculum import CurriculumPhase, RingDegreeScheduler
+
+    L, pt, page_bytes = 80, 64, 64 * 8 * 128 * 2
+    s = RingDegreeScheduler([CurriculumPhase("ring2", 2, 1 << 18, 1), CurriculumPhase("ring4", 4, 1 << 19, 1),
+                             CurriculumPhase("ring8", 8, 1 << 20)], num_devices=8)
+    n_pages = L * s.layer_stride(pt)
+    cap = int(64e9 // page_bytes)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    s.access_trace([0, 1, 2], 2, page_tokens=pt, device=dev)  # warm-up
+    ev[0].record()
+    trace = s.access_trace([0, 1, 2], L, page_tokens=pt, device=dev)
+    ev[1].record()
+    sim = kv.BeladyTraceSim(trace, n_pages, cap, evict_cap=1)
+    ev[2].record()
+    sim.run()
+    ev[3].record()
+    torch.cuda.synchronize(dev)
+    st = sim.stats()
+    t_trace, t_nu, t_sim = ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2]), ev[2].elapsed_time(ev[3])
+    out = {"workload": "3 training steps across two phase changes: ring 2 / 256k tokens, ring 4 / 512k, "
+                       "ring 8 / 1M; 80 layers, FP8 pages of 64 tokens, 64 GB HBM budget",
+           "accesses": int(trace.numel()), "pages": n_pages, "capacity_pages": cap, "evictions": st["evictions"],
+           "misses": st["misses"], "trace_ms": round(t_trace, 3), "trace_GBps": round(4 * trace.numel() / t_trace / 1e6, 1),
+           "next_use_ms": round(t_nu, 3), "simulate_ms": round(t_sim, 3),
+           "evictions_per_s": round(st["evictions"] / (t_sim * 1e-3), 1)}
+    log(f"curriculum: {trace.numel()} accesses, trace {t_trace:.2f} ms, next-use {t_nu:.2f} ms, simulate {t_sim:.1f} ms, "
+        f"{st['evictions']} evictions")
+    if not skip_cpu:
+        from oracle import oracle as O
+
+        t0 = time.perf_counter()
+        want = O.ring_curriculum_trace([2, 4, 8], [4096, 8192, 16384], L, s.layer_stride(pt))
+        t1 = time.perf_counter()
+        _, _, cst = O.belady_simulate(want, n_pages, cap, evict_cap=1)
+        t2 = time.perf_counter()
+        assert cst["evictions"] == st["evictions"], "GPU and CPU Belady disagree over the curriculum"
+        out["cpu_baseline"] = {"value": round(cst["evictions"] / (t2 - t1), 1), "unit": "evictions/s", "cores": 1,
+                               "kind": "port", "sample": f"C oracle: trace {t1 - t0:.2f} s, heap Belady {t2 - t1:.2f} s "
+                                                         f"over the same {want.size} accesses"}
     return out
 
 

@@ -241,6 +241,21 @@ int zx_belady_tier_plan(const int32_t *prev_use, const uint8_t *miss0, const uin
                         const int32_t *e01_pos, const int32_t *e01_page, int64_t n_e01, uint8_t *src,
                         int32_t *v0, int32_t *v1, int32_t *err, zx_stream_t stream);
 
+/* Ring-attention page trace of a curriculum of training steps (RingDegreeScheduler /
+ * CurriculumPhase, README.md:162-165, 330, 345, code absent; build_ring_timeline of
+ * kv_tiering.py:69-73 generalised).  Step k has ring degree degrees[k] = R and
+ * ctx_pages[k] = P pages per layer (host arrays); layer l's pages are
+ * [l * layer_stride, l * layer_stride + P).  Shard s holds pages
+ * [floor(s P / R), floor((s + 1) P / R)).  Forward of a step: per layer, per ring step
+ * r, per simulated device d, the pages of shard (d - r) mod R; backward: the exact
+ * reverse of the step's forward.  Steps are concatenated into out (device int32, at
+ * least zx_ring_curriculum_trace_len() ids; that query returns -1 for a degree or page
+ * count below 1). */
+int64_t zx_ring_curriculum_trace_len(const int32_t *degrees, const int32_t *ctx_pages, int32_t n_steps,
+                                     int32_t n_layers);
+int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, int32_t n_steps, int32_t n_layers,
+                             int32_t layer_stride, int32_t *out, int64_t out_len, zx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,7 @@ def lib() -> ctypes.CDLL:
             "zxo_next_use": (None, [P, i64, i32, P, P]),
             "zxo_belady_simulate": (i64, [P, i64, i32, i64, P, P, i64, P, P]),
             "zxo_belady_tiers": (i64, [P, i64, i32, i64, i64, P, P, P]),
+            "zxo_ring_curriculum_trace": (i64, [P, P, i32, i32, i32, P]),
             "zxo_ring_trace": (None, [i32, i32, i32, P]),
             "zxo_paged_attention_decode": (i32, [P, i32, P, i64, i32, i32, i32, P, P, i32, P, i32, f32, P]),
         }
@@ -260,6 +261,17 @@ def belady_tiers(trace: np.ndarray, n_pages: int, c0: int, c1: int):
     v1 = np.empty(trace.size, np.int32)
     m = lib().zxo_belady_tiers(_p(trace), trace.size, n_pages, c0, c1, _p(src), _p(v0), _p(v1))
     return src, v0, v1, int(m)
+
+
+def ring_curriculum_trace(degrees, ctx_pages, n_layers: int, layer_stride: int) -> np.ndarray:
+    """Concatenated ring traces of training steps with per-step degree and pages per layer."""
+    deg = np.ascontiguousarray(degrees, dtype=np.int32)
+    ctx = np.ascontiguousarray(ctx_pages, dtype=np.int32)
+    n = int(np.sum(2 * n_layers * deg.astype(np.int64) * ctx))
+    out = np.empty(max(n, 1), np.int32)
+    k = lib().zxo_ring_curriculum_trace(_p(deg), _p(ctx), deg.size, n_layers, layer_stride, _p(out))
+    assert k == n
+    return out[:n]
 
 
 def ring_trace(n_layers: int, ring: int, shard_pages: int) -> np.ndarray:

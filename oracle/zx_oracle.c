@@ -564,6 +564,35 @@ int64_t zxo_belady_tiers(const int32_t *trace, int64_t n, int32_t n_pages, int64
   return misses;
 }
 
+/* Ring-attention page accesses over a curriculum of training steps (README.md:162-165,
+ * 330, 345: RingDegreeScheduler / CurriculumPhase, "progressive ring degree expansion";
+ * code absent).  Step k has ring degree degrees[k] = R and ctx_pages[k] = P pages per
+ * layer; layer l's pages are [l * layer_stride, l * layer_stride + P).  Shard s of a
+ * layer holds pages [floor(s P / R), floor((s + 1) P / R)) (uneven shards allowed, empty
+ * ones too).  Forward of step k: for each layer, for ring step r, for simulated device
+ * d, the pages of shard (d - r) mod R in order; backward: the exact reverse of the
+ * step's forward (build_ring_timeline, kv_tiering.py:69-73, generalised).  Steps are
+ * concatenated; out holds sum_k 2 * L * R_k * P_k ids.  Returns the count. */
+int64_t zxo_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, int32_t n_steps,
+                                  int32_t n_layers, int32_t layer_stride, int32_t *out) {
+  int64_t k = 0;
+  for (int32_t st = 0; st < n_steps; ++st) {
+    const int64_t R = degrees[st], P = ctx_pages[st];
+    const int64_t begin = k;
+    for (int32_t l = 0; l < n_layers; ++l)
+      for (int64_t r = 0; r < R; ++r)
+        for (int64_t d = 0; d < R; ++d) {
+          const int64_t sh = ((d - r) % R + R) % R;
+          const int64_t lo = sh * P / R, hi = (sh + 1) * P / R;
+          for (int64_t j = lo; j < hi; ++j) out[k++] = (int32_t)((int64_t)l * layer_stride + j);
+        }
+    const int64_t n_fwd = k - begin;
+    for (int64_t i = 0; i < n_fwd; ++i) out[k + i] = out[k - 1 - i];
+    k += n_fwd;
+  }
+  return k;
+}
+
 /* Ring-attention access schedule of degree `ring` on one GPU (kv_tiering.py:69-73
  * generalised).  Layer l owns pages [l*ring*shard_pages, (l+1)*ring*shard_pages), split
  * into `ring` shards of shard_pages pages.  Forward: for each layer, for step s, for each

@@ -58,6 +58,8 @@ SIGNATURES = {
                                          ctypes.c_float, _P, _P, _P, ctypes.c_size_t, _P]),
     "zx_tier_move_pages": (_INT, [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I32, _P, _P]),
     "zx_belady_tier_plan": (_INT, [_P, _P, _P, _I64, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P]),
+    "zx_ring_curriculum_trace_len": (_I64, [_P, _P, _I32, _I32]),
+    "zx_ring_curriculum_trace": (_INT, [_P, _P, _I32, _I32, _I32, _P, _I64, _P]),
 }
 
 _lib = None

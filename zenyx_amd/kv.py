@@ -382,6 +382,29 @@ class BeladyTraceSim:
         return self.evict_pos[:k].cpu(), self.evict_page[:k].cpu()
 
 
+def ring_curriculum_trace(degrees, ctx_pages, n_layers: int, layer_stride: int,
+                          device: torch.device | None = None) -> torch.Tensor:
+    """Page trace of ring attention over training steps with per-step ring degree and
+    pages per layer (zx_ring_curriculum_trace): a 1-D int32 device tensor, steps
+    concatenated, each step's forward followed by its exact reverse."""
+    import numpy as np
+
+    deg = np.ascontiguousarray(degrees, dtype=np.int32)
+    ctx = np.ascontiguousarray(ctx_pages, dtype=np.int32)
+    if deg.ndim != 1 or deg.shape != ctx.shape:
+        raise ValueError("degrees and ctx_pages must be 1-D of equal length")
+    lib = N.load()
+    n = lib.zx_ring_curriculum_trace_len(deg.ctypes.data, ctx.ctypes.data, deg.size, int(n_layers))
+    if n < 0:
+        raise ValueError("ring degrees and pages per layer must be >= 1, n_layers >= 1")
+    dev = device or N.ensure_gpu()
+    out = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    N.check(lib.zx_ring_curriculum_trace(deg.ctypes.data, ctx.ctypes.data, deg.size, int(n_layers),
+                                         int(layer_stride), N.ptr(out), n, N.stream_ptr(dev)),
+            "ring_curriculum_trace")
+    return out[:n]
+
+
 def tier_move_pages(dst: torch.Tensor, src: torch.Tensor, dst_offs: torch.Tensor, src_offs: torch.Tensor,
                     page_bytes: int, stream: torch.cuda.Stream | None = None, max_workgroups: int = 0,
                     err: torch.Tensor | None = None) -> None:
