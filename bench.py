@@ -16,7 +16,7 @@ The CPU baseline is the C oracle (oracle/zx_oracle.c, one thread) timed on a bou
 sample of the same workload on this machine's host cores.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-                    [--only append|gather|belady|tiers|configs4|copy|all]
+                    [--only append|gather|belady|tiers|weights|configs4|copy|all]
 """
 from __future__ import annotations
 
@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
-    ap.add_argument("--only", choices=["append", "gather", "belady", "tiers", "configs4", "copy", "all"],
+    ap.add_argument("--only", choices=["append", "gather", "belady", "tiers", "weights", "configs4", "copy", "all"],
                     default="all")
     ap.add_argument("--seed", type=int, default=1)
     return ap.parse_args()
@@ -295,6 +295,68 @@ def curriculum_leg(torch, dev, skip_cpu):
         out["cpu_baseline"] = {"value": round(cst["evictions"] / (t2 - t1), 1), "unit": "evictions/s", "cores": 1,
                                "kind": "port", "sample": f"C oracle: trace {t1 - t0:.2f} s, heap Belady {t2 - t1:.2f} s "
                                                          f"over the same {want.size} accesses"}
+    return out
+
+
+def weights_leg(torch, dev):
+    """Layer-weight streaming on the KV tiers' transfer engine (LayerWeightStreamer,
+    parameter_streamer.py:32-87): 16 layers of 256 MiB in pinned DRAM, at most 2 resident;
+    per layer prefetch(i + 1), get(i), then ~5 ms of paged gather+dequant kernels.
+    Reports the copy rate alone, the compute alone and the pipelined loop."""
+    from zenyx_amd import kv
+    from zenyx_amd.streaming import LayerWeightStreamer, ParameterStore
+
+    n_layers, numel = 16, 128 << 20  # bf16: 256 MiB per layer
+    store = ParameterStore()
+    for i in range(n_layers):
+        store.register(f"layer{i}", torch.full((numel,), float(i), dtype=torch.bfloat16))
+    pool = torch.randint(0, 126, (8192, 2, 8, 16, 128), dtype=torch.uint8, device=dev)
+    bt = torch.randperm(8192, device=dev)[:64 * 128].to(torch.int32).view(64, 128)
+    sl = torch.full((64,), 2048, dtype=torch.int32, device=dev)
+    sc = torch.full((2, 8), 0.01, dtype=torch.float32, device=dev)
+
+    def compute(reps):
+        for _ in range(reps):
+            kv.kv_gather_dequant(pool, sc, bt, sl, 2048)
+
+    def timed(fn):
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize(dev)
+        return time.perf_counter() - t0
+
+    compute(4)
+    one = timed(lambda: compute(10)) / 10
+    reps = max(1, int(round(5e-3 / one)))
+    t_compute = timed(lambda: [compute(reps) for _ in range(n_layers)])
+
+    def copies_only():
+        s = LayerWeightStreamer(store, dev, max_resident_layers=2)
+        for i in range(n_layers):
+            s.get(f"layer{i}")
+
+    def pipelined():
+        s = LayerWeightStreamer(store, dev, max_resident_layers=2)
+        for i in range(n_layers):
+            if i + 1 < n_layers:
+                s.prefetch(f"layer{i + 1}")
+            s.get(f"layer{i}")
+            compute(reps)
+
+    copies_only()  # warm-up
+    t_copy = timed(copies_only)
+    pipelined()
+    t_pipe = timed(pipelined)
+    layer_bytes = numel * 2
+    hidden = (t_copy + t_compute - t_pipe) / min(t_copy, t_compute)
+    out = {"workload": f"{n_layers} layers x 256 MiB bf16 weights, 2 resident, prefetch-next, "
+                       f"{reps} gather+dequant kernels (~5 ms) per layer",
+           "h2d_GBps": round(n_layers * layer_bytes / t_copy / 1e9, 2), "copy_ms": round(t_copy * 1e3, 2),
+           "compute_ms": round(t_compute * 1e3, 2), "pipelined_ms": round(t_pipe * 1e3, 2),
+           "overlap_frac": round(hidden, 3)}
+    log(f"weights: copies {t_copy * 1e3:.1f} ms ({out['h2d_GBps']} GB/s), compute {t_compute * 1e3:.1f} ms, "
+        f"pipelined {t_pipe * 1e3:.1f} ms (overlap {hidden:.2f})")
     return out
 
 
@@ -605,6 +667,13 @@ def main():
             b = out["belady"]
             out.update({"value": b["evictions_per_s"], "unit": "evictions/s",
                         "ms_per_step": b["simulate_ms"], "config": {"workload": b["workload"]}})
+
+    if args.only in ("weights", "all"):
+        out["weight_streaming"] = weights_leg(torch, dev)
+        if "value" not in out:
+            w = out["weight_streaming"]
+            out.update({"value": w["h2d_GBps"], "ms_per_step": w["pipelined_ms"],
+                        "config": {"workload": w["workload"]}})
 
     if args.only == "tiers":
         out["three_tier"] = tiers_leg(torch, dev)

@@ -1,12 +1,16 @@
-"""MI355X drop-in for the KV-cache part of ``zenyx.streaming`` (zenyx/streaming/__init__.py:1-20).
+"""MI355X drop-in for ``zenyx.streaming`` (zenyx/streaming/__init__.py:1-20), the KV path
+and the weight streaming that shares its transfer engine.
 
 Kept names: ``quantize_to_fp8_storage``, ``dequantize_for_bf16_compute``,
-``BeladyApproxCache``, ``KVTierManager``, ``KVBlockRef``, ``build_ring_timeline``.
-The reference's weight streaming (``LayerWeightStreamer``, ``ParameterStore``), bandwidth
-throttle and training engine are not part of the KV hot path and are not provided.
+``BeladyApproxCache``, ``KVTierManager``, ``KVBlockRef``, ``build_ring_timeline``,
+``ParameterStore``, ``LayerWeightStreamer``, ``LayerBlock``, and the caller that drives
+them, ``StreamingExecutionEngine`` / ``StreamingConfig``.  The reference's bandwidth
+throttle is not part of this path and is not provided.
 """
 from .belady import AccessEvent, BeladyApproxCache
+from .engine import StreamingConfig, StreamingExecutionEngine
 from .kv_tiering import KVBlockRef, KVTierManager, build_ring_timeline
+from .parameter_streamer import LayerBlock, LayerWeightStreamer, ParameterStore
 from .precision import dequantize_for_bf16_compute, quantize_to_fp8_storage
 
 __all__ = [
@@ -15,6 +19,11 @@ __all__ = [
     "KVBlockRef",
     "KVTierManager",
     "build_ring_timeline",
+    "LayerBlock",
+    "StreamingConfig",
+    "StreamingExecutionEngine",
+    "LayerWeightStreamer",
+    "ParameterStore",
     "quantize_to_fp8_storage",
     "dequantize_for_bf16_compute",
 ]
