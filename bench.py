@@ -643,7 +643,9 @@ def main():
         qd = qd.to(torch.bfloat16)
         od = torch.empty_like(qd)
         astep = lambda: kv.paged_attention_decode(qd, G["pool"], sc, G["bt"], G["seq_lens"], out=od)
-        ms_a, _, _ = time_steps(torch, astep, args.steps, args.warmup)
+        # its first few dozen launches after the gather leg run ~10% slower (measured
+        # 0.885 ms at 3 warm-up steps, 0.786 ms at 40): time the steady state
+        ms_a, _, _ = time_steps(torch, astep, args.steps, max(args.warmup, 40))
         alg_a = G["N"] + 4 * G["B"] * (G["T"] // G["P"]) + 4 * 2 * G["H"] + 2 * 2 * G["B"] * Hq * G["D"]
         gb_a = alg_a / (ms_a * 1e-3) / 1e9
         log(f"attention decode from FP8 pages: {ms_a:.3f} ms/step, {gb_a:.1f} GB/s ({100 * gb_a / HBM_PEAK_GBPS:.1f}% "
@@ -651,7 +653,7 @@ def main():
         gather["attention_decode"] = {
             "GBps": round(gb_a, 2), "ms_per_step": round(ms_a, 4), "frac": round(gb_a / HBM_PEAK_GBPS, 4),
             "algorithmic_bytes_per_step": alg_a,
-            "workload": "paged_decode_partial/combine: 64 seqs x 32768 positions, 32 query heads over 8 KV heads, "
+            "workload": "paged_decode_mfma/combine: 64 seqs x 32768 positions, 32 query heads over 8 KV heads, "
                         "D=128, reading the configs[2] pool (1 B per K/V element)"}
         del qd, od
         out["gather_dequant"] = gather

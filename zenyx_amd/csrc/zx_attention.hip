@@ -319,14 +319,16 @@ paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const ui
 // Matrix-core variant of pass 1 for D = 128 and page sizes that are a multiple of 16:
 // q.K^T and P.V run on v_mfma_f32_16x16x32_bf16 with the (up to 4) query heads of the
 // block as the M rows (padded to 16).  A wave takes steps of 32 positions (two 16-token
-// tiles, each inside one page).  Lane l loads, for token l % 16 of a tile, the 32 K and V
-// codes of channels 32 (l / 16) ..+32, converts them to bf16 exactly and
-//   * uses the K codes directly as the B operand of q.K^T (k = channel, any consistent
-//     permutation of the channels works since the product sums over them);
-//   * writes the V values transposed into LDS (V^T[channel][token], bf16, 80-byte rows,
-//     16-byte token chunks XOR-swizzled by channel / 32 so the four lane groups of a
-//     store hit different banks), from where each lane reads the 8 consecutive tokens
-//     of one channel that the B operand of P.V needs.
+// tiles, each inside one page).  The K and V codes of a tile arrive as two contiguous
+// 1 KiB loads per run (lane l: token 8 i + l / 8, channels 16 (l % 8) ..+16: whole cache
+// lines per instruction) and are rearranged on chip:
+//   * K codes go through a staging area (144-byte token rows) and come back as lane
+//     (n, kg) = token n, channels 32 kg ..+32, converted to bf16 exactly: the B operand
+//     of q.K^T (k = channel; any channel permutation shared with q's A operand works,
+//     since the product sums over channels);
+//   * V values go transposed into LDS (V^T[channel][token], bf16, 80-byte rows, 16-byte
+//     token chunks XOR-swizzled by channel / 32), from where each lane reads the 8
+//     consecutive tokens of one channel that the B operand of P.V needs.
 // P goes through LDS as fp32 into the A-operand layout and is split into bf16 hi + lo
 // (two MFMAs), which keeps the products at ~2^-17 relative error.  Scores land in the C
 // layout: lanes 0-15 hold heads 0-3 of token l % 16, so the softmax bookkeeping is a
@@ -338,6 +340,8 @@ typedef unsigned int att_u32x4 __attribute__((ext_vector_type(4)));
 constexpr int AM_VROW = 80;                 // bytes per channel row of V^T (64 + 16 pad)
 constexpr int AM_VBYTES = 128 * AM_VROW;    // one wave's V^T (32 tokens)
 constexpr int AM_PBYTES = 4 * 32 * 4;       // one wave's P (4 heads x 32 tokens fp32)
+constexpr int AM_KROW = 144;                // bytes per token row of the K staging (128 + 16 pad)
+constexpr int AM_KBYTES = 32 * AM_KROW;     // one wave's K codes (32 tokens)
 
 __device__ __forceinline__ float row16_max(float v) {  // max over lanes 0-15 of each row
   v = fmaxf(v, dpp<0xB1>(v));
@@ -367,9 +371,10 @@ paged_decode_mfma_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8
   const int64_t head_off = (int64_t)h * g.page_size * D;
   const int64_t v_off = (int64_t)g.n_kv_heads * g.page_size * D;
   const int32_t *bt = block_tables + (int64_t)b * g.max_blocks;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[ATT_WAVES][AM_VBYTES + AM_PBYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[ATT_WAVES][AM_VBYTES + AM_PBYTES + AM_KBYTES];
   uint8_t *vt = lds[wave];
   float *pl = reinterpret_cast<float *>(lds[wave] + AM_VBYTES);
+  uint8_t *ks = lds[wave] + AM_VBYTES + AM_PBYTES;
 
   // q rows (heads) as the A operand: lane l holds head n, channels 32 kg + 8 c .. +8
   att_bf16x8 qa[4];
@@ -396,37 +401,55 @@ paged_decode_mfma_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8
   int32_t e = split == 0 && threadIdx.x == 0 && blockIdx.y == 0 && (int64_t)len > (int64_t)g.max_blocks * g.page_size
                   ? ZX_KERR_POS_RANGE : 0;
 
-  // one 16-token tile: K and V codes of token tp + n, channels 32 kg ..+32; rows = valid tokens
-  auto load_tile = [&](int64_t tp, uint4 (&kc)[2], uint4 (&vc)[2], int &rows) {
-    rows = (int)max((int64_t)0, min((int64_t)16, t_end - tp));
-    int nrec = 0;
-    const uint8_t *src = pool;
-    if (rows > 0) {
-      const uint32_t bi = page_of(g, (uint32_t)tp);
-      const int64_t page = bt[bi];
-      if (page < 0 || page >= g.n_pages) {
-        e |= ZX_KERR_PAGE_RANGE;
-        rows = 0;
-      } else {
-        src = pool + page * page_bytes + head_off + (tp - (int64_t)bi * g.page_size) * D;
-        nrec = rows * D;
-      }
-    }
+  // one 16-token tile: K and V codes of token tp + n, channels 32 kg ..+32; rows = valid tokens.
+  // Branch-free: the block-table entry is read for a position clamped into the split
+  // (always a valid index), validity is a select, and a tile past the end or on a bad
+  // page loads through resources with num_records = 0 (zeros, no memory traffic).  Every
+  // step therefore issues the same loads, so the compiler's s_waitcnt counts only wait
+  // for the step being computed and the next step's loads stay in flight.
+  const int64_t t_last = t_end > t_begin ? t_end - 1 : t_begin;
+  // page id of the tile at tp (position clamped into the split: always a valid index)
+  auto tile_page = [&](int64_t tp) -> int64_t {
+    const int64_t tc = tp < t_last ? tp : t_last;
+    return bt[page_of(g, (uint32_t)tc)];
+  };
+  auto load_tile = [&](int64_t tp, int64_t page, uint4 (&kc)[2], uint4 (&vc)[2], int &rows) {
+    const int live = (int)max((int64_t)0, min((int64_t)16, t_end - tp));
+    const int64_t tc = tp < t_last ? tp : t_last;
+    const uint32_t bi = page_of(g, (uint32_t)tc);
+    const bool ok = page >= 0 && page < g.n_pages;
+    e |= (live > 0 && !ok) ? ZX_KERR_PAGE_RANGE : 0;
+    rows = ok ? live : 0;
+    const int nrec = rows * D;
+    const uint8_t *src = pool + (ok ? page * page_bytes + head_off + (tc - (int64_t)bi * g.page_size) * D : 0);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src), (short)0, nrec,
                                                                         0x00020000);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(src + (nrec ? v_off : 0)), (short)0, nrec, 0x00020000);
-    const int off = n * D + kg * 32;
+        const_cast<uint8_t *>(src + (ok ? v_off : 0)), (short)0, nrec, 0x00020000);
+    // contiguous: load i gives lane l the 16 codes of token 8 i + l / 8, channels
+    // 16 (l % 8) ..+16, so one instruction reads 1 KiB of whole cache lines (the mapping
+    // that gives each lane its MFMA operand directly touches half lines and was ~20%
+    // slower on the same bytes); the operand layout is made on chip
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const att_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16 * i, 0, 2);
-      const att_u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(rv, off + 16 * i, 0, 2);
+      const att_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rk, 16 * lane + 1024 * i, 0, 2);
+      const att_u32x4 c = __builtin_amdgcn_raw_buffer_load_b128(rv, 16 * lane + 1024 * i, 0, 2);
       kc[i] = make_uint4(a.x, a.y, a.z, a.w);
       vc[i] = make_uint4(c.x, c.y, c.z, c.w);
     }
   };
 
   auto compute_step = [&](const uint4 (&kc)[2][2], const uint4 (&vc)[2][2], const int (&rows)[2]) {
+    // K codes through the staging rows: written as loaded, read back as lane (n, kg) =
+    // token n, channels 32 kg ..+32 (144-byte rows: the 16 rows of a read hit distinct banks)
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        *reinterpret_cast<uint4 *>(ks + (T * 16 + 8 * i + (lane >> 3)) * AM_KROW + 16 * (lane & 7)) = kc[T][i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // scores: S[head][token] for both tiles
     float sv[2][4];
 #pragma unroll
@@ -434,8 +457,9 @@ paged_decode_mfma_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8
       uint32_t kb[16];
       uint32_t (&k0)[8] = *reinterpret_cast<uint32_t (*)[8]>(&kb[0]);
       uint32_t (&k1)[8] = *reinterpret_cast<uint32_t (*)[8]>(&kb[8]);
-      decode16_bf16(kc[T][0], k0);
-      decode16_bf16(kc[T][1], k1);
+      const uint8_t *kr = ks + (T * 16 + n) * AM_KROW + kg * 32;
+      decode16_bf16(*reinterpret_cast<const uint4 *>(kr), k0);
+      decode16_bf16(*reinterpret_cast<const uint4 *>(kr + 16), k1);
       att_f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int c = 0; c < 4; ++c)
@@ -472,23 +496,24 @@ paged_decode_mfma_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8
         l[j] += p;
         if (kg == 0) pl[j * 32 + T * 16 + n] = p;
       }
-    // V^T into LDS: token t = 16 T + n, channels 32 kg + 2 i, +1
+    // V^T into LDS: element (channel c, token t) at c * AM_VROW + 16 ((t / 8) ^ (c / 32)) +
+    // 2 (t % 8).  Load i of tile T gave lane l token t = 16 T + 8 i + l / 8, channels
+    // c = 16 (l % 8) + 2 p, +1 (p < 8), so c / 32 = (l % 8) / 2
 #pragma unroll
-    for (int T = 0; T < 2; ++T) {
-      uint32_t vb[16];
-      uint32_t (&v0)[8] = *reinterpret_cast<uint32_t (*)[8]>(&vb[0]);
-      uint32_t (&v1)[8] = *reinterpret_cast<uint32_t (*)[8]>(&vb[8]);
-      decode16_bf16(vc[T][0], v0);
-      decode16_bf16(vc[T][1], v1);
-      const int t = T * 16 + n;
-      const int base = (((t >> 3) ^ kg) << 4) + (t & 7) * 2;
+    for (int T = 0; T < 2; ++T)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        uint8_t *row = vt + (kg * 32 + 2 * i) * AM_VROW + base;
-        *reinterpret_cast<uint16_t *>(row) = (uint16_t)(vb[i] & 0xFFFFu);
-        *reinterpret_cast<uint16_t *>(row + AM_VROW) = (uint16_t)(vb[i] >> 16);
+      for (int i = 0; i < 2; ++i) {
+        uint32_t vb[8];
+        decode16_bf16(vc[T][i], vb);
+        const int t = T * 16 + 8 * i + (lane >> 3), g8 = lane & 7;
+        const int base = (((t >> 3) ^ (g8 >> 1)) << 4) + (t & 7) * 2;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          uint8_t *row = vt + (16 * g8 + 2 * p) * AM_VROW + base;
+          *reinterpret_cast<uint16_t *>(row) = (uint16_t)(vb[p] & 0xFFFFu);
+          *reinterpret_cast<uint16_t *>(row + AM_VROW) = (uint16_t)(vb[p] >> 16);
+        }
       }
-    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -524,23 +549,34 @@ paged_decode_mfma_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
 
-  // steps of 32 positions: wave w takes steps w, w + 4, ...; loads one step ahead
+  // steps of 32 positions: wave w takes steps w, w + 4, ...; a step's K/V loads are issued
+  // one step ahead and its two page ids one step before that, so no step waits on a
+  // block-table read before it can issue its loads
   constexpr int STEP = 32;
   const int64_t stride = (int64_t)ATT_WAVES * STEP;
   int64_t t0 = t_begin + (int64_t)wave * STEP;
   uint4 ka[2][2], va[2][2], kb2[2][2], vb2[2][2];
   int ra[2], rb[2];
-  auto load_step = [&](int64_t ts0, uint4 (&kc)[2][2], uint4 (&vc)[2][2], int (&rows)[2]) {
-    load_tile(ts0, kc[0], vc[0], rows[0]);
-    load_tile(ts0 + 16, kc[1], vc[1], rows[1]);
+  int64_t pa[2], pb[2];
+  auto pages_of_step = [&](int64_t ts0, int64_t (&p)[2]) {
+    p[0] = tile_page(ts0);
+    p[1] = tile_page(ts0 + 16);
   };
-  if (t0 < t_end) load_step(t0, ka, va, ra);
+  auto load_step = [&](int64_t ts0, const int64_t (&p)[2], uint4 (&kc)[2][2], uint4 (&vc)[2][2], int (&rows)[2]) {
+    load_tile(ts0, p[0], kc[0], vc[0], rows[0]);
+    load_tile(ts0 + 16, p[1], kc[1], vc[1], rows[1]);
+  };
+  pages_of_step(t0, pa);
+  load_step(t0, pa, ka, va, ra);
+  pages_of_step(t0 + stride, pb);
   while (t0 < t_end) {
-    if (t0 + stride < t_end) load_step(t0 + stride, kb2, vb2, rb);
+    load_step(t0 + stride, pb, kb2, vb2, rb);  // past the end: zero-length loads
+    pages_of_step(t0 + 2 * stride, pa);
     compute_step(ka, va, ra);
     t0 += stride;
     if (t0 >= t_end) break;
-    if (t0 + stride < t_end) load_step(t0 + stride, ka, va, ra);
+    load_step(t0 + stride, pa, ka, va, ra);
+    pages_of_step(t0 + 2 * stride, pb);
     compute_step(kb2, vb2, rb);
     t0 += stride;
   }

@@ -4,7 +4,11 @@
 //   1. plain streams (one 16-byte vector per thread, nontemporal loads and stores) with
 //      the read:write mixes of the append (2:1) and the gather (1:2), at the byte counts
 //      of BASELINE configs[1] / configs[2];
-//   2. the access pattern the single-pass append is forced into: a layer of token rows
+//   2. reads of random 2 KiB runs (one (page, K/V, head) run of a 16-token FP8 page)
+//      out of a 300,000-page pool, the pattern of the paged gather and of decode
+//      attention (4.29 GB read), read-only and with the gather's
+//      2 bytes written per byte read;
+//   3. the access pattern the single-pass append is forced into: a layer of token rows
 //      of 4 KiB (2 x 8 heads x 128 bf16) cannot stay on chip (302 MB at configs[1] versus
 //      ~170 MB of registers + LDS on 256 CUs), and a slab's scale needs its amax over all
 //      tokens, so each step reads one 256-byte slab of every row, with NB = 4 steps in
@@ -57,7 +61,35 @@ __global__ void plain_stream(const char *__restrict__ src, char *__restrict__ ds
   }
 }
 
-// ---------------------------------------------------------------- 2. append pattern
+// ---------------------------------------------------------------- 2. random page runs
+
+// Workgroup w reads runs w*R .. w*R + R - 1 of the list (2 KiB each, 8 bytes per lane per
+// run); with WRITE it stores 16 bytes per lane per run contiguously (the bf16 output).
+template <bool WRITE>
+__global__ void __launch_bounds__(256) page_runs(const char *__restrict__ pool, const long *__restrict__ runs,
+                                                 long n_runs, char *__restrict__ out, unsigned *sink) {
+  constexpr int R = 4;
+  unsigned acc = 0;
+  sc_v2u v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long k = (long)blockIdx.x * R + r;
+    v[r] = k < n_runs ? __builtin_nontemporal_load(reinterpret_cast<const sc_v2u *>(pool + runs[k]) + threadIdx.x)
+                      : sc_v2u{0, 0};
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long k = (long)blockIdx.x * R + r;
+    if (WRITE && k < n_runs) {
+      const sc_v4u o = {v[r].x, v[r].y ^ 1u, v[r].x ^ 2u, v[r].y ^ 3u};
+      __builtin_nontemporal_store(o, reinterpret_cast<sc_v4u *>(out + k * 4096) + threadIdx.x);
+    }
+    acc ^= v[r].x ^ v[r].y;
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+// ---------------------------------------------------------------- 3. append pattern
 
 constexpr int SC_TPB = 1024;
 constexpr int SC_CT = 64;  // tokens per chunk: 64 x 16 vectors = one 16-byte vector per lane
@@ -177,6 +209,36 @@ int main() {
     const float ms = best_ms([&] { plain_stream<8, 16><<<(unsigned)((n + 255) / 256), 256>>>(x, out, n); }, 5);
     printf("plain stream 1:2 (read %.3f GB, write %.3f GB): %.3f ms, %.1f GB/s\n", n * 8 / 1e9, n * 16 / 1e9, ms,
            n * 24.0 / ms / 1e6);
+  }
+  {  // random 2 KiB runs of a 300,000-page pool (32 KiB pages: K and V x 8 heads x 2 KiB)
+    const long n_pool_pages = 300000, page = 32768;
+    const long pool_bytes = n_pool_pages * page;  // 9.83 GB
+    char *pool = nullptr;
+    SC_CHECK(hipMalloc(&pool, pool_bytes));
+    SC_CHECK(hipMemset(pool, 0x22, pool_bytes));
+    // 64 sequences x 2048 pages x 2 (K, V) x 8 heads runs, pages drawn at random
+    const long n_runs = 64L * 2048 * 2 * 8;
+    long *runs_h = (long *)malloc(n_runs * sizeof(long));
+    unsigned long long x = 88172645463325252ull;
+    for (long i = 0; i < n_runs / 16; ++i) {
+      x ^= x << 13, x ^= x >> 7, x ^= x << 17;
+      const long pg = (long)(x % (unsigned long long)n_pool_pages);
+      for (int j = 0; j < 16; ++j) runs_h[i * 16 + j] = pg * page + j * 2048;  // K and V runs of 8 heads
+    }
+    long *runs = nullptr;
+    SC_CHECK(hipMalloc(&runs, n_runs * sizeof(long)));
+    SC_CHECK(hipMemcpy(runs, runs_h, n_runs * sizeof(long), hipMemcpyHostToDevice));
+    free(runs_h);
+    unsigned *sink = counter;
+    const unsigned blocks = (unsigned)((n_runs + 3) / 4);
+    float ms = best_ms([&] { page_runs<false><<<blocks, 256>>>(pool, runs, n_runs, out, sink); }, 5);
+    printf("random 2 KiB page runs, read only (%.3f GB): %.3f ms, %.1f GB/s\n", n_runs * 2048 / 1e9, ms,
+           n_runs * 2048.0 / ms / 1e6);
+    ms = best_ms([&] { page_runs<true><<<blocks, 256>>>(pool, runs, n_runs, out, sink); }, 5);
+    printf("random 2 KiB page runs + 2 B written per byte read (%.3f GB moved): %.3f ms, %.1f GB/s\n",
+           n_runs * 6144 / 1e9, ms, n_runs * 6144.0 / ms / 1e6);
+    SC_CHECK(hipFree(pool));
+    SC_CHECK(hipFree(runs));
   }
   const int chunks = (int)((T + SC_CT - 1) / SC_CT);
   if ((long)ncu * SC_K < chunks) {
