@@ -1,0 +1,98 @@
+"""Parity at BASELINE's full sizes, on the exact workloads bench.py times.
+
+* configs[1] (seed 1: 32 layers x 74,902 tokens, 8 KV heads, D = 128, page 16, outlier
+  heads x50): one fused append of all layers; for sampled layers every scale is checked
+  bit-exact against the oracle's amax over the whole layer, and the codes of 2,048
+  sampled token rows (all K/V, heads and channels) bit-exact against the oracle's
+  append of those rows with the oracle's scales.
+* configs[2] (64 x 32,768 positions, 300,000-page pool): the full gather; 4,096 sampled
+  positions of every (sequence, head) checked bit-exact against the oracle's dequant.
+* the decode attention over the same pool, two whole sequences checked against the
+  oracle within the stated tolerance (one bf16 ulp plus 2^-17 max|V|).
+"""
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import oracle as O
+from zenyx_amd import kv
+from test_gpu_attention import assert_within_one_ulp
+
+pytestmark = pytest.mark.gpu
+
+
+def bits16(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_configs1_full_append_sampled_layers(dev):
+    W = bench.make_append_workload(torch, dev, seed=1)
+    print(f"configs[1]: {W['T']} tokens x {W['L']} layers", flush=True)
+    sc = kv.kv_quant_append(W["x"], W["cu"], W["bt"], W["pool"], check=True)
+    torch.cuda.synchronize()
+    L, H, D, P, T = W["L"], W["H"], W["D"], W["P"], W["T"]
+    cu, bt = W["cu_host"].numpy(), W["bt_host"].numpy()
+    rng = np.random.default_rng(11)
+    for layer in (0, 13, 31):
+        xb = bits16(W["x"][layer])  # [T, 2, H, D]
+        wsc = O.kv_scales(xb[None])[0]
+        np.testing.assert_array_equal(sc[layer].cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+        S = 2048
+        tok = np.sort(rng.choice(T, S, replace=False))
+        b = np.searchsorted(cu, tok, side="right") - 1
+        pos = tok - cu[b]
+        page = bt[b, pos // P]
+        got = W["pool"][layer].cpu().numpy()[page, :, :, pos % P, :]  # [S, 2, H, D]
+        compact = np.zeros((1, S // P, 2, H, P, D), np.uint8)
+        _, werr = O.kv_quant_append(np.ascontiguousarray(xb[tok])[None], np.array([0, S], np.int32), None,
+                                    np.arange(S // P, dtype=np.int32)[None], compact, P, scales=wsc[None])
+        assert werr == 0
+        want = compact[0].transpose(0, 3, 1, 2, 4).reshape(S, 2, H, D)
+        np.testing.assert_array_equal(got, want)
+        print(f"layer {layer}: scales and {S} rows bit-exact", flush=True)
+
+
+def test_configs2_full_gather_and_attention(dev):
+    G = bench.make_gather_workload(torch, dev)
+    B, H, D, P, T = G["B"], G["H"], G["D"], G["P"], G["T"]
+    sc = G["scales"][G["layer"]].contiguous()
+    k, v = kv.kv_gather_dequant(G["pool"], sc, G["bt"], G["seq_lens"], T, check=True)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(5)
+    S = 4096
+    t = np.sort(rng.choice(T, S, replace=False))
+    bt = G["bt_host"].numpy()
+    scl = G["scales_host"][G["layer"]].numpy()
+    dec = O.e4m3_decode(np.arange(256, dtype=np.uint8))
+    for b in (0, 21, 63):
+        pages = torch.from_numpy(bt[b, t // P].astype(np.int64)).to(dev)
+        codes = G["pool"][pages].cpu().numpy()  # [S, 2, H, P, D]
+        for kvi, out in ((0, k), (1, v)):
+            c = codes[np.arange(S), kvi, :, t % P, :]  # [S, H, D]
+            want = O.bf16_rne(dec[c] * scl[kvi][None, :, None])
+            got = bits16(out[b][:, t, :]).transpose(1, 0, 2)  # [S, H, D]
+            np.testing.assert_array_equal(got, want)
+    print("gather: 3 sequences x 4096 positions bit-exact", flush=True)
+    del k, v
+    torch.cuda.empty_cache()
+
+    Hq = 32
+    q = torch.randn((B, Hq, D), generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    out = kv.paged_attention_decode(q.to(dev), G["pool"], sc, G["bt"], G["seq_lens"], check=True)
+    torch.cuda.synchronize()
+    for b in (0, 40):
+        pages = np.unique(bt[b])
+        sub = G["pool"][torch.from_numpy(pages.astype(np.int64)).to(dev)].cpu().numpy()
+        remap = np.full(bt.max() + 1, -1, np.int64)
+        remap[pages] = np.arange(len(pages))
+        bt_b = remap[bt[b]][None].astype(np.int32)
+        qb = bits16(q[b:b + 1])
+        sm = float(np.float32(1.0 / np.sqrt(D)))
+        want, err = O.paged_attention_decode(qb, sub, scl, bt_b, np.array([T], np.int32), sm)
+        assert err == 0
+        vcodes = sub[:, 1]  # [pages, H, P, D]
+        vmax = np.abs(dec[vcodes].astype(np.float64)).max(axis=(0, 2)) * scl[1][:, None]  # [H, D]
+        vmax_q = np.repeat(vmax, Hq // H, axis=0)[None]  # [1, Hq, D]
+        assert_within_one_ulp(bits16(out[b:b + 1]), want, vmax_q)
+    print("attention: 2 sequences x 32 heads within tolerance", flush=True)
