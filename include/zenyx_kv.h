@@ -256,6 +256,35 @@ int64_t zx_ring_curriculum_trace_len(const int32_t *degrees, const int32_t *ctx_
 int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, int32_t n_steps, int32_t n_layers,
                              int32_t layer_stride, int32_t *out, int64_t out_len, zx_stream_t stream);
 
+/* Blocks of queries attending to K/V straight from the paged FP8 pool: one ring step of
+ * QuantizedRingAttention (README.md:344, code absent).  Query row i of sequence b (rows
+ * [cu_q[b], cu_q[b+1]) of q [n_q][n_q_heads][128] bf16, device) sits at position
+ * q_pos0[b] + i - cu_q[b]; query head hq reads kv head hq / (n_q_heads / n_kv_heads) at
+ * key positions kp in [kv_begin[b], kv_end[b]) (device int32), with kp <= the query's
+ * position when `causal`:
+ *   s = sm_scale * q . K_kp,  o = sum_kp softmax(s)_kp V_kp,  K/V = decode(code) * scale,
+ *   lse2 = log2(sum_kp exp(s))  (-inf and o = 0 when no key qualifies).
+ * Pool layer [n_pages][2][n_kv_heads][page_size][128] e4m3 codes, scales [2][n_kv_heads]
+ * fp32, block tables [n_seqs][max_blocks] int32 (an entry outside [0, n_pages) skips its
+ * keys and sets ZX_KERR_PAGE_RANGE in *err; kv_end beyond max_blocks * page_size is
+ * clipped and sets ZX_KERR_POS_RANGE).  max_q_per_seq >= every sequence's query count
+ * (host int).  flags:
+ *   ZX_PREFILL_MERGE: merge (o, lse2) into o_acc [n_q][n_q_heads][128] fp32 (normalised
+ *     rows) and lse2 [n_q][n_q_heads] fp32, which hold the steps so far;
+ *   ZX_PREFILL_INIT (with MERGE): the first step: overwrite instead of merging;
+ *   ZX_PREFILL_BF16: also write the (merged) rows to out as bf16.
+ * Running every step of a ring with MERGE (INIT on the first) and BF16 on the last gives
+ * attention over the union of the steps' key ranges.  Needs head_dim 128 and a page size
+ * that is a multiple of 16. */
+enum { ZX_PREFILL_MERGE = 1, ZX_PREFILL_INIT = 2, ZX_PREFILL_BF16 = 4 };
+int zx_paged_attention_prefill(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int32_t *q_pos0,
+                               int32_t n_q_heads, const uint8_t *pool, int64_t n_pages, int32_t n_kv_heads,
+                               int32_t head_dim, int32_t page_size, const float *scales,
+                               const int32_t *block_tables, int32_t max_blocks, const int32_t *kv_begin,
+                               const int32_t *kv_end, int32_t n_seqs, int32_t max_q_per_seq, int32_t causal,
+                               float sm_scale, int32_t flags, float *o_acc, float *lse2, uint16_t *out,
+                               int32_t *err, zx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

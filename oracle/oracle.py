@@ -59,6 +59,8 @@ def lib() -> ctypes.CDLL:
             "zxo_ring_curriculum_trace": (i64, [P, P, i32, i32, i32, P]),
             "zxo_ring_trace": (None, [i32, i32, i32, P]),
             "zxo_paged_attention_decode": (i32, [P, i32, P, i64, i32, i32, i32, P, P, i32, P, i32, f32, P]),
+            "zxo_paged_attention_prefill": (i32, [P, P, P, i32, P, i64, i32, i32, i32, P, P, i32, P, P, i32, i32,
+                                                  f32, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -198,6 +200,26 @@ def paged_attention_decode(q_bits, pool_layer, scales_layer, block_tables, seq_l
     err = lib().zxo_paged_attention_decode(_p(q_bits), Hq, _p(pool_layer), n_pages, Hkv, D, P, _p(sc), _p(bt),
                                            bt.shape[1], _p(sl), B, float(sm_scale), _p(out))
     return out, int(err)
+
+
+def paged_attention_prefill(q_bits, cu_q, q_pos0, pool_layer, scales_layer, block_tables, kv_begin, kv_end,
+                            causal: bool, sm_scale: float):
+    """Block attention over the FP8 pages; q_bits [n_q, Hq, D] uint16.  Returns
+    (out bf16 bits [n_q, Hq, D], lse2 float32 [n_q, Hq], error bits)."""
+    q_bits = np.ascontiguousarray(q_bits, dtype=np.uint16)
+    pool_layer = np.ascontiguousarray(pool_layer, dtype=np.uint8)
+    n_q, Hq, D = q_bits.shape
+    n_pages, _, Hkv, P, _ = pool_layer.shape
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    cu = np.ascontiguousarray(cu_q, dtype=np.int32)
+    out = np.zeros_like(q_bits)
+    lse = np.empty((n_q, Hq), np.float32)
+    err = lib().zxo_paged_attention_prefill(
+        _p(q_bits), _p(cu), _p(np.ascontiguousarray(q_pos0, dtype=np.int32)), Hq, _p(pool_layer), n_pages, Hkv, D,
+        P, _p(np.ascontiguousarray(scales_layer, dtype=np.float32)), _p(bt), bt.shape[1],
+        _p(np.ascontiguousarray(kv_begin, dtype=np.int32)), _p(np.ascontiguousarray(kv_end, dtype=np.int32)),
+        cu.size - 1, int(causal), sm_scale, _p(out), _p(lse))
+    return out, lse, int(err)
 
 
 def int8_legacy_quant(x: np.ndarray, dtype: str):

@@ -322,6 +322,80 @@ int32_t zxo_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, const u
 
 /* ---------------------------------------------------------------- legacy int8 */
 
+/* Block attention over the paged FP8 K/V: one ring step of QuantizedRingAttention
+ * (README.md:344; semantics defined by include/zenyx_kv.h).  Query token i of sequence b
+ * (rows [cu_q[b], cu_q[b+1]) of q [n_q][Hq][D] bf16) sits at position q_pos0[b] + i -
+ * cu_q[b]; query head hq reads kv head hq / (Hq / Hkv) at key positions kp in
+ * [kv_begin[b], kv_end[b]) with kp <= the query's position when causal:
+ *   s = sm_scale * q . K_kp,  out = sum softmax(s)_kp V_kp   (K, V = decode(code) * scale)
+ * in double, out rounded once to bf16 (via fp32); lse2 [n_q][Hq] = log2(sum exp(s)) in
+ * fp32 (-inf and out = 0 when no key qualifies).  Returns error bits (1: a block-table
+ * entry outside [0, n_pages), whose keys are skipped; 2: kv_end beyond max_blocks *
+ * page_size, clipped). */
+int32_t zxo_paged_attention_prefill(const uint16_t *q, const int32_t *cu_q, const int32_t *q_pos0,
+                                    int32_t n_q_heads, const uint8_t *pool, int64_t n_pages, int32_t n_kv_heads,
+                                    int32_t head_dim, int32_t page_size, const float *scales,
+                                    const int32_t *block_tables, int32_t max_blocks, const int32_t *kv_begin,
+                                    const int32_t *kv_end, int32_t n_seqs, int32_t causal, float sm_scale,
+                                    uint16_t *out, float *lse2) {
+  int32_t err = 0;
+  const int32_t grp = n_q_heads / n_kv_heads;
+  const int64_t page_bytes = 2LL * n_kv_heads * page_size * head_dim;
+  double *s = NULL, *acc = malloc(sizeof(double) * head_dim);
+  int64_t *pg = NULL, cap = 0;
+  for (int32_t b = 0; b < n_seqs; ++b) {
+    int64_t kb = kv_begin[b] > 0 ? kv_begin[b] : 0, ke = kv_end[b];
+    if (ke > (int64_t)max_blocks * page_size) { err |= 2; ke = (int64_t)max_blocks * page_size; }
+    const int64_t nk = ke > kb ? ke - kb : 0;
+    if (nk > cap) {
+      cap = nk;
+      s = realloc(s, sizeof(double) * (size_t)cap);
+      pg = realloc(pg, sizeof(int64_t) * (size_t)cap);
+    }
+    for (int64_t i = cu_q[b]; i < cu_q[b + 1]; ++i) {
+      const int64_t qp = (int64_t)q_pos0[b] + (i - cu_q[b]);
+      for (int32_t hq = 0; hq < n_q_heads; ++hq) {
+        const int32_t h = hq / grp;
+        const uint16_t *qv = q + (i * n_q_heads + hq) * head_dim;
+        uint16_t *o = out + (i * n_q_heads + hq) * head_dim;
+        double m = -INFINITY;
+        for (int64_t j = 0; j < nk; ++j) {
+          const int64_t t = kb + j;
+          pg[j] = -1;
+          if (causal && t > qp) continue;
+          const int64_t page = block_tables[(int64_t)b * max_blocks + t / page_size];
+          if (page < 0 || page >= n_pages) { err |= 1; continue; }
+          pg[j] = page;
+          const uint8_t *kr = pool + page * page_bytes + ((int64_t)h * page_size + t % page_size) * head_dim;
+          double dot = 0.0;
+          for (int32_t d = 0; d < head_dim; ++d)
+            dot += (double)zxo_bf16_to_f32(qv[d]) * ((double)zxo_e4m3_decode(kr[d]) * (double)scales[h]);
+          s[j] = dot * (double)sm_scale;
+          if (s[j] > m) m = s[j];
+        }
+        double l = 0.0;
+        for (int32_t d = 0; d < head_dim; ++d) acc[d] = 0.0;
+        for (int64_t j = 0; j < nk; ++j) {
+          if (pg[j] < 0) continue;
+          const int64_t t = kb + j;
+          const double p = exp(s[j] - m);
+          const uint8_t *vr = pool + pg[j] * page_bytes +
+                              ((int64_t)(n_kv_heads + h) * page_size + t % page_size) * head_dim;
+          l += p;
+          for (int32_t d = 0; d < head_dim; ++d)
+            acc[d] += p * ((double)zxo_e4m3_decode(vr[d]) * (double)scales[n_kv_heads + h]);
+        }
+        for (int32_t d = 0; d < head_dim; ++d) o[d] = l > 0.0 || isnan(l) ? zxo_bf16_rne((float)(acc[d] / l)) : 0;
+        if (lse2) lse2[i * n_q_heads + hq] = l > 0.0 ? (float)((m + log(l)) / log(2.0)) : -INFINITY;
+      }
+    }
+  }
+  free(s);
+  free(pg);
+  free(acc);
+  return err;
+}
+
 /* Round a float to the storage dtype and back (0 bf16, 1 f16, 2 f32), as torch stores
  * every intermediate of precision.py:10-11 in the input dtype. */
 static float to_dtype(float v, int dtype) {

@@ -1,0 +1,140 @@
+"""Blocks of queries over the FP8 pages (one ring step of QuantizedRingAttention,
+README.md:344) and ring attention composed from such steps on one GPU, against the C
+oracle (itself pinned against torch float64 in test_oracle.py).
+
+Tolerance, as for decode attention: the kernel computes scores in fp32 on matrix cores
+(bf16 q, K codes exact in bf16), an exp2-domain online softmax and P.V with P split into
+bf16 hi + lo; so |got - want| <= one bf16 ulp of the exact value + 2^-17 max|V| per
+channel.  lse2 (log2 of the softmax denominator) within 2e-5 (absolute + relative).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from zenyx_amd import kv
+from test_gpu_attention import assert_within_one_ulp
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def bits16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def make(Hq, Hkv, P, n_q, q_pos0, kv_len, seed, n_pages=None):
+    rng = np.random.default_rng(seed)
+    D = 128
+    B = len(n_q)
+    max_blocks = max(1, -(-max(kv_len) // P))
+    n_pages = n_pages or B * max_blocks + 3
+    pool = rng.integers(0, 256, (n_pages, 2, Hkv, P, D), dtype=np.uint8)
+    pool[(pool & 0x7F) == 0x7F] = 0x3A
+    perm = rng.permutation(n_pages)
+    bt = perm[:B * max_blocks].reshape(B, max_blocks).astype(np.int32)
+    scales = rng.uniform(1e-3, 0.05, (2, Hkv)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(n_q)]).astype(np.int32)
+    q = torch.from_numpy(rng.standard_normal((int(cu[-1]), Hq, D)).astype(np.float32)).to(torch.bfloat16)
+    return q, pool, scales, bt, cu, np.asarray(q_pos0, np.int32)
+
+
+def vmax_rows(pool, scales, bt, cu, kv_begin, kv_end, Hq):
+    """Per (row, query head, channel): max |V| over the sequence's key range (a bound
+    for the keys the row actually uses)."""
+    dec = np.abs(O.e4m3_decode(np.arange(256, dtype=np.uint8)).astype(np.float64))
+    n_pages, _, Hkv, P, D = pool.shape
+    out = np.zeros((int(cu[-1]), Hq, D))
+    for b in range(len(cu) - 1):
+        t = np.arange(kv_begin[b], kv_end[b])
+        if t.size == 0:
+            continue
+        pages = bt[b, t // P]
+        for hq in range(Hq):
+            h = hq // (Hq // Hkv)
+            out[cu[b]:cu[b + 1], hq] = dec[pool[pages, 1, h, t % P, :]].max(axis=0) * float(scales[1, h])
+    return out
+
+
+def run_step(q, pool, scales, bt, cu, q_pos0, kb, ke, causal):
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    o_acc = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+    lse = torch.empty(q.shape[:2], dtype=torch.float32, device=DEV)
+    out = kv.paged_attention_prefill(q.to(DEV), t(cu), t(q_pos0), t(pool), t(scales), t(bt), t(kb), t(ke),
+                                     causal=causal, o_acc=o_acc, lse2=lse, first=True, check=True)
+    return out, lse
+
+
+CASES = [  # Hq, Hkv, P, n_q, q_pos0, kv_begin, kv_end
+    (8, 2, 16, [37, 5, 64], [0, 20, 100], [0, 3, 17], [37, 25, 164]),
+    (32, 8, 16, [130, 1], [500, 0], [0, 0], [630, 1]),
+    (4, 4, 32, [70, 33], [0, 64], [5, 70], [70, 70]),       # second: empty key range
+    (6, 3, 16, [20, 0, 45], [10, 0, 5], [0, 0, 0], [30, 0, 50]),  # a sequence with no queries
+    (2, 1, 48, [129], [300], [40], [429]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_step_matches_oracle(case, causal):
+    Hq, Hkv, P, n_q, q_pos0, kb, ke = CASES[case]
+    print(f"prefill step case {case} causal={causal}", flush=True)
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, n_q, q_pos0, ke, seed=case)
+    kb, ke = np.asarray(kb, np.int32), np.asarray(ke, np.int32)
+    out, lse = run_step(q, pool, scales, bt, cu, qp, kb, ke, causal)
+    torch.cuda.synchronize()
+    sm = float(np.float32(1.0 / np.sqrt(128)))
+    want, wlse, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, kb, ke, causal, sm)
+    assert err == 0
+    assert_within_one_ulp(bits16(out), want, vmax_rows(pool, scales, bt, cu, kb, ke, Hq))
+    g = lse.cpu().numpy()
+    fin = np.isfinite(wlse)
+    np.testing.assert_array_equal(np.isfinite(g), fin)
+    assert np.all(np.abs(g[fin] - wlse[fin]) <= 2e-5 * (1 + np.abs(wlse[fin])))
+
+
+_RING_CASE = {}
+
+
+def _ring_case():
+    """One set of inputs and its oracle result, shared by the ring degrees."""
+    if not _RING_CASE:
+        Hq, Hkv, P = 32, 8, 16
+        n_q, lens, q_pos0 = [256, 77, 512], [256, 300, 1024], [0, 223, 512]  # queries end at the last key
+        q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, n_q, q_pos0, lens, seed=41)
+        zeros, lens_a = np.zeros(len(lens), np.int32), np.asarray(lens, np.int32)
+        sm = float(np.float32(1.0 / np.sqrt(128)))
+        want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, zeros, lens_a, True, sm)
+        assert err == 0
+        _RING_CASE.update(q=q, pool=pool, scales=scales, bt=bt, cu=cu, qp=qp, lens=lens_a, want=want,
+                          vmax=vmax_rows(pool, scales, bt, cu, zeros, lens_a, Hq))
+    return _RING_CASE
+
+
+@pytest.mark.parametrize("ring", [1, 3, 8])
+def test_ring_attention_equals_full_attention(ring):
+    c = _ring_case()
+    print(f"ring {ring}", flush=True)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    out = kv.ring_attention_fp8(c["q"].to(DEV), t(c["cu"]), t(c["qp"]), t(c["pool"]), t(c["scales"]), t(c["bt"]),
+                                t(c["lens"]), ring_degree=ring, causal=True, check=True)
+    torch.cuda.synchronize()
+    assert_within_one_ulp(bits16(out), c["want"], c["vmax"])
+
+
+def test_prefill_flags_bad_pages():
+    Hq, Hkv, P = 8, 2, 16
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, [40], [0], [64], seed=9, n_pages=8)
+    bt = bt.copy()
+    bt[0, 1] = 1000  # keys 16..31 on a page outside the pool
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    kb, ke = np.zeros(1, np.int32), np.full(1, 64, np.int32)
+    with pytest.raises(ValueError, match="block table"):
+        kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kb), t(ke), causal=False,
+                                   check=True)
+    out = kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kb), t(ke), causal=False)
+    torch.cuda.synchronize()
+    sm = float(np.float32(1.0 / np.sqrt(128)))
+    want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, kb, ke, False, sm)
+    assert err & 1
+    assert_within_one_ulp(bits16(out), want, vmax_rows(pool, scales, np.where(bt < 8, bt, 0), cu, kb, ke, Hq))

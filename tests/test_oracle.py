@@ -391,3 +391,52 @@ def test_paged_attention_oracle_matches_torch_sdpa(Hq, Hkv, D, P, seed):
                 want = (p @ V).float().to(torch.bfloat16)
             w = want.view(torch.int16).numpy().view(np.uint16)
             np.testing.assert_array_equal(got[b, hq], w)
+
+
+@pytest.mark.parametrize("Hq,Hkv,P,causal,seed", [(8, 2, 16, 1, 0), (4, 4, 32, 0, 1), (6, 3, 16, 1, 2),
+                                                   (2, 1, 48, 0, 3)])
+def test_prefill_attention_oracle_matches_torch(Hq, Hkv, P, causal, seed):
+    """The oracle's block attention (one ring step) against torch's float64
+    softmax(qK^T)V with an explicit key range and causal mask, K/V built by numpy indexing
+    of the pool; includes a query block starting mid-sequence, a key range starting
+    mid-page and an empty key range (zeros, lse -inf)."""
+    rng = np.random.default_rng(seed)
+    D = 128
+    n_q = [5, 17, 3]
+    q_pos0 = np.array([0, 40, 100], np.int32)
+    kv_begin = np.array([0, 9, 60], np.int32)
+    kv_end = np.array([5, 61, 60], np.int32)
+    cu = np.concatenate([[0], np.cumsum(n_q)]).astype(np.int32)
+    max_blocks = 8
+    n_pages = 40
+    pool = rng.integers(0, 256, (n_pages, 2, Hkv, P, D), dtype=np.uint8)
+    pool[(pool & 0x7F) == 0x7F] = 0x12
+    bt = np.stack([rng.permutation(n_pages)[:max_blocks] for _ in range(3)]).astype(np.int32)
+    scales = rng.uniform(1e-3, 0.05, (2, Hkv)).astype(np.float32)
+    q = torch.randn((cu[-1], Hq, D), generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16)
+    qb = q.view(torch.int16).numpy().view(np.uint16)
+    sm = float(np.float32(1.0 / np.sqrt(D)))
+    got, lse, err = O.paged_attention_prefill(qb, cu, q_pos0, pool, scales, bt, kv_begin, kv_end, causal, sm)
+    assert err == 0
+    dec = O.e4m3_decode(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    grp = Hq // Hkv
+    for b in range(3):
+        for i in range(cu[b], cu[b + 1]):
+            qp = q_pos0[b] + i - cu[b]
+            t = np.arange(kv_begin[b], kv_end[b])
+            if causal:
+                t = t[t <= qp]
+            pages = bt[b, t // P]
+            for hq in range(Hq):
+                h = hq // grp
+                w = got[i, hq]
+                if t.size == 0:
+                    assert np.all(w == 0) and lse[i, hq] == -np.inf
+                    continue
+                K = torch.from_numpy(dec[pool[pages, 0, h, t % P, :]] * float(scales[0, h]))
+                V = torch.from_numpy(dec[pool[pages, 1, h, t % P, :]] * float(scales[1, h]))
+                s = (K @ q[i, hq].double()) * sm
+                want = (torch.softmax(s, dim=0) @ V).float().to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+                np.testing.assert_array_equal(w, want)
+                want_lse = float(torch.logsumexp(s, dim=0)) / np.log(2.0)
+                assert abs(lse[i, hq] - want_lse) <= 2e-6 * max(1.0, abs(want_lse))

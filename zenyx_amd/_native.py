@@ -24,6 +24,7 @@ ZX_BF16, ZX_F16, ZX_F32 = 0, 1, 2
 ZX_KERR_PAGE_RANGE, ZX_KERR_POS_RANGE, ZX_KERR_SPIN = 1, 2, 4
 ZX_APPEND_STATIC_SCALES = 1
 ZX_APPEND_TWO_PASS = 2
+ZX_PREFILL_MERGE, ZX_PREFILL_INIT, ZX_PREFILL_BF16 = 1, 2, 4
 ZX_NEVER = 0x7FFFFFFF
 ABI_VERSION = 1
 
@@ -60,6 +61,8 @@ SIGNATURES = {
     "zx_belady_tier_plan": (_INT, [_P, _P, _P, _I64, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P, _P]),
     "zx_ring_curriculum_trace_len": (_I64, [_P, _P, _I32, _I32]),
     "zx_ring_curriculum_trace": (_INT, [_P, _P, _I32, _I32, _I32, _P, _I64, _P]),
+    "zx_paged_attention_prefill": (_INT, [_P, _I64, _P, _P, _I32, _P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P,
+                                          _P, _I32, _I32, _I32, ctypes.c_float, _I32, _P, _P, _P, _P, _P]),
 }
 
 _lib = None

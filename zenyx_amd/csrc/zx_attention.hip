@@ -18,7 +18,7 @@
 // (m, l, acc[D]) per query head is written to the workspace.  Pass 2
 // (paged_decode_combine_kernel) merges the splits of a (sequence, query head) and writes
 // bf16.
-#include "zx_common.h"
+#include "zx_attn_common.h"
 
 namespace zx {
 
@@ -26,7 +26,6 @@ constexpr int ATT_THREADS = 256;  // 4 waves
 constexpr int ATT_WAVES = ATT_THREADS / 64;
 constexpr int ATT_U = 4;          // passes per online-softmax step
 constexpr int ATT_SPLIT_MIN = 1024;  // positions per block: a multiple of this, chosen per call
-constexpr float ATT_LOG2E = 1.4426950408889634f;
 
 struct AttnGeom {
   int32_t n_q_heads, n_kv_heads, head_dim, page_size, max_blocks, n_seqs;
@@ -49,30 +48,6 @@ __device__ __forceinline__ void decode16(uint4 c, float (&f)[16]) {
   e4m3x4_decode(c.w, f[12], f[13], f[14], f[15]);
 }
 
-typedef __bf16 att_bf2 __attribute__((ext_vector_type(2)));
-// 16 e4m3 codes -> 8 bf16 pairs (exact: every e4m3 value is a bf16 value).
-__device__ __forceinline__ void decode16_bf16(uint4 c, uint32_t (&b)[8]) {
-  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    b[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[i], 1.0f, false));
-    b[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w[i], 1.0f, true));
-  }
-}
-
-template <int CTRL> __device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-// Sum over aligned groups of N lanes inside a 16-lane row, by DPP (quad_perm swaps, then
-// half-row and row mirrors, which pair groups whose lanes already agree; every lane of a
-// group ends with the result).
-template <int N> __device__ __forceinline__ float group_sum(float v) {
-  if (N >= 2) v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
-  if (N >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
-  if (N >= 8) v += dpp<0x141>(v);  // row_half_mirror
-  if (N >= 16) v += dpp<0x140>(v); // row_mirror
-  return v;
-}
 // Across 16-lane rows: the lane 16 and 32 positions away (ds_bpermute).  (The
 // v_permlane16/32_swap builtins return one of their two outputs twice with this
 // compiler, so they are not used.)
@@ -334,21 +309,12 @@ paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const ui
 // layout: lanes 0-15 hold heads 0-3 of token l % 16, so the softmax bookkeeping is a
 // 16-lane DPP reduction; the O accumulators (8 tiles of 16 channels) live in MFMA
 // results, rows = heads.
-typedef __bf16 att_bf16x8 __attribute__((ext_vector_type(8)));
-typedef float att_f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int att_u32x4 __attribute__((ext_vector_type(4)));
 constexpr int AM_VROW = 80;                 // bytes per channel row of V^T (64 + 16 pad)
 constexpr int AM_VBYTES = 128 * AM_VROW;    // one wave's V^T (32 tokens)
 constexpr int AM_PBYTES = 4 * 32 * 4;       // one wave's P (4 heads x 32 tokens fp32)
 constexpr int AM_KROW = 144;                // bytes per token row of the K staging (128 + 16 pad)
 constexpr int AM_KBYTES = 32 * AM_KROW;     // one wave's K codes (32 tokens)
 
-__device__ __forceinline__ float row16_max(float v) {  // max over lanes 0-15 of each row
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  return fmaxf(v, dpp<0x140>(v));
-}
 
 template <int G>
 __global__ void __launch_bounds__(ATT_THREADS)

@@ -290,6 +290,92 @@ def paged_attention_decode(q: torch.Tensor, pool_layer: torch.Tensor, scales_lay
 
 # ------------------------------------------------------------------ Belady
 
+def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor, pool_layer: torch.Tensor,
+                            scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_begin: torch.Tensor,
+                            kv_end: torch.Tensor, causal: bool = True, sm_scale: float | None = None,
+                            o_acc: torch.Tensor | None = None, lse2: torch.Tensor | None = None,
+                            first: bool = True, out: torch.Tensor | None = None, write_bf16: bool = True,
+                            max_q_per_seq: int | None = None, check: bool = False):
+    """One ring step of attention over the FP8 pages (zx_paged_attention_prefill).
+
+    ``q`` [n_q, Hq, 128] bf16 rows of all sequences (``cu_q`` [B+1] int32 offsets,
+    ``q_pos0`` [B] int32 position of each sequence's first query row); keys
+    [kv_begin[b], kv_end[b]) of the pool layer through the block tables.  With ``o_acc``
+    / ``lse2`` (fp32 [n_q, Hq, 128] / [n_q, Hq]) the step merges into them (``first``
+    overwrites); with ``write_bf16`` the (merged) rows go to ``out`` as bf16.  Returns
+    ``out`` (or None)."""
+    N.require_device(q, "q")
+    if q.dtype != torch.bfloat16 or q.dim() != 3:
+        raise ValueError("q must be [n_q, n_q_heads, head_dim] bfloat16")
+    N.require_device(pool_layer, "pool_layer")
+    n_pages, two, Hkv, P, D = pool_layer.shape
+    n_q, Hq, Dq = q.shape
+    if two != 2 or Dq != D:
+        raise ValueError("pool_layer must be [n_pages, 2, n_kv_heads, page_size, head_dim] matching q")
+    for t, name in ((cu_q, "cu_q"), (q_pos0, "q_pos0"), (block_tables, "block_tables"), (kv_begin, "kv_begin"),
+                    (kv_end, "kv_end")):
+        N.require_device(t, name)
+        if t.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32")
+    B = cu_q.numel() - 1
+    if q_pos0.numel() != B or kv_begin.numel() != B or kv_end.numel() != B or block_tables.shape[0] != B:
+        raise ValueError("cu_q, q_pos0, kv_begin, kv_end and block_tables disagree on the number of sequences")
+    if (o_acc is None) != (lse2 is None):
+        raise ValueError("o_acc and lse2 go together")
+    if o_acc is not None:
+        N.require_device(o_acc, "o_acc")
+        N.require_device(lse2, "lse2")
+        if o_acc.dtype != torch.float32 or o_acc.shape != q.shape or lse2.dtype != torch.float32 or \
+                lse2.shape != (n_q, Hq):
+            raise ValueError("o_acc must be float32 like q, lse2 float32 [n_q, n_q_heads]")
+    if write_bf16:
+        out = torch.empty_like(q) if out is None else out
+        N.require_device(out, "out")
+        if out.shape != q.shape or out.dtype != torch.bfloat16:
+            raise ValueError("out must be bfloat16 like q")
+    if max_q_per_seq is None:
+        max_q_per_seq = int((cu_q[1:] - cu_q[:-1]).max().item()) if B else 0
+    flags = (N.ZX_PREFILL_MERGE if o_acc is not None else 0) | (N.ZX_PREFILL_INIT if o_acc is not None and first
+                                                                else 0) | (N.ZX_PREFILL_BF16 if write_bf16 else 0)
+    sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
+    dev = q.device
+    err = _err_word(dev)
+    N.check(N.load().zx_paged_attention_prefill(
+        N.ptr(q), n_q, N.ptr(cu_q), N.ptr(q_pos0), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer),
+        N.ptr(block_tables), block_tables.shape[1], N.ptr(kv_begin), N.ptr(kv_end), B, int(max_q_per_seq),
+        int(bool(causal)), sm, flags, N.ptr(o_acc), N.ptr(lse2), N.ptr(out if write_bf16 else None), N.ptr(err),
+        N.stream_ptr(dev)), "paged_attention_prefill")
+    if check:
+        _raise_kernel_error(err, "paged_attention_prefill")
+    return out if write_bf16 else None
+
+
+def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor, pool_layer: torch.Tensor,
+                       scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_len: torch.Tensor,
+                       ring_degree: int, causal: bool = True, sm_scale: float | None = None,
+                       check: bool = False) -> torch.Tensor:
+    """Ring attention over the FP8 pages on one GPU: the keys [0, kv_len[b]) of every
+    sequence are split into ``ring_degree`` shards (the KV blocks a ring would pass
+    around), each shard is one ring step (paged_attention_prefill) merged into a running
+    fp32 output and log-sum-exp, and the last step writes bf16.  Equals attention over all
+    keys (the exchange between devices is what one GPU leaves out)."""
+    if ring_degree < 1:
+        raise ValueError("ring_degree must be >= 1")
+    n_q, Hq, D = q.shape
+    o_acc = torch.empty((n_q, Hq, D), dtype=torch.float32, device=q.device)
+    lse2 = torch.empty((n_q, Hq), dtype=torch.float32, device=q.device)
+    out = torch.empty_like(q)
+    kl = kv_len.to(torch.int64)
+    mq = int((cu_q[1:] - cu_q[:-1]).max().item()) if cu_q.numel() > 1 else 0
+    for r in range(ring_degree):
+        kb = (kl * r // ring_degree).to(torch.int32)
+        ke = (kl * (r + 1) // ring_degree).to(torch.int32)
+        paged_attention_prefill(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables, kb, ke, causal=causal,
+                                sm_scale=sm_scale, o_acc=o_acc, lse2=lse2, first=r == 0, out=out,
+                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, check=check)
+    return out
+
+
 def belady_argmax(keys: torch.Tensor, resident: torch.Tensor) -> torch.Tensor:
     """belady.py:39-51 over slots: device int64 ``[slot, key]`` ({-1, -1} if none)."""
     N.ensure_gpu()
