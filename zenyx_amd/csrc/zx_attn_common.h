@@ -41,5 +41,32 @@ __device__ __forceinline__ float row16_max(float v) {  // max over lanes 0-15 of
   v = fmaxf(v, dpp<0x141>(v));
   return fmaxf(v, dpp<0x140>(v));
 }
+// Over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows, lane position kept):
+// v_permlane32_swap pairs lane l with l ^ 32 across its two results, v_permlane16_swap
+// pairs rows 0/1 and 2/3; both results of a swap together hold the pair's two values.
+// (Elements are converted with __uint_as_float: with this compiler __builtin_bit_cast of
+// the builtin's vector result reads element 0 for both.)
+__device__ __forceinline__ void xrow_pair32(float v, float &x, float &y) {
+  auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  x = __uint_as_float(s[0]);
+  y = __uint_as_float(s[1]);
+}
+__device__ __forceinline__ void xrow_pair16(float v, float &x, float &y) {
+  auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  x = __uint_as_float(s[0]);
+  y = __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float xrow_max(float v) {
+  float x, y;
+  xrow_pair32(v, x, y);
+  xrow_pair16(fmaxf(x, y), x, y);
+  return fmaxf(x, y);
+}
+__device__ __forceinline__ float xrow_sum(float v) {
+  float x, y;
+  xrow_pair32(v, x, y);
+  xrow_pair16(x + y, x, y);
+  return x + y;
+}
 
 }  // namespace zx

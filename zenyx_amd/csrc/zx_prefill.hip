@@ -11,10 +11,13 @@
 //     cache lines), one step ahead of the compute; K codes go to LDS staging rows as
 //     they are, V values go transposed into LDS (V^T[channel][key], bf16), both double
 //     buffered so one block barrier per step suffices;
-//   * each wave: S = Q . K^T on v_mfma_f32_16x16x32_bf16 (Q rows as A, K codes converted
-//     to bf16 exactly as B), key range / causal mask, online softmax per row in the exp2
-//     domain (rows live in 16-lane groups of the C layout: DPP reductions), P through
-//     LDS into the A layout split into bf16 hi + lo, O += P . V on the same MFMA.
+//   * each wave computes the transposed problem, so that one query row sits in one lane
+//     column of every MFMA tile: S^T = K . Q^T on v_mfma_f32_16x16x32_bf16 (K codes
+//     converted to bf16 exactly as A, Q rows as B), key range / causal mask only on the
+//     steps that cross a boundary, online softmax in the exp2 domain with row maxima
+//     over the 4 lane rows by v_permlane32/16_swap, P^T kept in registers as the B
+//     operand split into bf16 hi + lo, O^T += V^T . P^T on the same MFMA (the rescale
+//     of O skipped when no row maximum moved).
 // At the end each row is normalised; with MERGE the step's (O, lse2) is combined with
 // the running one in o_acc / lse2 (each (row, head) belongs to one block, so no races);
 // with the bf16 flag the merged row is also written as bf16.
@@ -24,12 +27,14 @@ namespace zx {
 
 constexpr int PF_THREADS = 256;
 constexpr int PF_KEYS = 32;                  // keys per step
-constexpr int PF_KROW = 144;                 // K staging row (128 codes + 16 pad: conflict-free reads)
+constexpr int PF_KROW = 272;                 // K row in LDS (128 channels bf16 + 16 pad: conflict-free reads)
 constexpr int PF_VROW = 80;                  // V^T row (32 keys bf16 + 16 pad)
 constexpr int PF_KBYTES = PF_KEYS * PF_KROW;
 constexpr int PF_VBYTES = 128 * PF_VROW;
-constexpr int PF_PBYTES = 32 * PF_KEYS * 4;  // one wave's P: 32 rows x 32 keys fp32
 constexpr int PF_MERGE = 1, PF_WRITE_BF16 = 2, PF_INIT = 4;
+// a row's running maximum m is raised only when a score exceeds it by more than this
+// (log2 units), so p = 2^(s - m) <= 2^PF_LAZY and O is rarely rescaled
+constexpr float PF_LAZY = 8.0f;
 
 struct PrefillArgs {
   const uint16_t *q;  // [n_q][Hq][128] bf16
@@ -53,7 +58,7 @@ __device__ __forceinline__ uint32_t pf_page_of(const PrefillArgs &a, uint32_t t)
 }
 
 template <int G>
-__global__ void __launch_bounds__(PF_THREADS) paged_prefill_mfma_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(PrefillArgs a) {
   constexpr int D = 128;
   constexpr int QT = 32 * 4 / G;  // query rows per block
   const int b = blockIdx.z;
@@ -61,40 +66,41 @@ __global__ void __launch_bounds__(PF_THREADS) paged_prefill_mfma_kernel(PrefillA
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kg = lane >> 4;
   const int64_t q_lo = a.cu_q[b];
-  const int64_t n_qb = (int64_t)a.cu_q[b + 1] - q_lo;
-  const int64_t row0_blk = (int64_t)blockIdx.x * QT;
-  if (row0_blk >= n_qb) return;
+  const int n_qb = a.cu_q[b + 1] - a.cu_q[b];
+  // the last query tiles see the most keys under a causal mask: they are launched first
+  const int64_t row0_64 = (int64_t)(gridDim.x - 1 - blockIdx.x) * QT;
+  if (row0_64 >= n_qb) return;
+  const int row0_blk = (int)row0_64;
   const int grp = a.n_q_heads / a.n_kv_heads;
   const int hq = blockIdx.y * G + wave % G;
   const int h = hq / grp;
-  const int64_t wrow0 = row0_blk + 32 * (wave / G);  // this wave's first row (in the sequence)
+  const int wrow0 = row0_blk + 32 * (wave / G);  // this wave's first row (in the sequence)
   const int64_t qp0 = a.q_pos0[b];
   const int64_t page_bytes = 2LL * a.n_kv_heads * a.page_size * D;
   const int64_t head_off = (int64_t)h * a.page_size * D;
   const int64_t v_off = (int64_t)a.n_kv_heads * a.page_size * D;
   const int32_t *bt = a.bt + (int64_t)b * a.max_blocks;
   int32_t e = 0;
-  int64_t kb = a.kv_begin[b] > 0 ? a.kv_begin[b] : 0;
-  int64_t ke = a.kv_end[b];
-  if (ke > (int64_t)a.max_blocks * a.page_size) {
+  const int kb = a.kv_begin[b] > 0 ? a.kv_begin[b] : 0;
+  int ke = a.kv_end[b];
+  const int kmax = a.max_blocks * a.page_size;  // < 2^31 (checked by the host)
+  if (ke > kmax) {
     e |= ZX_KERR_POS_RANGE;
-    ke = (int64_t)a.max_blocks * a.page_size;
+    ke = kmax;
   }
   // keys past the block's last query position never count when causal
-  const int64_t last_row = min(row0_blk + QT, n_qb) - 1;
-  const int64_t ke_blk = a.causal ? min(ke, qp0 + last_row + 1) : ke;
+  const int last_row = min(row0_blk + QT, n_qb) - 1;
+  const int ke_blk = a.causal ? (int)max((int64_t)-1, min((int64_t)ke, qp0 + last_row + 1)) : ke;
 
   __shared__ __attribute__((aligned(16))) uint8_t kst[2][PF_KBYTES];
   __shared__ __attribute__((aligned(16))) uint8_t vtl[2][PF_VBYTES];
-  __shared__ __attribute__((aligned(16))) float pls[4][32 * PF_KEYS];
-  float *pl = pls[wave];
 
-  // Q rows as the A operand: lane (n, kg) of row tile rt holds row wrow0 + 16 rt + n,
-  // channels 32 kg + 8 c ..+8 for MFMA c (the same channel order as the K operand)
+  // Q rows as the B operand of S^T = K . Q^T: lane (n, kg) of row tile rt holds row
+  // wrow0 + 16 rt + n, channels 32 kg + 8 c ..+8 for MFMA c (the K operand's channel order)
   att_bf16x8 qa[2][4];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    const int64_t r = wrow0 + 16 * rt + n;
+    const int r = wrow0 + 16 * rt + n;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       att_u32x4 w = {0u, 0u, 0u, 0u};
@@ -106,42 +112,43 @@ __global__ void __launch_bounds__(PF_THREADS) paged_prefill_mfma_kernel(PrefillA
       qa[rt][c] = __builtin_bit_cast(att_bf16x8, w);
     }
   }
-  const float qs = a.scales[h] * a.sm_log2e;            // K's dequant scale folds into the scores
+  const float qs = a.scales[h] * a.sm_log2e;  // K's dequant scale folds into the scores
   const float vscale = a.scales[a.n_kv_heads + h];
 
+  // O^T tiles: o[rt][jt] holds channels 16 jt + 4 kg ..+4 of row 16 rt + n; m and l per
+  // row (l: this lane's share of the row's keys, summed over the 4 lane rows at the end)
   att_f32x4 o[2][8];
-  float m[2][4], l[2][4];
+  float m[2], l[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
     for (int jt = 0; jt < 8; ++jt) o[rt][jt] = att_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      m[rt][i] = -INFINITY;
-      l[rt][i] = 0.0f;
-    }
+    m[rt] = -INFINITY;
+    l[rt] = 0.0f;
   }
 
   // block-cooperative load of one step: thread t moves 16 bytes of K and of V of key
   // t / 8 (tile (t / 8) / 16), channels 16 (t % 8) ..+16; tiles past the range or on a
   // bad page load through zero-length resources
   const int kk = threadIdx.x >> 3, g8 = threadIdx.x & 7;
-  const int64_t s_first = (kb / 16) * 16;
-  auto tile_ok = [&](int64_t tp) -> bool {  // uniform
+  const int s_first = (kb / 16) * 16;
+  auto tile_ok = [&](int tp) -> bool {  // uniform
     if (tp >= ke) return false;
     const int64_t page = bt[pf_page_of(a, (uint32_t)tp)];
     return page >= 0 && page < a.n_pages;
   };
-  auto load_step = [&](int64_t s0, uint4 &kc, uint4 &vc) {
-    const int64_t tp = s0 + (kk & 16);  // this thread's 16-key tile
-    const int live = (int)max((int64_t)0, min((int64_t)16, ke - tp));
-    const int64_t tc = tp < ke ? tp : (ke > 0 ? ke - 1 : 0);
+  const int tile16 = (wave >> 1) << 4;  // = kk & 16, uniform over the wave
+  auto load_step = [&](int s0, uint4 &kc, uint4 &vc) {
+    const int tp = s0 + tile16;  // this thread's 16-key tile (scalar: the buffer resources stay in SGPRs)
+    const int live = max(0, min(16, ke - tp));
+    const int tc = tp < ke ? tp : (ke > 0 ? ke - 1 : 0);
     const uint32_t bi = pf_page_of(a, (uint32_t)tc);
     const int64_t page = bt[bi];
     const bool ok = live > 0 && page >= 0 && page < a.n_pages;
     e |= (live > 0 && !ok) ? ZX_KERR_PAGE_RANGE : 0;
     const int nrec = ok ? live * D : 0;
-    const uint8_t *src = a.pool + (ok ? page * page_bytes + head_off + (tc - (int64_t)bi * a.page_size) * D : 0);
+    const uint8_t *src =
+        a.pool + (ok ? page * page_bytes + head_off + (int64_t)(tc - (int)bi * a.page_size) * D : 0);
     const __amdgpu_buffer_rsrc_t rk =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src), (short)0, nrec, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv =
@@ -152,13 +159,20 @@ __global__ void __launch_bounds__(PF_THREADS) paged_prefill_mfma_kernel(PrefillA
     kc = make_uint4(x.x, x.y, x.z, x.w);
     vc = make_uint4(y.x, y.y, y.z, y.w);
   };
+  // P^T (the B operand of O^T = V^T . P^T) is built in registers from the S^T tiles, so
+  // the 32 keys of a step sit in MFMA k order: k = 8 kg' + 4 KT + i is key 16 KT + 4 kg' + i.
+  // V^T rows use the same order: key k of the step at slot
+  // 8 ((k % 16) / 4) + 4 (k / 16) + k % 4, its 16-byte chunk (k % 16) / 4 swizzled with c / 32
   auto store_step = [&](int buf, const uint4 &kc, const uint4 &vc) {
-    *reinterpret_cast<uint4 *>(&kst[buf][kk * PF_KROW + 16 * g8]) = kc;
-    // V^T element (channel c, key k) at c * PF_VROW + 16 ((k / 8) ^ (c / 32)) + 2 (k % 8);
+    uint32_t kb8[8];
+    decode16_bf16(kc, kb8);  // K decoded once per block, read as bf16 by the 4 waves
+    uint4 *kd = reinterpret_cast<uint4 *>(&kst[buf][kk * PF_KROW + 32 * g8]);
+    kd[0] = make_uint4(kb8[0], kb8[1], kb8[2], kb8[3]);
+    kd[1] = make_uint4(kb8[4], kb8[5], kb8[6], kb8[7]);
     // this thread's channels c = 16 g8 + 2 p, +1, so c / 32 = g8 / 2
     uint32_t vb[8];
     decode16_bf16(vc, vb);
-    const int base = (((kk >> 3) ^ (g8 >> 1)) << 4) + (kk & 7) * 2;
+    const int base = ((((kk & 15) >> 2) ^ (g8 >> 1)) << 4) + (4 * (kk >> 4) + (kk & 3)) * 2;
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
       uint8_t *row = &vtl[buf][(16 * g8 + 2 * p) * PF_VROW + base];
@@ -167,88 +181,110 @@ __global__ void __launch_bounds__(PF_THREADS) paged_prefill_mfma_kernel(PrefillA
     }
   };
 
-  auto compute_step = [&](int buf, int64_t s0) {
+  auto compute_step = [&](int buf, int s0) {
     const bool ok0 = tile_ok(s0), ok1 = tile_ok(s0 + 16);
-    // scores for both key tiles and both row tiles
+    // S^T tiles: sc[rt][KT] lane (n, kg) holds keys 16 KT + 4 kg + i of row 16 rt + n
     att_f32x4 sc[2][2];
 #pragma unroll
     for (int KT = 0; KT < 2; ++KT) {
-      uint32_t kbv[16];
-      uint32_t (&k0)[8] = *reinterpret_cast<uint32_t (*)[8]>(&kbv[0]);
-      uint32_t (&k1)[8] = *reinterpret_cast<uint32_t (*)[8]>(&kbv[8]);
-      const uint8_t *kr = &kst[buf][(16 * KT + n) * PF_KROW + kg * 32];
-      decode16_bf16(*reinterpret_cast<const uint4 *>(kr), k0);
-      decode16_bf16(*reinterpret_cast<const uint4 *>(kr + 16), k1);
+      att_bf16x8 ka[4];  // A operand: key 16 KT + n, channels 32 kg + 8 c ..+8
+      const uint8_t *kr = &kst[buf][(16 * KT + n) * PF_KROW + kg * 64];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        ka[c] = __builtin_bit_cast(att_bf16x8, *reinterpret_cast<const att_u32x4 *>(kr + 16 * c));
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         att_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              qa[rt][c],
-              __builtin_bit_cast(att_bf16x8, att_u32x4{kbv[4 * c], kbv[4 * c + 1], kbv[4 * c + 2], kbv[4 * c + 3]}),
-              acc, 0, 0, 0);
+        for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[c], qa[rt][c], acc, 0, 0, 0);
         sc[rt][KT] = acc;
       }
     }
-    // C layout: lane holds rows 16 rt + 4 kg + i, key 16 KT + n
+    // wave-uniform: every (row, key) of the step counts, no mask needed (and qs >= 0, so
+    // the row maximum of s * qs is qs times the maximum of s)
+    const bool full = ok0 && ok1 && s0 >= kb && s0 + PF_KEYS <= ke && wrow0 + 32 <= n_qb && qs >= 0.0f &&
+                      (!a.causal || (int64_t)s0 + PF_KEYS - 1 <= qp0 + wrow0);
+    float alpha[2];
+    bool grow_any = false;
+    att_u32x4 ph[2], pl[2];  // P^T hi / lo as bf16 pairs: element 4 KT + i
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float sv[2][4];
+      float mx;
+      if (full) {
 #pragma unroll
-      for (int KT = 0; KT < 2; ++KT) {
-        const int64_t kp = s0 + 16 * KT + n;
-        const bool tok = KT == 0 ? ok0 : ok1;
+        for (int KT = 0; KT < 2; ++KT)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t r = wrow0 + 16 * rt + 4 * kg + i;
-          const bool valid = tok && kp >= kb && kp < ke && r < n_qb && (!a.causal || kp <= qp0 + r);
-          sv[KT][i] = valid ? sc[rt][KT][i] * qs : -INFINITY;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float mx = row16_max(fmaxf(sv[0][i], sv[1][i]));
-        const float mn = fmaxf(m[rt][i], mx);
-        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[rt][i] - mn);
-        m[rt][i] = mn;
-        l[rt][i] *= alpha;
-#pragma unroll
-        for (int jt = 0; jt < 8; ++jt) o[rt][jt][i] *= alpha;
+          for (int i = 0; i < 4; ++i) sv[KT][i] = sc[rt][KT][i];
+        mx = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
+                   fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3]))) * qs;
+      } else {
+        const int r = wrow0 + 16 * rt + n;
+        const int64_t lim = (r < n_qb) ? (a.causal ? qp0 + r : (int64_t)INT32_MAX) : (int64_t)-1;
 #pragma unroll
         for (int KT = 0; KT < 2; ++KT) {
-          const float p = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[KT][i] - mn);
-          l[rt][i] += p;
-          pl[(16 * rt + 4 * kg + i) * PF_KEYS + 16 * KT + n] = p;
+          const bool tok = KT == 0 ? ok0 : ok1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kp = s0 + 16 * KT + 4 * kg + i;
+            const bool valid = tok && kp >= kb && kp < ke && (int64_t)kp <= lim;
+            sv[KT][i] = valid ? sc[rt][KT][i] * qs : -INFINITY;
+          }
         }
+        mx = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
+                   fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
       }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // A operand: P[row 16 rt + n][keys 8 kg ..+8], split into bf16 hi + lo
-    att_bf16x8 ah[2], al[2];
+      mx = xrow_max(mx);
+      const bool grow = mx > m[rt] + PF_LAZY;  // a row with no key yet grows at its first key
+      const float mn = grow ? mx : m[rt];
+      const float ms = mn == -INFINITY ? 0.0f : mn;  // a row with no key yet keeps p = 0
+      alpha[rt] = grow ? __builtin_amdgcn_exp2f(m[rt] - ms) : 1.0f;
+      grow_any |= grow;
+      m[rt] = mn;
+      float pv[2][4];
+      if (full) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const float4 x = *reinterpret_cast<const float4 *>(pl + (16 * rt + n) * PF_KEYS + kg * 8);
-      const float4 y = *reinterpret_cast<const float4 *>(pl + (16 * rt + n) * PF_KEYS + kg * 8 + 4);
-      const float pr[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+        for (int KT = 0; KT < 2; ++KT)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        ah[rt][i] = (__bf16)pr[i];
-        al[rt][i] = (__bf16)(pr[i] - (float)ah[rt][i]);
+          for (int i = 0; i < 4; ++i) pv[KT][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[KT][i], qs, -ms));
+      } else {
+#pragma unroll
+        for (int KT = 0; KT < 2; ++KT)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pv[KT][i] = __builtin_amdgcn_exp2f(sv[KT][i] - ms);
       }
+      float ls = 0.0f;
+#pragma unroll
+      for (int KT = 0; KT < 2; ++KT)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float p0 = pv[KT][2 * j], p1 = pv[KT][2 * j + 1];
+          ls += p0 + p1;
+          const uint32_t h = pack_bf16(p0, p1);
+          ph[rt][2 * KT + j] = h;
+          pl[rt][2 * KT + j] = pack_bf16(p0 - __uint_as_float(h << 16), p1 - __uint_as_float(h & 0xFFFF0000u));
+        }
+      l[rt] = l[rt] * alpha[rt] + ls;
     }
-    // B operand per 16-channel tile: V^T[channel 16 jt + n][keys 8 kg ..+8]
+    // rescale O only when some row's maximum was raised
+    if (__builtin_amdgcn_ballot_w64(grow_any)) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int jt = 0; jt < 8; ++jt) o[rt][jt] *= alpha[rt];
+    }
+    // A operand per 16-channel tile: V^T[channel 16 jt + n][k 8 kg ..+8]
 #pragma unroll
     for (int jt = 0; jt < 8; ++jt) {
       const int ch = 16 * jt + n;
       const att_u32x4 w = *reinterpret_cast<const att_u32x4 *>(&vtl[buf][ch * PF_VROW + ((kg ^ (ch >> 5)) << 4)]);
-      const att_bf16x8 bv = __builtin_bit_cast(att_bf16x8, w);
+      const att_bf16x8 av = __builtin_bit_cast(att_bf16x8, w);
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[rt], bv, o[rt][jt], 0, 0, 0);
-        o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[rt], bv, o[rt][jt], 0, 0, 0);
+        o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, ph[rt]), o[rt][jt], 0,
+                                                            0, 0);
+        o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, pl[rt]), o[rt][jt], 0,
+                                                            0, 0);
       }
     }
   };
@@ -256,7 +292,7 @@ __global__ void __launch_bounds__(PF_THREADS) paged_prefill_mfma_kernel(PrefillA
   // steps: data of step s + 1 loaded into registers while step s computes; one barrier
   // per step (the LDS buffers alternate)
   uint4 kc, vc;
-  int64_t s0 = s_first;
+  int s0 = s_first;
   if (s0 < ke_blk) {
     load_step(s0, kc, vc);
     store_step(0, kc, vc);
@@ -264,7 +300,7 @@ __global__ void __launch_bounds__(PF_THREADS) paged_prefill_mfma_kernel(PrefillA
   __syncthreads();
   int buf = 0;
   while (s0 < ke_blk) {
-    const int64_t s1 = s0 + PF_KEYS;
+    const int s1 = s0 + PF_KEYS;
     const bool more = s1 < ke_blk;  // uniform
     if (more) load_step(s1, kc, vc);
     compute_step(buf, s0);
@@ -274,43 +310,50 @@ __global__ void __launch_bounds__(PF_THREADS) paged_prefill_mfma_kernel(PrefillA
     s0 = s1;
   }
 
-  // rows: l over the 16 lanes of the row group; normalise; merge; store
+  // rows: l over the 4 lane rows; normalise; merge; store channels 16 jt + 4 kg ..+4
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t r = wrow0 + 16 * rt + 4 * kg + i;
-      const float lt = group_sum<16>(l[rt][i]);
-      if (r >= n_qb) continue;
-      const float lse_new = lt > 0.0f ? m[rt][i] + __builtin_amdgcn_logf(lt) : -INFINITY;
-      const float inv = lt > 0.0f ? vscale / lt : 0.0f;  // V's dequant scale applied once, here
-      const int64_t row = (q_lo + r) * a.n_q_heads + hq;
-      float wa = 0.0f, wb = 1.0f, lse = lse_new;
-      if ((a.mode & PF_MERGE) && !(a.mode & PF_INIT)) {
-        const float lse_old = a.lse2[row];
-        const float mm = fmaxf(lse_old, lse_new);
-        if (mm == -INFINITY) {
-          wa = 0.0f;
-          wb = 0.0f;
-          lse = -INFINITY;
-        } else {
-          const float ea = __builtin_amdgcn_exp2f(lse_old - mm), eb = __builtin_amdgcn_exp2f(lse_new - mm);
-          const float den = ea + eb;
-          wa = ea / den;
-          wb = eb / den;
-          lse = mm + __builtin_amdgcn_logf(den);
-        }
+  for (int rt = 0; rt < 2; ++rt) {
+    const int r = wrow0 + 16 * rt + n;
+    const float lt = xrow_sum(l[rt]);
+    if (r >= n_qb) continue;
+    const float lse_new = lt > 0.0f ? m[rt] + __builtin_amdgcn_logf(lt) : -INFINITY;
+    const float inv = lt > 0.0f ? vscale / lt : 0.0f;  // V's dequant scale applied once, here
+    const int64_t row = (q_lo + r) * a.n_q_heads + hq;
+    float wa = 0.0f, wb = 1.0f, lse = lse_new;
+    if ((a.mode & PF_MERGE) && !(a.mode & PF_INIT)) {
+      const float lse_old = a.lse2[row];
+      const float mm = fmaxf(lse_old, lse_new);
+      if (mm == -INFINITY) {
+        wa = 0.0f;
+        wb = 0.0f;
+        lse = -INFINITY;
+      } else {
+        const float ea = __builtin_amdgcn_exp2f(lse_old - mm), eb = __builtin_amdgcn_exp2f(lse_new - mm);
+        const float den = ea + eb;
+        wa = ea / den;
+        wb = eb / den;
+        lse = mm + __builtin_amdgcn_logf(den);
       }
-#pragma unroll
-      for (int jt = 0; jt < 8; ++jt) {
-        const int64_t idx = row * D + 16 * jt + n;
-        float v = o[rt][jt][i] * inv * wb;
-        if (wa != 0.0f) v += wa * a.o_acc[idx];
-        if (a.mode & PF_MERGE) a.o_acc[idx] = v;
-        if (a.mode & PF_WRITE_BF16) a.out[idx] = (uint16_t)(pack_bf16(v, 0.0f) & 0xFFFFu);
-      }
-      if ((a.mode & PF_MERGE) && n == 0) a.lse2[row] = lse;
     }
+#pragma unroll
+    for (int jt = 0; jt < 8; ++jt) {
+      const int64_t idx = row * D + 16 * jt + 4 * kg;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = o[rt][jt][i] * inv * wb;
+      if (wa != 0.0f) {
+        const float4 old = *reinterpret_cast<const float4 *>(a.o_acc + idx);
+        v[0] += wa * old.x;
+        v[1] += wa * old.y;
+        v[2] += wa * old.z;
+        v[3] += wa * old.w;
+      }
+      if (a.mode & PF_MERGE) *reinterpret_cast<float4 *>(a.o_acc + idx) = make_float4(v[0], v[1], v[2], v[3]);
+      if (a.mode & PF_WRITE_BF16)
+        *reinterpret_cast<uint2 *>(a.out + idx) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+    }
+    if ((a.mode & PF_MERGE) && kg == 0) a.lse2[row] = lse;
+  }
   if (e && a.err) atomicOr(a.err, e);
 }
 
