@@ -6,7 +6,9 @@ U[1k, 8k] tokens, 5% of each sequence's (layer, head) pairs x50), one step = one
 of every layer, inputs already resident in HBM.  Reported as algorithmic GB/s
 (3 bytes per KV element + scales + block tables) and as a fraction of the 8 TB/s HBM3E
 peak.  Also measured: configs[2] (paged gather + dequant, 64 x 32k decode, 300k-page
-pool; plus decode attention computed straight from those FP8 pages), configs[3] (Belady tiering of a ring-attention trace: evictions/s, plus the
+pool; plus decode attention computed straight from those FP8 pages), ring attention over FP8
+pages (4 x 8k causal, ring degree 1 and 8: TFLOP/s against the bf16 matrix-core peak), configs[3]
+(Belady tiering of a ring-attention trace: evictions/s, plus the
 pinned-host tier moves of one layer overlapped with compute; and the same schedule over three
 tiers, HBM / pinned DRAM / a file, planned on the GPU and replayed for three windows) and configs[4] (80-layer
 70B-shape share streamed through 60 HBM layer slots and pinned DRAM: per-kernel append
@@ -16,7 +18,7 @@ The CPU baseline is the C oracle (oracle/zx_oracle.c, one thread) timed on a bou
 sample of the same workload on this machine's host cores.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-                    [--only append|gather|belady|tiers|weights|configs4|copy|all]
+                    [--only append|gather|ring|belady|tiers|weights|configs4|copy|all]
 """
 from __future__ import annotations
 
@@ -40,7 +42,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
-    ap.add_argument("--only", choices=["append", "gather", "belady", "tiers", "weights", "configs4", "copy", "all"],
+    ap.add_argument("--only", choices=["append", "gather", "ring", "belady", "tiers", "weights", "configs4", "copy",
+                                       "all"],
                     default="all")
     ap.add_argument("--seed", type=int, default=1)
     return ap.parse_args()
@@ -433,6 +436,69 @@ def tiers_leg(torch, dev):
 C5 = dict(L=80, H=8, D=128, P=16, B=4, Tb=131072, hbm_layers=60)
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 on MI355X
+
+
+def ring_attention_leg(torch, dev, steps, warmup, skip_cpu):
+    """Ring attention straight from the FP8 pages (QuantizedRingAttention's compute,
+    README.md:344): 4 sequences x 8,192 tokens, causal, 32 query heads over 8 KV heads,
+    D = 128, page 16, pages at random in the pool; ring degree 1 (one step over all keys)
+    and 8 (eight key shards merged through the running log-sum-exp, as the ring's steps
+    would run on one GPU)."""
+    import numpy as np
+    from oracle import oracle as O
+    from zenyx_amd import kv
+
+    B, T, Hq, H, D, P = 4, 8192, 32, 8, 128, 16
+    n_pages = B * T // P
+    g = torch.Generator().manual_seed(7)
+    codes = torch.randint(0, 256, (n_pages, 2, H, P, D), dtype=torch.uint8, generator=g)
+    codes[(codes & 0x7F) == 0x7F] = 0x3A  # no NaN codes, as the quantizer writes none
+    pool = codes.to(dev)
+    bt_h = torch.randperm(n_pages, generator=g).to(torch.int32).view(B, T // P)
+    bt = bt_h.to(dev)
+    sc_h = torch.rand((2, H), generator=g) * 0.01 + 0.001
+    sc = sc_h.to(dev)
+    q_h = torch.randn((B * T, Hq, D), generator=g).to(torch.bfloat16)
+    q = q_h.to(dev)
+    cu = torch.arange(0, B * T + 1, T, dtype=torch.int32, device=dev)
+    qp = torch.zeros(B, dtype=torch.int32, device=dev)
+    kl = torch.full((B,), T, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    flops = 4.0 * B * Hq * D * (T * (T + 1) / 2)  # QK^T and PV over the causal (row, key) pairs
+    res = {"workload": "ring attention from FP8 pages: 4 seqs x 8192 tokens causal, 32 query heads over 8 KV "
+                       "heads, D=128, page 16 (Llama-3-8B attention shape); kernel paged_prefill_mfma",
+           "useful_flop_per_step": flops,
+           "note": "P.V runs twice on the matrix cores (P split into bf16 hi + lo), so the matrix cores execute "
+                   "1.5x the useful flops"}
+    for ring in (1, 8):
+        fn = lambda: kv.ring_attention_fp8(q, cu, qp, pool, sc, bt, kl, ring_degree=ring, causal=True)  # noqa: E731
+        ms, _, _ = time_steps(torch, fn, steps, warmup)
+        tf = flops / (ms * 1e-3) / 1e12
+        log(f"ring attention degree {ring}: {ms:.3f} ms/step, {tf:.1f} TFLOP/s "
+            f"({100 * tf / MFMA_BF16_PEAK_TFLOPS:.1f}% of the bf16 MFMA peak)")
+        res[f"ring{ring}"] = {"ms_per_step": round(ms, 4), "TFLOPs": round(tf, 1),
+                              "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+    if not skip_cpu:
+        # the C oracle (double precision, one thread) on the last 16 query rows of sequence 0
+        # (about 20 s on one host core)
+        rows = 16
+        qs = q_h[T - rows:T].contiguous().view(torch.int16).numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        O.paged_attention_prefill(qs, np.array([0, rows], np.int32), np.array([T - rows], np.int32),
+                                  codes.numpy(), sc_h.numpy(), bt_h[:1].numpy(), np.zeros(1, np.int32),
+                                  np.full(1, T, np.int32), True, float(np.float32(1.0 / np.sqrt(D))))
+        dt = time.perf_counter() - t0
+        f_s = 4.0 * Hq * D * sum(T - rows + r + 1 for r in range(rows))
+        res["cpu_baseline"] = {"value": round(f_s / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                               "sample": f"oracle zxo_paged_attention_prefill, last {rows} query rows of one "
+                                         f"sequence (keys 0..8191, 32 heads): {dt:.2f} s"}
+        log(f"CPU oracle: {res['cpu_baseline']['value']:.6f} TFLOP/s ({dt:.2f} s)")
+    del pool, q, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def make_c5_layer(torch, dev, layer, out, seed=5, chunk=65536):
     """configs[4] KV of one layer, [B*Tb, 2, H, D] bf16 written into ``out``: Student-t
     (nu = 3) draws times a per-(kv, head, channel) scale 10**U(-2, 2), generated on the
@@ -662,6 +728,18 @@ def main():
                         "config": {"workload": gather["workload"]}})
         del G, k, v
         torch.cuda.empty_cache()
+
+    if args.only in ("ring", "all"):
+        out["ring_attention"] = ring_attention_leg(torch, dev, args.steps, args.warmup, args.skip_cpu)
+        if "value" not in out:
+            r = out["ring_attention"]
+            out.update({"value": r["ring1"]["TFLOPs"], "unit": "TFLOP/s", "ms_per_step": r["ring1"]["ms_per_step"],
+                        "dtype": "bf16", "config": {"workload": r["workload"]},
+                        "roofline": {"bound": "mfma", "achieved": r["ring1"]["TFLOPs"],
+                                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": r["ring1"]["frac"],
+                                     "traffic": None, "kernel": "paged_prefill_mfma_kernel<4>"}})
+            if "cpu_baseline" in r:
+                out["cpu_baseline"] = r["cpu_baseline"]
 
     if args.only in ("belady", "all"):
         out["belady"] = belady_leg(torch, dev, args.skip_cpu)

@@ -5,19 +5,20 @@
 //
 // A block owns (sequence, G query heads of one kv head, a tile of 32 * 4 / G query rows);
 // its 4 waves each take one head and 32 rows (two 16-row MFMA tiles), so every K/V tile
-// is read from HBM once per block and serves 128 query rows.  Steps of 32 keys (two
+// is read from HBM once per block and serves 128 query rows.  Steps of 64 keys (four
 // 16-key tiles, each inside one page):
 //   * the block loads the step's K and V runs with contiguous 16-byte lane loads (whole
-//     cache lines), one step ahead of the compute; K codes go to LDS staging rows as
-//     they are, V values go transposed into LDS (V^T[channel][key], bf16), both double
+//     cache lines; a thread takes channels 16 g ..+16 of two adjacent keys), one step
+//     ahead of the compute; K goes to LDS decoded to bf16 rows, V goes transposed
+//     (V^T[channel][key], bf16, the two keys of a thread as one 32-bit word), both double
 //     buffered so one block barrier per step suffices;
 //   * each wave computes the transposed problem, so that one query row sits in one lane
-//     column of every MFMA tile: S^T = K . Q^T on v_mfma_f32_16x16x32_bf16 (K codes
-//     converted to bf16 exactly as A, Q rows as B), key range / causal mask only on the
-//     steps that cross a boundary, online softmax in the exp2 domain with row maxima
-//     over the 4 lane rows by v_permlane32/16_swap, P^T kept in registers as the B
-//     operand split into bf16 hi + lo, O^T += V^T . P^T on the same MFMA (the rescale
-//     of O skipped when no row maximum moved).
+//     column of every MFMA tile: S^T = K . Q^T on v_mfma_f32_16x16x32_bf16 (K rows as A,
+//     Q rows as B), key range / causal mask only on the steps that cross a boundary,
+//     online softmax in the exp2 domain with row maxima over the 4 lane rows by
+//     v_permlane32/16_swap, P^T kept in registers as the B operand split into bf16
+//     hi + lo, O^T += V^T . P^T on the same MFMA (the rescale of O skipped unless a row
+//     maximum was raised).
 // At the end each row is normalised; with MERGE the step's (O, lse2) is combined with
 // the running one in o_acc / lse2 (each (row, head) belongs to one block, so no races);
 // with the bf16 flag the merged row is also written as bf16.
@@ -26,9 +27,9 @@
 namespace zx {
 
 constexpr int PF_THREADS = 256;
-constexpr int PF_KEYS = 32;                  // keys per step
+constexpr int PF_KEYS = 64;                  // keys per step
 constexpr int PF_KROW = 272;                 // K row in LDS (128 channels bf16 + 16 pad: conflict-free reads)
-constexpr int PF_VROW = 80;                  // V^T row (32 keys bf16 + 16 pad)
+constexpr int PF_VROW = 144;                 // V^T row (64 keys bf16 + 16 pad)
 constexpr int PF_KBYTES = PF_KEYS * PF_KROW;
 constexpr int PF_VBYTES = 128 * PF_VROW;
 constexpr int PF_MERGE = 1, PF_WRITE_BF16 = 2, PF_INIT = 4;
@@ -55,6 +56,15 @@ struct PrefillArgs {
 
 __device__ __forceinline__ uint32_t pf_page_of(const PrefillArgs &a, uint32_t t) {
   return (uint32_t)(((uint64_t)t * a.p_magic) >> (31 + a.p_shift));
+}
+
+// MFMA k order of a step's keys: the 64 keys form two k-blocks of 32 (one PV MFMA each);
+// inside k-block kb, k = 8 kg + 4 KT + i is key 32 kb + 16 KT + 4 kg + i, which is where
+// the S^T tiles leave that key (tile 2 kb + KT, lane row kg, element i).  V^T rows hold
+// the keys in this order, in 16-byte chunks (8 keys) swizzled by channel / 16.
+__device__ __forceinline__ int pf_vslot_byte(int c, int key) {
+  const int kb = key >> 5, KT = (key >> 4) & 1, kg = (key >> 2) & 3, i = key & 3;
+  return c * PF_VROW + ((((kb << 2) + kg) ^ (c >> 4)) << 4) + 2 * (4 * KT + i);
 }
 
 template <int G>
@@ -91,9 +101,23 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   // keys past the block's last query position never count when causal
   const int last_row = min(row0_blk + QT, n_qb) - 1;
   const int ke_blk = a.causal ? (int)max((int64_t)-1, min((int64_t)ke, qp0 + last_row + 1)) : ke;
+  const int s_first = (kb / 16) * 16;
 
   __shared__ __attribute__((aligned(16))) uint8_t kst[2][PF_KBYTES];
   __shared__ __attribute__((aligned(16))) uint8_t vtl[2][PF_VBYTES];
+
+  // every page the block may load inside the pool? (then the steps skip the per-tile
+  // block-table checks; otherwise tiles on bad pages count as masked)
+  bool all_ok = true;
+  if (s_first < ke) {
+    const int p_lo = (int)pf_page_of(a, (uint32_t)s_first), p_hi = (int)pf_page_of(a, (uint32_t)(ke - 1));
+    bool bad = false;
+    for (int pi = p_lo + (int)threadIdx.x; pi <= p_hi; pi += PF_THREADS) {
+      const int64_t pg = bt[pi];
+      bad |= pg < 0 || pg >= a.n_pages;
+    }
+    all_ok = !__syncthreads_or(bad);
+  }
 
   // Q rows as the B operand of S^T = K . Q^T: lane (n, kg) of row tile rt holds row
   // wrow0 + 16 rt + n, channels 32 kg + 8 c ..+8 for MFMA c (the K operand's channel order)
@@ -127,19 +151,19 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     l[rt] = 0.0f;
   }
 
-  // block-cooperative load of one step: thread t moves 16 bytes of K and of V of key
-  // t / 8 (tile (t / 8) / 16), channels 16 (t % 8) ..+16; tiles past the range or on a
-  // bad page load through zero-length resources
-  const int kk = threadIdx.x >> 3, g8 = threadIdx.x & 7;
-  const int s_first = (kb / 16) * 16;
+  // block-cooperative load of one step: thread t moves 16 bytes of K and of V of keys
+  // 2 (t / 8) and 2 (t / 8) + 1 (so wave w loads 16-key tile w), channels 16 (t % 8) ..+16;
+  // tiles past the range or on a bad page load through zero-length resources
+  const int kp2 = threadIdx.x >> 3, g8 = threadIdx.x & 7;
+  const int kk0 = 2 * kp2;
   auto tile_ok = [&](int tp) -> bool {  // uniform
     if (tp >= ke) return false;
+    if (all_ok) return true;
     const int64_t page = bt[pf_page_of(a, (uint32_t)tp)];
     return page >= 0 && page < a.n_pages;
   };
-  const int tile16 = (wave >> 1) << 4;  // = kk & 16, uniform over the wave
-  auto load_step = [&](int s0, uint4 &kc, uint4 &vc) {
-    const int tp = s0 + tile16;  // this thread's 16-key tile (scalar: the buffer resources stay in SGPRs)
+  auto load_step = [&](int s0, att_u32x4 (&kc)[2], att_u32x4 (&vc)[2]) {
+    const int tp = s0 + 16 * wave;  // this wave's 16-key tile (scalar: the buffer resources stay in SGPRs)
     const int live = max(0, min(16, ke - tp));
     const int tc = tp < ke ? tp : (ke > 0 ? ke - 1 : 0);
     const uint32_t bi = pf_page_of(a, (uint32_t)tc);
@@ -153,40 +177,42 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src), (short)0, nrec, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src + (ok ? v_off : 0)), (short)0, nrec, 0x00020000);
-    const int off = (kk & 15) * D + 16 * g8;
-    const att_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 2);
-    const att_u32x4 y = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 2);
-    kc = make_uint4(x.x, x.y, x.z, x.w);
-    vc = make_uint4(y.x, y.y, y.z, y.w);
+    const int off = (kk0 & 15) * D + 16 * g8;
+    kc[0] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 2);
+    kc[1] = __builtin_amdgcn_raw_buffer_load_b128(rk, off + D, 0, 2);
+    vc[0] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 2);
+    vc[1] = __builtin_amdgcn_raw_buffer_load_b128(rv, off + D, 0, 2);
   };
-  // P^T (the B operand of O^T = V^T . P^T) is built in registers from the S^T tiles, so
-  // the 32 keys of a step sit in MFMA k order: k = 8 kg' + 4 KT + i is key 16 KT + 4 kg' + i.
-  // V^T rows use the same order: key k of the step at slot
-  // 8 ((k % 16) / 4) + 4 (k / 16) + k % 4, its 16-byte chunk (k % 16) / 4 swizzled with c / 32
-  auto store_step = [&](int buf, const uint4 &kc, const uint4 &vc) {
-    uint32_t kb8[8];
-    decode16_bf16(kc, kb8);  // K decoded once per block, read as bf16 by the 4 waves
-    uint4 *kd = reinterpret_cast<uint4 *>(&kst[buf][kk * PF_KROW + 32 * g8]);
-    kd[0] = make_uint4(kb8[0], kb8[1], kb8[2], kb8[3]);
-    kd[1] = make_uint4(kb8[4], kb8[5], kb8[6], kb8[7]);
-    // this thread's channels c = 16 g8 + 2 p, +1, so c / 32 = g8 / 2
-    uint32_t vb[8];
-    decode16_bf16(vc, vb);
-    const int base = ((((kk & 15) >> 2) ^ (g8 >> 1)) << 4) + (4 * (kk >> 4) + (kk & 3)) * 2;
+  auto store_step = [&](int buf, const att_u32x4 (&kc)[2], const att_u32x4 (&vc)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {  // K decoded once per block, read as bf16 by the 4 waves
+      uint32_t kb8[8];
+      decode16_bf16(make_uint4(kc[j].x, kc[j].y, kc[j].z, kc[j].w), kb8);
+      uint4 *kd = reinterpret_cast<uint4 *>(&kst[buf][(kk0 + j) * PF_KROW + 32 * g8]);
+      kd[0] = make_uint4(kb8[0], kb8[1], kb8[2], kb8[3]);
+      kd[1] = make_uint4(kb8[4], kb8[5], kb8[6], kb8[7]);
+    }
+    // V^T: channel c = 16 g8 + 2 p (+1) gets keys kk0, kk0 + 1 (adjacent k slots) as one word
+    uint32_t v0[8], v1[8];
+    decode16_bf16(make_uint4(vc[0].x, vc[0].y, vc[0].z, vc[0].w), v0);
+    decode16_bf16(make_uint4(vc[1].x, vc[1].y, vc[1].z, vc[1].w), v1);
+    const int slot0 = pf_vslot_byte(16 * g8, kk0);  // channel 16 g8; the others add c * PF_VROW
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
-      uint8_t *row = &vtl[buf][(16 * g8 + 2 * p) * PF_VROW + base];
-      *reinterpret_cast<uint16_t *>(row) = (uint16_t)(vb[p] & 0xFFFFu);
-      *reinterpret_cast<uint16_t *>(row + PF_VROW) = (uint16_t)(vb[p] >> 16);
+      uint8_t *row = &vtl[buf][slot0 + 2 * p * PF_VROW];
+      *reinterpret_cast<uint32_t *>(row) = __builtin_amdgcn_perm(v1[p], v0[p], 0x05040100u);
+      *reinterpret_cast<uint32_t *>(row + PF_VROW) = __builtin_amdgcn_perm(v1[p], v0[p], 0x07060302u);
     }
   };
 
   auto compute_step = [&](int buf, int s0) {
-    const bool ok0 = tile_ok(s0), ok1 = tile_ok(s0 + 16);
-    // S^T tiles: sc[rt][KT] lane (n, kg) holds keys 16 KT + 4 kg + i of row 16 rt + n
-    att_f32x4 sc[2][2];
+    bool tok[4];
 #pragma unroll
-    for (int KT = 0; KT < 2; ++KT) {
+    for (int KT = 0; KT < 4; ++KT) tok[KT] = tile_ok(s0 + 16 * KT);
+    // S^T tiles: sc[rt][KT] lane (n, kg) holds keys 16 KT + 4 kg + i of row 16 rt + n
+    att_f32x4 sc[2][4];
+#pragma unroll
+    for (int KT = 0; KT < 4; ++KT) {
       att_bf16x8 ka[4];  // A operand: key 16 KT + n, channels 32 kg + 8 c ..+8
       const uint8_t *kr = &kst[buf][(16 * KT + n) * PF_KROW + kg * 64];
 #pragma unroll
@@ -202,37 +228,37 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     }
     // wave-uniform: every (row, key) of the step counts, no mask needed (and qs >= 0, so
     // the row maximum of s * qs is qs times the maximum of s)
-    const bool full = ok0 && ok1 && s0 >= kb && s0 + PF_KEYS <= ke && wrow0 + 32 <= n_qb && qs >= 0.0f &&
+    const bool full = tok[0] && tok[1] && tok[2] && tok[3] && s0 >= kb && s0 + PF_KEYS <= ke &&
+                      wrow0 + 32 <= n_qb && qs >= 0.0f &&
                       (!a.causal || (int64_t)s0 + PF_KEYS - 1 <= qp0 + wrow0);
     float alpha[2];
     bool grow_any = false;
-    att_u32x4 ph[2], pl[2];  // P^T hi / lo as bf16 pairs: element 4 KT + i
+    att_u32x4 ph[2][2], pl[2][2];  // [rt][k-block] P^T hi / lo as bf16 pairs: word 2 KT + i / 2
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      float sv[2][4];
-      float mx;
+      float sv[4][4];
+      float mx = -INFINITY;
       if (full) {
 #pragma unroll
-        for (int KT = 0; KT < 2; ++KT)
+        for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sv[KT][i] = sc[rt][KT][i];
-        mx = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
-                   fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3]))) * qs;
+          for (int i = 0; i < 4; ++i) {
+            sv[KT][i] = sc[rt][KT][i];
+            mx = fmaxf(mx, sv[KT][i]);
+          }
+        mx *= qs;
       } else {
         const int r = wrow0 + 16 * rt + n;
         const int64_t lim = (r < n_qb) ? (a.causal ? qp0 + r : (int64_t)INT32_MAX) : (int64_t)-1;
 #pragma unroll
-        for (int KT = 0; KT < 2; ++KT) {
-          const bool tok = KT == 0 ? ok0 : ok1;
+        for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int kp = s0 + 16 * KT + 4 * kg + i;
-            const bool valid = tok && kp >= kb && kp < ke && (int64_t)kp <= lim;
+            const bool valid = tok[KT] && kp >= kb && kp < ke && (int64_t)kp <= lim;
             sv[KT][i] = valid ? sc[rt][KT][i] * qs : -INFINITY;
+            mx = fmaxf(mx, sv[KT][i]);
           }
-        }
-        mx = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
-                   fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
       }
       mx = xrow_max(mx);
       const bool grow = mx > m[rt] + PF_LAZY;  // a row with no key yet grows at its first key
@@ -241,28 +267,23 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
       alpha[rt] = grow ? __builtin_amdgcn_exp2f(m[rt] - ms) : 1.0f;
       grow_any |= grow;
       m[rt] = mn;
-      float pv[2][4];
-      if (full) {
+      float pv[4][4];
 #pragma unroll
-        for (int KT = 0; KT < 2; ++KT)
+      for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) pv[KT][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[KT][i], qs, -ms));
-      } else {
-#pragma unroll
-        for (int KT = 0; KT < 2; ++KT)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) pv[KT][i] = __builtin_amdgcn_exp2f(sv[KT][i] - ms);
-      }
+        for (int i = 0; i < 4; ++i)
+          pv[KT][i] = __builtin_amdgcn_exp2f(full ? __builtin_fmaf(sv[KT][i], qs, -ms) : sv[KT][i] - ms);
       float ls = 0.0f;
 #pragma unroll
-      for (int KT = 0; KT < 2; ++KT)
+      for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const float p0 = pv[KT][2 * j], p1 = pv[KT][2 * j + 1];
           ls += p0 + p1;
-          const uint32_t h = pack_bf16(p0, p1);
-          ph[rt][2 * KT + j] = h;
-          pl[rt][2 * KT + j] = pack_bf16(p0 - __uint_as_float(h << 16), p1 - __uint_as_float(h & 0xFFFF0000u));
+          const uint32_t hw = pack_bf16(p0, p1);
+          ph[rt][KT >> 1][2 * (KT & 1) + j] = hw;
+          pl[rt][KT >> 1][2 * (KT & 1) + j] =
+              pack_bf16(p0 - __uint_as_float(hw << 16), p1 - __uint_as_float(hw & 0xFFFF0000u));
         }
       l[rt] = l[rt] * alpha[rt] + ls;
     }
@@ -273,25 +294,29 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 #pragma unroll
         for (int jt = 0; jt < 8; ++jt) o[rt][jt] *= alpha[rt];
     }
-    // A operand per 16-channel tile: V^T[channel 16 jt + n][k 8 kg ..+8]
+    // A operand per 16-channel tile and k-block: V^T[channel 16 jt + n][k 8 kg ..+8]
 #pragma unroll
     for (int jt = 0; jt < 8; ++jt) {
       const int ch = 16 * jt + n;
-      const att_u32x4 w = *reinterpret_cast<const att_u32x4 *>(&vtl[buf][ch * PF_VROW + ((kg ^ (ch >> 5)) << 4)]);
-      const att_bf16x8 av = __builtin_bit_cast(att_bf16x8, w);
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, ph[rt]), o[rt][jt], 0,
-                                                            0, 0);
-        o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, pl[rt]), o[rt][jt], 0,
-                                                            0, 0);
+      for (int kbk = 0; kbk < 2; ++kbk) {
+        const att_u32x4 w =
+            *reinterpret_cast<const att_u32x4 *>(&vtl[buf][ch * PF_VROW + ((((kbk << 2) + kg) ^ jt) << 4)]);
+        const att_bf16x8 av = __builtin_bit_cast(att_bf16x8, w);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, ph[rt][kbk]),
+                                                              o[rt][jt], 0, 0, 0);
+          o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, pl[rt][kbk]),
+                                                              o[rt][jt], 0, 0, 0);
+        }
       }
     }
   };
 
   // steps: data of step s + 1 loaded into registers while step s computes; one barrier
   // per step (the LDS buffers alternate)
-  uint4 kc, vc;
+  att_u32x4 kc[2], vc[2];
   int s0 = s_first;
   if (s0 < ke_blk) {
     load_step(s0, kc, vc);
