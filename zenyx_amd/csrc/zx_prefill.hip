@@ -102,6 +102,12 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   const int last_row = min(row0_blk + QT, n_qb) - 1;
   const int ke_blk = a.causal ? (int)max((int64_t)-1, min((int64_t)ke, qp0 + last_row + 1)) : ke;
   const int s_first = (kb / 16) * 16;
+  if (ke_blk <= s_first && !(a.mode & (PF_INIT | PF_WRITE_BF16))) {
+    // no key of this step reaches the block's rows: merging would leave o_acc and lse2 as
+    // they are (block-uniform exit)
+    if (e && a.err && threadIdx.x == 0) atomicOr(a.err, e);
+    return;
+  }
 
   __shared__ __attribute__((aligned(16))) uint8_t kst[2][PF_KBYTES];
   __shared__ __attribute__((aligned(16))) uint8_t vtl[2][PF_VBYTES];
@@ -205,7 +211,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     }
   };
 
-  auto compute_step = [&](int buf, int s0) {
+  // one step: S^T, softmax, then the next step's K/V stored into the other LDS buffer
+  // (free since the last barrier) ahead of the PV products so the two can overlap
+  auto compute_step = [&](int buf, int s0, const att_u32x4 (&kc)[2], const att_u32x4 (&vc)[2]) {
     bool tok[4];
 #pragma unroll
     for (int KT = 0; KT < 4; ++KT) tok[KT] = tile_ok(s0 + 16 * KT);
@@ -236,29 +244,26 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     att_u32x4 ph[2][2], pl[2][2];  // [rt][k-block] P^T hi / lo as bf16 pairs: word 2 KT + i / 2
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      float sv[4][4];
+      const int r = wrow0 + 16 * rt + n;
+      // last key position the row may see (keys are < 2^31)
+      const int lim = (r < n_qb) ? (a.causal ? (int)min(max(qp0 + r, (int64_t)-1), (int64_t)INT32_MAX) : INT32_MAX)
+                                 : -1;
+      auto valid = [&](int KT, int i) {  // branch-free
+        const int kp = s0 + 16 * KT + 4 * kg + i;
+        return tok[KT] & (kp >= kb) & (kp < ke) & (kp <= lim);
+      };
       float mx = -INFINITY;
       if (full) {
 #pragma unroll
         for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            sv[KT][i] = sc[rt][KT][i];
-            mx = fmaxf(mx, sv[KT][i]);
-          }
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[rt][KT][i]);
         mx *= qs;
       } else {
-        const int r = wrow0 + 16 * rt + n;
-        const int64_t lim = (r < n_qb) ? (a.causal ? qp0 + r : (int64_t)INT32_MAX) : (int64_t)-1;
 #pragma unroll
         for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kp = s0 + 16 * KT + 4 * kg + i;
-            const bool valid = tok[KT] && kp >= kb && kp < ke && (int64_t)kp <= lim;
-            sv[KT][i] = valid ? sc[rt][KT][i] * qs : -INFINITY;
-            mx = fmaxf(mx, sv[KT][i]);
-          }
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, valid(KT, i) ? sc[rt][KT][i] * qs : -INFINITY);
       }
       mx = xrow_max(mx);
       const bool grow = mx > m[rt] + PF_LAZY;  // a row with no key yet grows at its first key
@@ -267,18 +272,26 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
       alpha[rt] = grow ? __builtin_amdgcn_exp2f(m[rt] - ms) : 1.0f;
       grow_any |= grow;
       m[rt] = mn;
-      float pv[4][4];
+      // exponent s qs - m, -inf for the masked (row, key) pairs (qs >= 0 keeps the
+      // unmasked exponents <= PF_LAZY; with qs < 0 every step takes the masked branch,
+      // where the maximum was taken over s qs itself)
+      float xe[4][4];
 #pragma unroll
       for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pv[KT][i] = __builtin_amdgcn_exp2f(full ? __builtin_fmaf(sv[KT][i], qs, -ms) : sv[KT][i] - ms);
+        for (int i = 0; i < 4; ++i) xe[KT][i] = __builtin_fmaf(sc[rt][KT][i], qs, -ms);
+      if (!full) {
+#pragma unroll
+        for (int KT = 0; KT < 4; ++KT)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xe[KT][i] = valid(KT, i) ? xe[KT][i] : -INFINITY;
+      }
       float ls = 0.0f;
 #pragma unroll
       for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const float p0 = pv[KT][2 * j], p1 = pv[KT][2 * j + 1];
+          const float p0 = __builtin_amdgcn_exp2f(xe[KT][2 * j]), p1 = __builtin_amdgcn_exp2f(xe[KT][2 * j + 1]);
           ls += p0 + p1;
           const uint32_t hw = pack_bf16(p0, p1);
           ph[rt][KT >> 1][2 * (KT & 1) + j] = hw;
@@ -294,6 +307,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 #pragma unroll
         for (int jt = 0; jt < 8; ++jt) o[rt][jt] *= alpha[rt];
     }
+    store_step(buf ^ 1, kc, vc);
     // A operand per 16-channel tile and k-block: V^T[channel 16 jt + n][k 8 kg ..+8]
 #pragma unroll
     for (int jt = 0; jt < 8; ++jt) {
@@ -315,7 +329,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   };
 
   // steps: data of step s + 1 loaded into registers while step s computes; one barrier
-  // per step (the LDS buffers alternate)
+  // per step (the LDS buffers alternate).  The last step also loads and stores the step
+  // after it (zero-length loads past kv_end; that buffer is never read).
   att_u32x4 kc[2], vc[2];
   int s0 = s_first;
   if (s0 < ke_blk) {
@@ -326,10 +341,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   int buf = 0;
   while (s0 < ke_blk) {
     const int s1 = s0 + PF_KEYS;
-    const bool more = s1 < ke_blk;  // uniform
-    if (more) load_step(s1, kc, vc);
-    compute_step(buf, s0);
-    if (more) store_step(buf ^ 1, kc, vc);
+    load_step(s1, kc, vc);
+    compute_step(buf, s0, kc, vc);
     __syncthreads();
     buf ^= 1;
     s0 = s1;
