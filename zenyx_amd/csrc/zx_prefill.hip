@@ -17,8 +17,8 @@
 //     Q rows as B), key range / causal mask only on the steps that cross a boundary,
 //     online softmax in the exp2 domain with row maxima over the 4 lane rows by
 //     v_permlane32/16_swap, P^T kept in registers as the B operand split into bf16
-//     hi + lo, O^T += V^T . P^T on the same MFMA (the rescale of O skipped unless a row
-//     maximum was raised).
+//     hi + lo, O^T += V^T . P^T on the same MFMA, and the row sums of P as a ninth tile
+//     against ones (the rescale of O skipped unless a row maximum was raised).
 // At the end each row is normalised; with MERGE the step's (O, lse2) is combined with
 // the running one in o_acc / lse2 (each (row, head) belongs to one block, so no races);
 // with the bf16 flag the merged row is also written as bf16.
@@ -145,17 +145,19 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   const float qs = a.scales[h] * a.sm_log2e;  // K's dequant scale folds into the scores
   const float vscale = a.scales[a.n_kv_heads + h];
 
-  // O^T tiles: o[rt][jt] holds channels 16 jt + 4 kg ..+4 of row 16 rt + n; m and l per
-  // row (l: this lane's share of the row's keys, summed over the 4 lane rows at the end)
-  att_f32x4 o[2][8];
-  float m[2], l[2];
+  // O^T tiles: o[rt][jt] holds channels 16 jt + 4 kg ..+4 of row 16 rt + n; m per row.
+  // The softmax denominator l is a ninth tile on the matrix cores: V^T rows of ones, so
+  // every element of ol[rt] is the row's sum of the same bf16 hi + lo P that O uses.
+  att_f32x4 o[2][8], ol[2];
+  float m[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
     for (int jt = 0; jt < 8; ++jt) o[rt][jt] = att_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    ol[rt] = att_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     m[rt] = -INFINITY;
-    l[rt] = 0.0f;
   }
+  const att_bf16x8 ones = __builtin_bit_cast(att_bf16x8, att_u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
   // block-cooperative load of one step: thread t moves 16 bytes of K and of V of keys
   // 2 (t / 8) and 2 (t / 8) + 1 (so wave w loads 16-key tile w), channels 16 (t % 8) ..+16;
@@ -286,26 +288,25 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 #pragma unroll
           for (int i = 0; i < 4; ++i) xe[KT][i] = valid(KT, i) ? xe[KT][i] : -INFINITY;
       }
-      float ls = 0.0f;
 #pragma unroll
       for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const float p0 = __builtin_amdgcn_exp2f(xe[KT][2 * j]), p1 = __builtin_amdgcn_exp2f(xe[KT][2 * j + 1]);
-          ls += p0 + p1;
           const uint32_t hw = pack_bf16(p0, p1);
           ph[rt][KT >> 1][2 * (KT & 1) + j] = hw;
           pl[rt][KT >> 1][2 * (KT & 1) + j] =
               pack_bf16(p0 - __uint_as_float(hw << 16), p1 - __uint_as_float(hw & 0xFFFF0000u));
         }
-      l[rt] = l[rt] * alpha[rt] + ls;
     }
     // rescale O only when some row's maximum was raised
     if (__builtin_amdgcn_ballot_w64(grow_any)) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
         for (int jt = 0; jt < 8; ++jt) o[rt][jt] *= alpha[rt];
+        ol[rt] *= alpha[rt];
+      }
     }
     store_step(buf ^ 1, kc, vc);
     // A operand per 16-channel tile and k-block: V^T[channel 16 jt + n][k 8 kg ..+8]
@@ -326,6 +327,15 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
         }
       }
     }
+#pragma unroll
+    for (int kbk = 0; kbk < 2; ++kbk)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        ol[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(att_bf16x8, ph[rt][kbk]), ol[rt], 0,
+                                                         0, 0);
+        ol[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(att_bf16x8, pl[rt][kbk]), ol[rt], 0,
+                                                         0, 0);
+      }
   };
 
   // steps: data of step s + 1 loaded into registers while step s computes; one barrier
@@ -348,11 +358,11 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     s0 = s1;
   }
 
-  // rows: l over the 4 lane rows; normalise; merge; store channels 16 jt + 4 kg ..+4
+  // rows: normalise; merge; store channels 16 jt + 4 kg ..+4
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int r = wrow0 + 16 * rt + n;
-    const float lt = xrow_sum(l[rt]);
+    const float lt = ol[rt][0];
     if (r >= n_qb) continue;
     const float lse_new = lt > 0.0f ? m[rt] + __builtin_amdgcn_logf(lt) : -INFINITY;
     const float inv = lt > 0.0f ? vscale / lt : 0.0f;  // V's dequant scale applied once, here
