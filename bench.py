@@ -12,13 +12,14 @@ pages (4 x 8k causal, ring degree 1 and 8: TFLOP/s against the bf16 matrix-core 
 pinned-host tier moves of one layer overlapped with compute; and the same schedule over three
 tiers, HBM / pinned DRAM / a file, planned on the GPU and replayed for three windows) and configs[4] (80-layer
 70B-shape share streamed through 60 HBM layer slots and pinned DRAM: per-kernel append
-and gather GB/s, D2H / H2D GB/s).
+and gather GB/s, D2H / H2D GB/s), and configs[0] (the reference's CPU-runnable cache:
+quant + dequant on the GPU and in torch on the host cores).
 
 The CPU baseline is the C oracle (oracle/zx_oracle.c, one thread) timed on a bounded
 sample of the same workload on this machine's host cores.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-                    [--only append|gather|ring|belady|tiers|weights|configs4|copy|all]
+                    [--only append|gather|ring|belady|tiers|weights|configs4|configs0|copy|all]
 """
 from __future__ import annotations
 
@@ -42,8 +43,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
-    ap.add_argument("--only", choices=["append", "gather", "ring", "belady", "tiers", "weights", "configs4", "copy",
-                                       "all"],
+    ap.add_argument("--only", choices=["append", "gather", "ring", "belady", "tiers", "weights", "configs4",
+                                       "configs0", "copy", "all"],
                     default="all")
     ap.add_argument("--seed", type=int, default=1)
     return ap.parse_args()
@@ -436,6 +437,99 @@ def tiers_leg(torch, dev):
 C5 = dict(L=80, H=8, D=128, P=16, B=4, Tb=131072, hbm_layers=60)
 
 
+def configs0_leg(torch, dev, steps, warmup):
+    """the reference's CPU-runnable case -- the README toy model's cache
+    [12 layers, K/V, B=1, 12 heads, 4096 tokens, 64], seed 0, quantised per (layer, kv,
+    head) and dequantised: FP8 e4m3 per head (FP8KVQuantizer, README.md:157) and the
+    legacy int8 per-tensor functions of precision.py:8-16 applied per slab.  GPU: the HIP
+    kernels; CPU: the same semantics in torch on the host (all of torch's threads and one
+    thread, median of 5 after a warm-up)."""
+    import platform
+    import statistics
+
+    from zenyx_amd import kv
+
+    torch.manual_seed(0)
+    x = torch.randn([12, 2, 1, 12, 4096, 64], dtype=torch.float32).to(torch.bfloat16)
+    n = x.numel()
+    xd = x.to(dev).reshape(24, 1, 12, 4096 * 64)
+
+    def gpu_fp8():
+        c, s = kv.fp8_quant_heads(xd)
+        return c, s, kv.fp8_dequant_heads(c, s)
+
+    slabs = [xd[o, 0, h] for o in range(24) for h in range(12)]
+
+    def gpu_int8():
+        return [kv.int8_legacy_dequant(*kv.int8_legacy_quant(t)) for t in slabs]
+
+    ms_f, _, _ = time_steps(torch, gpu_fp8, steps, warmup)
+    ms_i, _, _ = time_steps(torch, gpu_int8, max(1, steps // 4), 1)
+
+    def cpu_fp8(x):
+        xf = x.reshape(24, 1, 12, 4096 * 64).float()
+        sc = xf.abs().amax(dim=(1, 3)).clamp_min(1e-8) / 448.0
+        codes = (xf / sc[:, None, :, None]).to(torch.float8_e4m3fn)
+        return codes, sc, (codes.float() * sc[:, None, :, None]).to(torch.bfloat16)
+
+    def cpu_int8(x):
+        out = []
+        for o in range(24):
+            for h in range(12):
+                t = x[o // 2, o % 2, 0, h]
+                scale = t.abs().amax().clamp_min(1e-8) / 127.0  # in t's dtype (bf16), as precision.py
+                q = torch.clamp(torch.round(t / scale), -127, 127).to(torch.int8)
+                out.append((q.float() * scale).to(torch.bfloat16))
+        return out
+
+    def med(fn, reps=5):
+        fn(x)
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn(x)
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    threads = torch.get_num_threads()
+    cpu = {}
+    for nt in (threads, 1):
+        torch.set_num_threads(nt)
+        cpu[nt] = (med(cpu_fp8), med(cpu_int8))
+    torch.set_num_threads(threads)
+    # parity of this very run: GPU codes / scales / dequant against the CPU restatement
+    gc, gs, gy = gpu_fp8()
+    cc, cs, cy = cpu_fp8(x)
+    same = (torch.equal(gc.cpu(), cc.view(torch.uint8)) and torch.equal(gs.cpu().view(torch.int32), cs.view(torch.int32))
+            and torch.equal(gy.cpu().view(torch.int16), cy.reshape(gy.shape).view(torch.int16)))
+    same_i8 = all(torch.equal(g.cpu().reshape(-1).view(torch.int16), c.reshape(-1).view(torch.int16))
+                  for g, c in zip(gpu_int8()[:24], cpu_int8(x)[:24]))
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    gb = lambda sec: round(2 * 3 * n / sec / 1e9, 3)  # noqa: E731  quant + dequant, 3 B/element each
+    res = {"workload": "configs[0]: [12,2,1,12,4096,64] bf16 (seed 0), per (layer, kv, head) quant then dequant; "
+                       "FP8 e4m3 per head and the legacy int8 per-tensor functions per slab",
+           "elements": n,
+           "gpu": {"fp8_heads_ms": round(ms_f, 4), "fp8_heads_GBps": gb(ms_f * 1e-3),
+                   "int8_legacy_per_slab_ms": round(ms_i, 3), "int8_legacy_GBps": gb(ms_i * 1e-3),
+                   "note": "the int8 path is 576 launches (one quant and one dequant per slab, the "
+                           "reference's per-tensor API), so it is launch-bound"},
+           "cpu": {"nproc": os.cpu_count(), "model": model, "machine": platform.machine(),
+                   f"threads_{threads}": {"fp8_s": round(cpu[threads][0], 4), "int8_s": round(cpu[threads][1], 4),
+                                          "fp8_GBps": gb(cpu[threads][0]), "int8_GBps": gb(cpu[threads][1])},
+                   "threads_1": {"fp8_s": round(cpu[1][0], 4), "int8_s": round(cpu[1][1], 4),
+                                 "fp8_GBps": gb(cpu[1][0]), "int8_GBps": gb(cpu[1][1])},
+                   "kind": "torch ATen on the host, same semantics (median of 5 after a warm-up)"},
+           "gpu_equals_cpu": {"fp8_codes_scales_dequant": bool(same), "int8_first_24_slabs": bool(same_i8)}}
+    log(f"configs[0]: GPU fp8 {ms_f:.4f} ms, int8 per slab {ms_i:.3f} ms; CPU {threads} threads fp8 "
+        f"{cpu[threads][0]:.3f} s, 1 thread {cpu[1][0]:.3f} s; GPU == CPU: {same}, {same_i8}")
+    return res
+
+
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 on MI355X
 
 
@@ -728,6 +822,13 @@ def main():
                         "config": {"workload": gather["workload"]}})
         del G, k, v
         torch.cuda.empty_cache()
+
+    if args.only in ("configs0", "all"):
+        out["configs0"] = configs0_leg(torch, dev, args.steps, args.warmup)
+        if "value" not in out:
+            c = out["configs0"]
+            out.update({"value": c["gpu"]["fp8_heads_GBps"], "ms_per_step": c["gpu"]["fp8_heads_ms"],
+                        "config": {"workload": c["workload"]}})
 
     if args.only in ("ring", "all"):
         out["ring_attention"] = ring_attention_leg(torch, dev, args.steps, args.warmup, args.skip_cpu)
