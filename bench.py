@@ -533,6 +533,25 @@ def configs0_leg(torch, dev, steps, warmup):
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 on MI355X
 
 
+def make_ring_workload(torch, dev, seed=7):
+    """4 sequences x 8,192 tokens at the Llama-3-8B attention shape (32 query heads over 8 KV
+    heads, D = 128, page 16): random FP8 codes (no NaN codes), pages at random in the pool,
+    fp32 scales, N(0,1) bf16 queries, every sequence's queries at positions 0..8191."""
+    B, T, Hq, H, D, P = 4, 8192, 32, 8, 128, 16
+    n_pages = B * T // P
+    g = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, 256, (n_pages, 2, H, P, D), dtype=torch.uint8, generator=g)
+    codes[(codes & 0x7F) == 0x7F] = 0x3A  # no NaN codes, as the quantizer writes none
+    bt_h = torch.randperm(n_pages, generator=g).to(torch.int32).view(B, T // P)
+    sc_h = torch.rand((2, H), generator=g) * 0.01 + 0.001
+    q_h = torch.randn((B * T, Hq, D), generator=g).to(torch.bfloat16)
+    return dict(B=B, T=T, Hq=Hq, H=H, D=D, P=P, codes=codes, bt_host=bt_h, scales_host=sc_h, q_host=q_h,
+                pool=codes.to(dev), bt=bt_h.to(dev), scales=sc_h.to(dev), q=q_h.to(dev),
+                cu=torch.arange(0, B * T + 1, T, dtype=torch.int32, device=dev),
+                q_pos0=torch.zeros(B, dtype=torch.int32, device=dev),
+                kv_len=torch.full((B,), T, dtype=torch.int32, device=dev))
+
+
 def ring_attention_leg(torch, dev, steps, warmup, skip_cpu):
     """Ring attention straight from the FP8 pages (QuantizedRingAttention's compute,
     README.md:344): 4 sequences x 8,192 tokens, causal, 32 query heads over 8 KV heads,
@@ -543,21 +562,10 @@ def ring_attention_leg(torch, dev, steps, warmup, skip_cpu):
     from oracle import oracle as O
     from zenyx_amd import kv
 
-    B, T, Hq, H, D, P = 4, 8192, 32, 8, 128, 16
-    n_pages = B * T // P
-    g = torch.Generator().manual_seed(7)
-    codes = torch.randint(0, 256, (n_pages, 2, H, P, D), dtype=torch.uint8, generator=g)
-    codes[(codes & 0x7F) == 0x7F] = 0x3A  # no NaN codes, as the quantizer writes none
-    pool = codes.to(dev)
-    bt_h = torch.randperm(n_pages, generator=g).to(torch.int32).view(B, T // P)
-    bt = bt_h.to(dev)
-    sc_h = torch.rand((2, H), generator=g) * 0.01 + 0.001
-    sc = sc_h.to(dev)
-    q_h = torch.randn((B * T, Hq, D), generator=g).to(torch.bfloat16)
-    q = q_h.to(dev)
-    cu = torch.arange(0, B * T + 1, T, dtype=torch.int32, device=dev)
-    qp = torch.zeros(B, dtype=torch.int32, device=dev)
-    kl = torch.full((B,), T, dtype=torch.int32, device=dev)
+    R = make_ring_workload(torch, dev)
+    B, T, Hq, D = R["B"], R["T"], R["Hq"], R["D"]
+    codes, bt_h, sc_h, q_h = R["codes"], R["bt_host"], R["scales_host"], R["q_host"]
+    pool, bt, sc, q, cu, qp, kl = R["pool"], R["bt"], R["scales"], R["q"], R["cu"], R["q_pos0"], R["kv_len"]
     out = torch.empty_like(q)
     flops = 4.0 * B * Hq * D * (T * (T + 1) / 2)  # QK^T and PV over the causal (row, key) pairs
     res = {"workload": "ring attention from FP8 pages: 4 seqs x 8192 tokens causal, 32 query heads over 8 KV "
@@ -588,7 +596,7 @@ def ring_attention_leg(torch, dev, steps, warmup, skip_cpu):
                                "sample": f"oracle zxo_paged_attention_prefill, last {rows} query rows of one "
                                          f"sequence (keys 0..8191, 32 heads): {dt:.2f} s"}
         log(f"CPU oracle: {res['cpu_baseline']['value']:.6f} TFLOP/s ({dt:.2f} s)")
-    del pool, q, out
+    del pool, q, out, R
     torch.cuda.empty_cache()
     return res
 

@@ -9,6 +9,8 @@
   positions of every (sequence, head) checked bit-exact against the oracle's dequant.
 * the decode attention over the same pool, two whole sequences checked against the
   oracle within the stated tolerance (one bf16 ulp plus 2^-17 max|V|).
+* ring attention at bench.py's ring workload (4 x 8,192 causal): sampled rows against the
+  oracle at ring degree 1 and 8, and ring 8 against ring 1 on every output.
 """
 import numpy as np
 import pytest
@@ -96,3 +98,48 @@ def test_configs2_full_gather_and_attention(dev):
         vmax_q = np.repeat(vmax, Hq // H, axis=0)[None]  # [1, Hq, D]
         assert_within_one_ulp(bits16(out[b:b + 1]), want, vmax_q)
     print("attention: 2 sequences x 32 heads within tolerance", flush=True)
+
+
+def test_ring_attention_bench_shape(dev):
+    """The ring-attention workload bench.py times (4 x 8,192 causal, 32 query heads over 8
+    KV heads): rows at both ends of the causal range against the oracle for ring degree 1
+    and 8, and every element of ring 8 against ring 1 (each within one bf16 ulp + 2^-17
+    max|V| of the exact value, so within twice that of each other)."""
+    R = bench.make_ring_workload(torch, dev)
+    T, Hq, H, D, P = R["T"], R["Hq"], R["H"], R["D"], R["P"]
+    outs = {}
+    for ring in (1, 8):
+        outs[ring] = kv.ring_attention_fp8(R["q"], R["cu"], R["q_pos0"], R["pool"], R["scales"], R["bt"],
+                                           R["kv_len"], ring_degree=ring, causal=True, check=True)
+    torch.cuda.synchronize()
+    codes, bt, sc = R["codes"].numpy(), R["bt_host"].numpy(), R["scales_host"].numpy()
+    dec = np.abs(O.e4m3_decode(np.arange(256, dtype=np.uint8)).astype(np.float64))
+    sm = float(np.float32(1.0 / np.sqrt(D)))
+    grp = Hq // H
+    # per sequence and KV head: running max over keys of |V| per channel
+    vmax = np.zeros((R["B"], H, T, D))
+    t = np.arange(T)
+    for b in range(R["B"]):
+        pages = bt[b, t // P]
+        for h in range(H):
+            vmax[b, h] = np.maximum.accumulate(dec[codes[pages, 1, h, t % P, :]], axis=0) * float(sc[1, h])
+    q_bits = bits16(R["q_host"])
+    for b, row in ((0, 0), (0, 1), (0, 4095), (0, 8191), (3, 17), (3, 8190)):
+        i = b * T + row
+        want, _, err = O.paged_attention_prefill(q_bits[i:i + 1], np.array([0, 1], np.int32),
+                                                 np.array([row], np.int32), codes, sc, bt[b:b + 1],
+                                                 np.zeros(1, np.int32), np.full(1, T, np.int32), True, sm)
+        assert err == 0
+        vm = np.repeat(vmax[b, :, row], grp, axis=0)[None]  # [1, Hq, D]
+        for ring in (1, 8):
+            assert_within_one_ulp(bits16(outs[ring][i:i + 1]), want, vm)
+    print("ring 1 and 8: 6 rows x 32 heads within tolerance of the oracle", flush=True)
+    for b in range(R["B"]):  # one sequence at a time (float32 is exact for bf16 values and their differences)
+        a = outs[1][b * T:(b + 1) * T].float().cpu().numpy()
+        c = outs[8][b * T:(b + 1) * T].float().cpu().numpy()
+        vm_b = np.repeat(vmax[b], grp, axis=0).transpose(1, 0, 2).astype(np.float32)  # [T, Hq, D]
+        mag = np.maximum(np.maximum(np.abs(a), np.abs(c)), np.float32(2.0 ** -100))
+        tol = 2 * np.exp2(np.floor(np.log2(mag)) - 7) + np.float32(2.0 ** -16) * vm_b
+        bad = np.abs(a - c) > tol
+        assert not bad.any(), f"sequence {b}: {bad.sum()} elements of ring 8 differ from ring 1 beyond tolerance"
+    print("ring 8 == ring 1 within tolerance on all 33.5 M outputs", flush=True)
