@@ -138,3 +138,33 @@ def test_prefill_flags_bad_pages():
     want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, kb, ke, False, sm)
     assert err & 1
     assert_within_one_ulp(bits16(out), want, vmax_rows(pool, scales, np.where(bt < 8, bt, 0), cu, kb, ke, Hq))
+
+
+def test_prefill_kv_end_past_table_is_clipped_and_flagged():
+    """kv_end beyond max_blocks * page_size: the kernel clips the key range to the table
+    (as the oracle does), flags ZX_KERR_POS_RANGE, and check=True raises."""
+    Hq, Hkv, P = 8, 2, 16
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, [40], [24], [64], seed=11)  # table holds 64 keys
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    kb, ke = np.zeros(1, np.int32), np.full(1, 80, np.int32)
+    with pytest.raises(ValueError, match="max_blocks"):
+        kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kb), t(ke), causal=True,
+                                   check=True)
+    out = kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kb), t(ke), causal=True)
+    torch.cuda.synchronize()
+    sm = float(np.float32(1.0 / np.sqrt(128)))
+    want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, kb, ke, True, sm)
+    assert err & 2
+    assert_within_one_ulp(bits16(out), want, vmax_rows(pool, scales, bt, cu, kb, np.full(1, 64, np.int32), Hq))
+
+
+def test_prefill_rejects_bad_scales():
+    Hq, Hkv, P = 8, 2, 16
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, [16], [0], [16], seed=12)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    kb, ke = np.zeros(1, np.int32), np.full(1, 16, np.int32)
+    with pytest.raises(ValueError, match="scales_layer"):
+        kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales[:, :1]), t(bt), t(kb), t(ke))
+    with pytest.raises(ValueError, match="scales_layer"):
+        kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales.astype(np.float64)), t(bt), t(kb),
+                                   t(ke))

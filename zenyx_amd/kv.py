@@ -308,10 +308,17 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
     if q.dtype != torch.bfloat16 or q.dim() != 3:
         raise ValueError("q must be [n_q, n_q_heads, head_dim] bfloat16")
     N.require_device(pool_layer, "pool_layer")
+    if pool_layer.dim() != 5 or pool_layer.dtype != torch.uint8:
+        raise ValueError("pool_layer must be uint8 [n_pages, 2, n_kv_heads, page_size, head_dim]")
     n_pages, two, Hkv, P, D = pool_layer.shape
     n_q, Hq, Dq = q.shape
     if two != 2 or Dq != D:
         raise ValueError("pool_layer must be [n_pages, 2, n_kv_heads, page_size, head_dim] matching q")
+    N.require_device(scales_layer, "scales_layer")
+    if scales_layer.shape != (2, Hkv) or scales_layer.dtype != torch.float32:
+        raise ValueError(f"scales_layer must be float32 [2, {Hkv}]")
+    if block_tables.dim() != 2:
+        raise ValueError("block_tables must be int32 [n_seqs, max_blocks]")
     for t, name in ((cu_q, "cu_q"), (q_pos0, "q_pos0"), (block_tables, "block_tables"), (kv_begin, "kv_begin"),
                     (kv_end, "kv_end")):
         N.require_device(t, name)
