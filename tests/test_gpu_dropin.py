@@ -154,6 +154,22 @@ def test_kv_tier_manager_lru_and_bytes(dev):
     assert build_ring_timeline(3) == {"forward": [0, 1, 2], "backward": [2, 1, 0]}
 
 
+def test_kv_tier_manager_synchronize_before_another_stream(dev):
+    """After synchronize(), a prefetched block can be read on a stream that was not ordered
+    after the copy."""
+    mgr = KVTierManager(t0_capacity=4, t1_capacity=4)
+    host = torch.randn(1 << 20, generator=torch.Generator().manual_seed(3))
+    mgr.put(7, host)
+    g = mgr.prefetch_to_t0(7, dev)
+    mgr.synchronize(dev)
+    other = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(other):
+        copy = g.clone()
+    other.synchronize()
+    assert torch.equal(copy.cpu(), host)
+    mgr.synchronize()  # every device used so far
+
+
 # ------------------------------------------------------------------ fp8_kv_quantization.py
 
 def test_fp8_kv_quantizer_config1_shape(dev):

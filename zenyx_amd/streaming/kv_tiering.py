@@ -130,6 +130,18 @@ class KVTierManager:
             self.t1[block_id] = to_host(tensor) if tensor.device.type == "cuda" else tensor.detach()
             self._evict_t1_if_needed()
 
+    def synchronize(self, device: torch.device | None = None) -> None:
+        """Wait until the tier copies queued on the side stream (of ``device``, or of every
+        device used so far) are done.  Copies to host already complete before returning, as
+        ``.cpu()`` does in the reference; copies to the device are ordered before later
+        work on the caller's stream and need this only when another stream or the host
+        reads them."""
+        if device is not None:
+            _SideStream.get(torch.device(device)).synchronize()
+            return
+        for s in list(_SideStream._streams.values()):
+            s.synchronize()
+
     def _evict_t0_if_needed(self) -> None:  # :57-61, least recently used first
         while len(self.t0) > self.t0_capacity:
             old_block, old_tensor = self.t0.popitem(last=False)
