@@ -268,7 +268,8 @@ int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, i
  * fp32, block tables [n_seqs][max_blocks] int32 (an entry outside [0, n_pages) skips its
  * keys and sets ZX_KERR_PAGE_RANGE in *err; kv_end beyond max_blocks * page_size is
  * clipped and sets ZX_KERR_POS_RANGE).  max_q_per_seq >= every sequence's query count
- * (host int).  flags:
+ * (host int; a sequence with more rows has the rest left unwritten and sets
+ * ZX_KERR_POS_RANGE).  flags:
  *   ZX_PREFILL_MERGE: merge (o, lse2) into o_acc [n_q][n_q_heads][128] fp32 (normalised
  *     rows) and lse2 [n_q][n_q_heads] fp32, which hold the steps so far;
  *   ZX_PREFILL_INIT (with MERGE): the first step: overwrite instead of merging;

@@ -168,3 +168,24 @@ def test_prefill_rejects_bad_scales():
     with pytest.raises(ValueError, match="scales_layer"):
         kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales.astype(np.float64)), t(bt), t(kb),
                                    t(ke))
+
+
+def test_prefill_flags_rows_beyond_max_q_per_seq():
+    """A max_q_per_seq below a sequence's query count leaves the extra rows unwritten and is
+    flagged (ZX_KERR_POS_RANGE); the covered rows are still right."""
+    Hq, Hkv, P = 8, 2, 16
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, [200], [0], [200], seed=13)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    kb, ke = np.zeros(1, np.int32), np.full(1, 200, np.int32)
+    with pytest.raises(ValueError, match="max_q_per_seq"):
+        kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kb), t(ke),
+                                   max_q_per_seq=64, check=True)
+    out = kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kb), t(ke),
+                                     max_q_per_seq=64)
+    torch.cuda.synchronize()
+    sm = float(np.float32(1.0 / np.sqrt(128)))
+    want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, kb, ke, True, sm)
+    assert err == 0
+    covered = 64  # query tiles of 32 * 4 / G = 32 rows (G = 4 here): ceil(64 / 32) = 2 tiles cover rows 0..63
+    assert_within_one_ulp(bits16(out)[:covered], want[:covered],
+                          vmax_rows(pool, scales, bt, cu, kb, ke, Hq)[:covered])

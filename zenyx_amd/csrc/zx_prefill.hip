@@ -91,6 +91,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   const int64_t v_off = (int64_t)a.n_kv_heads * a.page_size * D;
   const int32_t *bt = a.bt + (int64_t)b * a.max_blocks;
   int32_t e = 0;
+  // rows past gridDim.x * QT (max_q_per_seq too small) are not computed: flag it
+  if (blockIdx.x == 0 && (int64_t)gridDim.x * QT < n_qb) e |= ZX_KERR_POS_RANGE;
   const int kb = a.kv_begin[b] > 0 ? a.kv_begin[b] : 0;
   int ke = a.kv_end[b];
   const int kmax = a.max_blocks * a.page_size;  // < 2^31 (checked by the host)

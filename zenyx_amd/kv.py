@@ -36,7 +36,8 @@ def _raise_kernel_error(err: torch.Tensor, what: str) -> None:
         if e & N.ZX_KERR_PAGE_RANGE:
             parts.append("block table entry outside [0, n_pages)")
         if e & N.ZX_KERR_POS_RANGE:
-            parts.append("token position beyond max_blocks * page_size")
+            parts.append("token position beyond max_blocks * page_size (attention: or a query row beyond "
+                         "max_q_per_seq)")
         if e & N.ZX_KERR_SPIN:
             parts.append("bounded wait ran out")
         raise ValueError(f"{what}: " + "; ".join(parts))
