@@ -9,7 +9,7 @@ from oracle import oracle as O
 from zenyx_amd.streaming import (BeladyApproxCache, KVTierManager, build_ring_timeline,
                                  dequantize_for_bf16_compute, quantize_to_fp8_storage)
 from zenyx_amd.train.belayd_kv_cache_tiering import BeladyKVCacheTieringManager, RingAttentionAccessSequence
-from zenyx_amd.train.fp8_kv_quantization import FP8KVQuantizer, PagedFP8KVCache
+from zenyx_amd.train.fp8_kv_quantization import FP8KVQuantizer, PagedFP8KVCache, QuantizedRingAttention
 
 pytestmark = pytest.mark.gpu
 
@@ -235,3 +235,45 @@ def test_tiering_manager_plan_matches_oracle(dev):
     assert len(h2d) > 0 and len(d2h) >= 0
     r = m.replay_transfers(n // 2, n)
     assert r["h2d_pages"] == len(h2d) and r["d2h_pages"] == len(d2h)
+
+
+def test_quantized_ring_attention_over_paged_cache(dev):
+    """README.md:344's import line, then ring attention and decode over a PagedFP8KVCache
+    (appended twice: a prefill and a continuation) against the oracle, within one bf16 ulp
+    of the exact value + 2^-17 max|V|."""
+    from test_gpu_attention import assert_within_one_ulp
+    from zenyx_amd.train.fp8_kv_quantization import FP8KVQuantizer as _Q, QuantizedRingAttention as _R  # noqa: F401
+
+    L, H, D, P, Hq = 2, 4, 128, 16, 16
+    cache = PagedFP8KVCache(L, H, D, num_pages=64, page_size=P, device=dev)
+    g = torch.Generator().manual_seed(21)
+    lens1, lens2 = [70, 33], [20, 31]
+    cache.append(torch.randn((L, sum(lens1), 2, H, D), generator=g).to(torch.bfloat16), ["a", "b"], lens1)
+    # the continuation reuses the first append's scales: keep it inside their range (no NaN codes)
+    cache.append((0.5 * torch.randn((L, sum(lens2), 2, H, D), generator=g)).to(torch.bfloat16), ["a", "b"], lens2)
+    att = QuantizedRingAttention(cache, ring_degree=3)
+    q = torch.randn((sum(lens2), Hq, D), generator=g).to(torch.bfloat16)
+    layer = 1
+    out = att(q, layer, ["a", "b"], lens2)
+    torch.cuda.synchronize()
+    pool = cache.pool[layer].cpu().numpy()
+    sc = cache.scales[layer].cpu().numpy()
+    bt = cache._tables(["a", "b"]).cpu().numpy()
+    tot = np.array([lens1[0] + lens2[0], lens1[1] + lens2[1]], np.int32)
+    cu = np.array([0, lens2[0], sum(lens2)], np.int32)
+    sm = float(np.float32(1.0 / np.sqrt(D)))
+    want, _, err = O.paged_attention_prefill(bits16(q), cu, tot - np.array(lens2, np.int32), pool, sc, bt,
+                                             np.zeros(2, np.int32), tot, True, sm)
+    assert err == 0
+    dec = np.abs(O.e4m3_decode(np.arange(256, dtype=np.uint8)).astype(np.float64))
+    assert not np.isnan(dec[pool]).any()
+    vmax = float(dec[pool[:, 1]].max() * sc[1].max())
+    assert_within_one_ulp(bits16(out), want, np.full(want.shape, vmax))
+    qd = torch.randn((2, Hq, D), generator=g).to(torch.bfloat16)
+    od = att.decode(qd, layer, ["a", "b"])
+    torch.cuda.synchronize()
+    wd, derr = O.paged_attention_decode(bits16(qd), pool, sc, bt, tot, sm)
+    assert derr == 0
+    assert_within_one_ulp(bits16(od), wd, np.full(wd.shape, vmax))
+    with pytest.raises(ValueError):
+        att(q, layer, ["a", "b"], [lens2[0], lens2[1] + 1])

@@ -7,6 +7,8 @@ its behaviour is defined here and in include/zenyx_kv.h).
 * ``PagedFP8KVCache`` -- a paged FP8 KV cache: page pool ``[L, n_pages, 2, H, P, D]``,
   host-side page allocator and block tables, fused quantize+append of new tokens and
   gather+dequant of whole sequences for decode.
+* ``QuantizedRingAttention`` -- ring attention (and decode) over that cache, reading the
+  FP8 pages directly.
 All arithmetic runs in libzenyx_kv.so on the HIP device.
 """
 from __future__ import annotations
@@ -113,4 +115,51 @@ class PagedFP8KVCache:
         self.lengths.pop(seq_id, None)
 
 
-__all__ = ["FP8KVQuantizer", "PagedFP8KVCache"]
+class QuantizedRingAttention:
+    """Ring attention over a paged FP8 KV cache.  README.md:344 imports it beside
+    ``FP8KVQuantizer``; its code is absent from the reference, so the behaviour is defined
+    here.  The cached keys of each sequence are split into ``ring_degree`` shards (the KV
+    blocks a ring passes between devices); each shard is one ring step that attends the
+    queries to it straight from the FP8 pages (no bf16 copy of K/V) and merges by
+    log-sum-exp into a running fp32 output, so the result is softmax(sm_scale q K^T) V over
+    all cached keys (causal: keys up to each query's position).  On one GPU the steps run
+    in sequence.  ``decode`` is the one-token case (split-K decode kernel)."""
+
+    def __init__(self, cache: PagedFP8KVCache, ring_degree: int = 8, causal: bool = True,
+                 sm_scale: float | None = None):
+        if ring_degree < 1:
+            raise ValueError("ring_degree must be >= 1")
+        self.cache = cache
+        self.ring_degree = ring_degree
+        self.causal = causal
+        self.sm_scale = sm_scale
+
+    def __call__(self, q: torch.Tensor, layer: int, seq_ids: list, q_lens: list[int]) -> torch.Tensor:
+        """q ``[n_q, Hq, D]`` bf16: the queries of ``seq_ids[i]`` packed in order, ``q_lens[i]``
+        rows each, standing for that sequence's newest ``q_lens[i]`` cached tokens (the
+        tokens just appended, as in prefill).  Returns bf16 ``[n_q, Hq, D]``."""
+        c = self.cache
+        if len(q_lens) != len(seq_ids) or sum(q_lens) != q.shape[0]:
+            raise ValueError("q_lens must give the row count of every sequence in seq_ids, summing to q.shape[0]")
+        lens = [c.lengths.get(s, 0) for s in seq_ids]
+        if any(n > m for n, m in zip(q_lens, lens)):
+            raise ValueError("a sequence has more query rows than cached tokens")
+        cu = [0]
+        for n in q_lens:
+            cu.append(cu[-1] + n)
+        dev = c.device
+        return kv.ring_attention_fp8(
+            q.to(dev).contiguous(), torch.tensor(cu, dtype=torch.int32).to(dev),
+            torch.tensor([m - n for n, m in zip(q_lens, lens)], dtype=torch.int32).to(dev), c.pool[layer],
+            c.scales[layer].contiguous(), c._tables(seq_ids), torch.tensor(lens, dtype=torch.int32).to(dev),
+            ring_degree=self.ring_degree, causal=self.causal, sm_scale=self.sm_scale, check=True)
+
+    def decode(self, q: torch.Tensor, layer: int, seq_ids: list) -> torch.Tensor:
+        """q ``[B, Hq, D]`` bf16, one query token per sequence over all its cached tokens."""
+        c = self.cache
+        lens = torch.tensor([c.lengths.get(s, 0) for s in seq_ids], dtype=torch.int32).to(c.device)
+        return kv.paged_attention_decode(q.to(c.device).contiguous(), c.pool[layer], c.scales[layer].contiguous(),
+                                         c._tables(seq_ids), lens, sm_scale=self.sm_scale, check=True)
+
+
+__all__ = ["FP8KVQuantizer", "PagedFP8KVCache", "QuantizedRingAttention"]
