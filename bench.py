@@ -729,7 +729,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the KV hot path is benchmarked on a "
-                          "single MI355X (multi-GPU sharding is described in DESIGN.md, not run)",
+                          "single MI355X (how the path shards over GPUs is designed, not run)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
