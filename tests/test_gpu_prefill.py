@@ -189,3 +189,22 @@ def test_prefill_flags_rows_beyond_max_q_per_seq():
     covered = 64  # query tiles of 32 * 4 / G = 32 rows (G = 4 here): ceil(64 / 32) = 2 tiles cover rows 0..63
     assert_within_one_ulp(bits16(out)[:covered], want[:covered],
                           vmax_rows(pool, scales, bt, cu, kb, ke, Hq)[:covered])
+
+
+def test_ring_degree_above_sequence_lengths():
+    """Ring degree 8 over sequences of 3, 1 and 20 keys: most shards are empty (the first
+    one too, which must still initialise the running output), the result is still full
+    causal attention."""
+    Hq, Hkv, P = 8, 2, 16
+    lens = [3, 1, 20]
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, lens, [0, 0, 0], lens, seed=17)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    kl = np.asarray(lens, np.int32)
+    out = kv.ring_attention_fp8(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kl), ring_degree=8,
+                                causal=True, check=True)
+    torch.cuda.synchronize()
+    sm = float(np.float32(1.0 / np.sqrt(128)))
+    zeros = np.zeros(3, np.int32)
+    want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, zeros, kl, True, sm)
+    assert err == 0
+    assert_within_one_ulp(bits16(out), want, vmax_rows(pool, scales, bt, cu, zeros, kl, Hq))
