@@ -62,11 +62,5 @@ __device__ __forceinline__ float xrow_max(float v) {
   xrow_pair16(fmaxf(x, y), x, y);
   return fmaxf(x, y);
 }
-__device__ __forceinline__ float xrow_sum(float v) {
-  float x, y;
-  xrow_pair32(v, x, y);
-  xrow_pair16(x + y, x, y);
-  return x + y;
-}
 
 }  // namespace zx
