@@ -69,25 +69,23 @@ def test_three_tier_replay_keeps_bytes(tmp_path, which, c0, c1, spare, max_batch
     pb = 4096
     print(f"replay case {which}: n={trace.size} c0={c0} c1={c1} spare={spare}", flush=True)
     plan = ThreeTierPlan(torch.from_numpy(trace).to(DEV), n_pages, c0, c1, spare=spare)
-    rep = ThreeTierReplay(plan, pb, str(tmp_path / "t2.bin"), device=DEV, io_threads=4)
-    t0_rows = rep.t0.view(-1, pb)
+    with ThreeTierReplay(plan, pb, str(tmp_path / "t2.bin"), device=DEV, io_threads=4) as rep:
+        t0_rows = rep.t0.view(-1, pb)
 
-    def create(pages, slots):
-        t0_rows[torch.from_numpy(slots).to(DEV)] = _pattern(torch.from_numpy(pages).to(DEV), pb)
+        def create(pages, slots):
+            t0_rows[torch.from_numpy(slots).to(DEV)] = _pattern(torch.from_numpy(pages).to(DEV), pb)
 
-    checked = [0]
+        checked = [0]
 
-    def after_batch(a, b):
-        pages = torch.from_numpy(plan.trace[a:b]).to(DEV)
-        slots = torch.from_numpy(plan.slot0[a:b]).to(DEV)
-        got = t0_rows[slots]
-        assert torch.equal(got, _pattern(pages, pb)), f"bytes differ in batch [{a}, {b})"
-        checked[0] += b - a
+        def after_batch(a, b):
+            pages = torch.from_numpy(plan.trace[a:b]).to(DEV)
+            slots = torch.from_numpy(plan.slot0[a:b]).to(DEV)
+            got = t0_rows[slots]
+            assert torch.equal(got, _pattern(pages, pb)), f"bytes differ in batch [{a}, {b})"
+            checked[0] += b - a
 
-    try:
         out = rep.run(0, trace.size, create=create, after_batch=after_batch, max_batch=max_batch)
-    finally:
-        rep.close()
+    assert rep.fd is None
     assert checked[0] == trace.size
     st = plan.stats()
     assert out["new_pages"] == st["new"] and out["t2_t0_pages"] == st["from_t2"]

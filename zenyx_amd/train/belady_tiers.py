@@ -286,13 +286,15 @@ class ThreeTierReplay:
         if direct_io and hasattr(os, "O_DIRECT") and self.pb % 4096 == 0:
             try:
                 fd = os.open(t2_path, flags | os.O_DIRECT, 0o600)
+                probe = mmap.mmap(-1, self.pb)
                 try:
-                    probe = mmap.mmap(-1, self.pb)
                     os.pwritev(fd, [probe], 0)
                     os.preadv(fd, [probe], 0)
                     self.fd, self.direct = fd, True
                 except OSError:
                     os.close(fd)
+                finally:
+                    probe.close()
             except OSError:
                 pass
         if self.fd is None:
@@ -327,6 +329,12 @@ class ThreeTierReplay:
         if self.fd is not None:
             os.close(self.fd)
             self.fd = None
+
+    def __enter__(self) -> "ThreeTierReplay":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()
 
     def _stage(self, which: str, n: int) -> torch.Tensor:
         cur = getattr(self, which)
