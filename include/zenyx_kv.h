@@ -74,6 +74,17 @@ int zx_int8_legacy_quant(const void *x, int dtype, int64_t n, int8_t *q, void *s
 int zx_int8_legacy_dequant(const int8_t *q, const void *scale, int scale_dtype, int64_t n,
                            uint16_t *y, zx_stream_t stream);
 
+/* The two functions above applied to n_slabs equal, contiguous slabs of slab_len
+ * elements in one launch each, one scale per slab (scales: n_slabs elements of dtype):
+ * precision.py:8-16 applied per (layer, kv, head) slab, bit-identical to calling the
+ * per-tensor functions on every slab.  1 <= n_slabs <= 65535, slab_len >= 1 for the
+ * quant; workspace of zx_int8_legacy_quant_slabs_workspace_bytes(n_slabs) bytes. */
+size_t zx_int8_legacy_quant_slabs_workspace_bytes(int64_t n_slabs);
+int zx_int8_legacy_quant_slabs(const void *x, int dtype, int64_t n_slabs, int64_t slab_len, int8_t *q,
+                               void *scales, void *workspace, size_t workspace_bytes, zx_stream_t stream);
+int zx_int8_legacy_dequant_slabs(const int8_t *q, const void *scales, int scale_dtype, int64_t n_slabs,
+                                 int64_t slab_len, uint16_t *y, zx_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * FP8 e4m3fn with one scale per (outer, head): FP8KVQuantizer.quantize
  * (README.md:329, 344; "per-head dynamic scaling" README.md:157).

@@ -39,6 +39,28 @@ def test_int8_legacy_quant_dequant(dev, dt, mag):
     np.testing.assert_array_equal(got[~g_nan], want[~w_nan])
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_int8_legacy_slabs_match_per_tensor_and_oracle(dev, dt):
+    """Per-slab batch (one launch) == the per-tensor functions on every slab == the oracle,
+    with slabs of different magnitudes, an all-zero slab (scale from the 1e-8 floor) and a
+    slab with one outlier; slab length not a multiple of the block size."""
+    g = torch.Generator().manual_seed(3 + len(dt))
+    mags = [1.0, 1e-3, 0.0, 3e2, 1.0, 7.5]
+    x = torch.stack([torch.randn(2, 1037, generator=g) * m for m in mags])
+    x[4, 1, 5] = 40.0
+    x = x.to(DTYPES[dt])
+    q, sc = kv.int8_legacy_quant_slabs(x.to(dev))
+    y = kv.int8_legacy_dequant_slabs(q, sc)
+    assert q.shape == x.shape and sc.shape == (len(mags),) and sc.dtype == x.dtype and y.dtype == torch.bfloat16
+    for i in range(len(mags)):
+        q1, s1 = kv.int8_legacy_quant(x[i].to(dev))
+        assert torch.equal(q[i].cpu(), q1.cpu())
+        assert raw(sc[i:i + 1]).tobytes() == raw(s1.reshape(1)).tobytes()
+        wq, ws = O.int8_legacy_quant(raw(x[i]), dt)
+        np.testing.assert_array_equal(q[i].cpu().numpy(), wq)
+        np.testing.assert_array_equal(raw(y[i]), O.int8_legacy_dequant(wq, ws))
+
+
 def test_int8_legacy_empty_raises(dev):
     with pytest.raises(RuntimeError):
         kv.int8_legacy_quant(torch.empty(0, device=dev))

@@ -37,6 +37,9 @@ SIGNATURES = {
     "zx_abi_version": (_INT, []),
     "zx_int8_legacy_quant": (_INT, [_P, _INT, _I64, _P, _P, _P, _SZ, _P]),
     "zx_int8_legacy_dequant": (_INT, [_P, _P, _INT, _I64, _P, _P]),
+    "zx_int8_legacy_quant_slabs_workspace_bytes": (_SZ, [_I64]),
+    "zx_int8_legacy_quant_slabs": (_INT, [_P, _INT, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "zx_int8_legacy_dequant_slabs": (_INT, [_P, _P, _INT, _I64, _I64, _P, _P]),
     "zx_fp8_quant_heads": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "zx_fp8_dequant_heads": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "zx_fp8_encode_f32": (_INT, [_P, _I64, _P, _P]),

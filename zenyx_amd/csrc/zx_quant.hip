@@ -113,6 +113,47 @@ __global__ void legacy_dequant_kernel(const int8_t *q, const void *scale, int64_
   }
 }
 
+// The same functions applied to n_slabs equal slabs in one launch (one scale per slab):
+// grid.y = slab, grid.x blocks stride through the slab.
+template <int DT>
+__global__ void legacy_amax_slabs_kernel(const void *x, int64_t slab_len, uint32_t *amax_bits) {
+  const int64_t base = (int64_t)blockIdx.y * slab_len;
+  uint32_t m = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < slab_len; i += (int64_t)gridDim.x * blockDim.x)
+    m = max(m, Dt<DT>::absbits(x, base + i));
+  m = block_max(m);
+  if (threadIdx.x == 0) atomicMax(&amax_bits[blockIdx.y], m);
+}
+
+template <int DT>
+__global__ void legacy_quant_slabs_kernel(const void *x, int64_t slab_len, const uint32_t *amax_bits, int8_t *q,
+                                          void *scales) {
+  const int64_t base = (int64_t)blockIdx.y * slab_len;
+  float a = Dt<DT>::from_absbits(amax_bits[blockIdx.y]);
+  const float lo = Dt<DT>::round(1e-8f);
+  if (a < lo) a = lo;
+  const float s = Dt<DT>::round(a / 127.0f);
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    Dt<DT>::store((char *)scales + (DT == ZX_F32 ? 4 : 2) * (int64_t)blockIdx.y, s);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < slab_len; i += (int64_t)gridDim.x * blockDim.x) {
+    float v = __builtin_rintf(Dt<DT>::round(Dt<DT>::load(x, base + i) / s));
+    int8_t o;
+    if (v != v) o = 0;
+    else o = (int8_t)fminf(fmaxf(v, -127.0f), 127.0f);
+    q[base + i] = o;
+  }
+}
+
+template <int DT>
+__global__ void legacy_dequant_slabs_kernel(const int8_t *q, const void *scales, int64_t slab_len, uint16_t *y) {
+  const int64_t base = (int64_t)blockIdx.y * slab_len;
+  const float s = Dt<DT>::load(scales, blockIdx.y);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < slab_len; i += (int64_t)gridDim.x * blockDim.x) {
+    __bf16 h = (__bf16)((float)q[base + i] * s);
+    y[base + i] = __builtin_bit_cast(uint16_t, h);
+  }
+}
+
 static unsigned grid_for(int64_t n, int per_thread = 1) {
   int64_t want = ceil_div(n, 256LL * per_thread);
   int64_t cap = (int64_t)num_cus() * 16;
@@ -426,6 +467,69 @@ extern "C" int zx_int8_legacy_quant(const void *x, int dtype, int64_t n, int8_t 
       return fail(ZX_ERR_INVALID, "int8_legacy_quant: unknown dtype %d", dtype);
   }
   return check_launch("legacy_quant");
+}
+
+extern "C" size_t zx_int8_legacy_quant_slabs_workspace_bytes(int64_t n_slabs) {
+  return (size_t)((n_slabs > 0 ? n_slabs : 0) * 4 + 255) / 256 * 256;
+}
+
+extern "C" int zx_int8_legacy_quant_slabs(const void *x, int dtype, int64_t n_slabs, int64_t slab_len, int8_t *q,
+                                          void *scales, void *workspace, size_t workspace_bytes, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(x && q && scales, "int8_legacy_quant_slabs: null pointer");
+  ZX_REQUIRE(n_slabs > 0 && n_slabs <= 65535 && slab_len > 0,
+             "int8_legacy_quant_slabs: need 1..65535 slabs of at least one element (the reference raises on amax of "
+             "an empty tensor)");
+  if (!workspace || workspace_bytes < zx_int8_legacy_quant_slabs_workspace_bytes(n_slabs))
+    return fail(ZX_ERR_WORKSPACE, "int8_legacy_quant_slabs: workspace < %zu bytes",
+                zx_int8_legacy_quant_slabs_workspace_bytes(n_slabs));
+  hipStream_t st = as_stream(stream);
+  uint32_t *amax = reinterpret_cast<uint32_t *>(workspace);
+  int rc = fill_u32(amax, n_slabs, 0, st);
+  if (rc) return rc;
+  // blocks per slab: enough for ~16 per CU over all slabs, at least one
+  int64_t bps = ceil_div((int64_t)num_cus() * 16, n_slabs);
+  bps = bps < 1 ? 1 : (bps > ceil_div(slab_len, 256LL * 8) ? ceil_div(slab_len, 256LL * 8) : bps);
+  const dim3 grid((unsigned)bps, (unsigned)n_slabs);
+  switch (dtype) {
+    case ZX_BF16:
+      legacy_amax_slabs_kernel<ZX_BF16><<<grid, 256, 0, st>>>(x, slab_len, amax);
+      if ((rc = check_launch("legacy_amax_slabs"))) return rc;
+      legacy_quant_slabs_kernel<ZX_BF16><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
+      break;
+    case ZX_F16:
+      legacy_amax_slabs_kernel<ZX_F16><<<grid, 256, 0, st>>>(x, slab_len, amax);
+      if ((rc = check_launch("legacy_amax_slabs"))) return rc;
+      legacy_quant_slabs_kernel<ZX_F16><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
+      break;
+    case ZX_F32:
+      legacy_amax_slabs_kernel<ZX_F32><<<grid, 256, 0, st>>>(x, slab_len, amax);
+      if ((rc = check_launch("legacy_amax_slabs"))) return rc;
+      legacy_quant_slabs_kernel<ZX_F32><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
+      break;
+    default:
+      return fail(ZX_ERR_INVALID, "int8_legacy_quant_slabs: unknown dtype %d", dtype);
+  }
+  return check_launch("legacy_quant_slabs");
+}
+
+extern "C" int zx_int8_legacy_dequant_slabs(const int8_t *q, const void *scales, int scale_dtype, int64_t n_slabs,
+                                            int64_t slab_len, uint16_t *y, zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(q && scales && y, "int8_legacy_dequant_slabs: null pointer");
+  ZX_REQUIRE(n_slabs >= 0 && n_slabs <= 65535 && slab_len >= 0, "int8_legacy_dequant_slabs: bad sizes");
+  if (n_slabs == 0 || slab_len == 0) return ZX_OK;
+  hipStream_t st = as_stream(stream);
+  int64_t bps = ceil_div((int64_t)num_cus() * 16, n_slabs);
+  bps = bps < 1 ? 1 : (bps > ceil_div(slab_len, 256LL * 8) ? ceil_div(slab_len, 256LL * 8) : bps);
+  const dim3 grid((unsigned)bps, (unsigned)n_slabs);
+  switch (scale_dtype) {
+    case ZX_BF16: legacy_dequant_slabs_kernel<ZX_BF16><<<grid, 256, 0, st>>>(q, scales, slab_len, y); break;
+    case ZX_F16: legacy_dequant_slabs_kernel<ZX_F16><<<grid, 256, 0, st>>>(q, scales, slab_len, y); break;
+    case ZX_F32: legacy_dequant_slabs_kernel<ZX_F32><<<grid, 256, 0, st>>>(q, scales, slab_len, y); break;
+    default: return fail(ZX_ERR_INVALID, "int8_legacy_dequant_slabs: unknown dtype %d", scale_dtype);
+  }
+  return check_launch("legacy_dequant_slabs");
 }
 
 extern "C" int zx_int8_legacy_dequant(const int8_t *q, const void *scale, int scale_dtype, int64_t n,

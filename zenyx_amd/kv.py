@@ -85,6 +85,44 @@ def int8_legacy_dequant(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def int8_legacy_quant_slabs(x: torch.Tensor):
+    """precision.py:8-12 applied to every slab ``x[i]`` of ``x [n_slabs, ...]`` in one launch:
+    (q int8 like x, scales ``[n_slabs]`` in x.dtype), bit-identical to
+    ``int8_legacy_quant(x[i])`` for every i."""
+    N.ensure_gpu()
+    if x.dtype not in _DT:
+        raise TypeError(f"quantize_to_fp8_storage: unsupported dtype {x.dtype}")
+    if x.dim() < 1 or x.shape[0] == 0 or x[0].numel() == 0:
+        raise RuntimeError("quantize_to_fp8_storage: cannot quantize an empty tensor (amax over zero elements)")
+    x = x.contiguous()
+    N.require_device(x, "x")
+    n_slabs, slab = x.shape[0], x[0].numel()
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scales = torch.empty((n_slabs,), dtype=x.dtype, device=x.device)
+    ws = _workspace(N.load().zx_int8_legacy_quant_slabs_workspace_bytes(n_slabs), x.device)
+    N.check(N.load().zx_int8_legacy_quant_slabs(N.ptr(x), _DT[x.dtype], n_slabs, slab, N.ptr(q), N.ptr(scales),
+                                                N.ptr(ws), ws.numel(), N.stream_ptr(x.device)),
+            "int8_legacy_quant_slabs")
+    return q, scales
+
+
+def int8_legacy_dequant_slabs(q: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """precision.py:15-16 applied to every slab: bf16 ``y[i] = (q[i].float() * scales[i]).to(bf16)``."""
+    N.ensure_gpu()
+    if q.dtype != torch.int8 or q.dim() < 1:
+        raise ValueError("q must be int8 [n_slabs, ...]")
+    if scales.dtype not in _DT or scales.shape != (q.shape[0],):
+        raise ValueError("scales must be [n_slabs] in bf16, f16 or f32")
+    q, scales = q.contiguous(), scales.contiguous()
+    N.require_device(q, "q")
+    N.require_device(scales, "scales")
+    y = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    N.check(N.load().zx_int8_legacy_dequant_slabs(N.ptr(q), N.ptr(scales), _DT[scales.dtype], q.shape[0],
+                                                  q[0].numel() if q.shape[0] else 0, N.ptr(y), N.stream_ptr(q.device)),
+            "int8_legacy_dequant_slabs")
+    return y
+
+
 # ------------------------------------------------------------------ FP8 per head
 
 def fp8_quant_heads(x: torch.Tensor):
