@@ -5,6 +5,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
+from zenyx_amd import _native as N
 from zenyx_amd import kv
 
 pytestmark = pytest.mark.gpu
@@ -40,13 +41,14 @@ def test_int8_legacy_quant_dequant(dev, dt, mag):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
-def test_int8_legacy_slabs_match_per_tensor_and_oracle(dev, dt):
+@pytest.mark.parametrize("shape", [(2, 1037), (4, 256)])  # unaligned slabs (element path), aligned (16-byte path)
+def test_int8_legacy_slabs_match_per_tensor_and_oracle(dev, dt, shape):
     """Per-slab batch (one launch) == the per-tensor functions on every slab == the oracle,
     with slabs of different magnitudes, an all-zero slab (scale from the 1e-8 floor) and a
     slab with one outlier; slab length not a multiple of the block size."""
     g = torch.Generator().manual_seed(3 + len(dt))
     mags = [1.0, 1e-3, 0.0, 3e2, 1.0, 7.5]
-    x = torch.stack([torch.randn(2, 1037, generator=g) * m for m in mags])
+    x = torch.stack([torch.randn(*shape, generator=g) * m for m in mags])
     x[4, 1, 5] = 40.0
     x = x.to(DTYPES[dt])
     q, sc = kv.int8_legacy_quant_slabs(x.to(dev))
@@ -59,6 +61,29 @@ def test_int8_legacy_slabs_match_per_tensor_and_oracle(dev, dt):
         wq, ws = O.int8_legacy_quant(raw(x[i]), dt)
         np.testing.assert_array_equal(q[i].cpu().numpy(), wq)
         np.testing.assert_array_equal(raw(y[i]), O.int8_legacy_dequant(wq, ws))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_int8_legacy_unaligned_view(dev, dt):
+    """A view starting one element in (not 16-byte aligned) takes the element-by-element
+    path; results equal the oracle's."""
+    g = torch.Generator().manual_seed(9)
+    base = (torch.randn(4097, generator=g) * 3).to(DTYPES[dt]).to(dev)
+    x = base[1:]  # the Python wrappers require 16-byte alignment: call the C ABI directly
+    qb = torch.empty(4097, dtype=torch.int8, device=dev)
+    q = qb[1:]
+    s = torch.empty((), dtype=x.dtype, device=dev)
+    ws = torch.empty(256, dtype=torch.uint8, device=dev)
+    lib = N.load()
+    N.check(lib.zx_int8_legacy_quant(N.ptr(x), kv._DT[x.dtype], x.numel(), N.ptr(q), N.ptr(s), N.ptr(ws), 256,
+                                     N.stream_ptr(dev)), "int8_legacy_quant")
+    wq, wsc = O.int8_legacy_quant(raw(x), dt)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+    yb = torch.empty(4097, dtype=torch.bfloat16, device=dev)
+    y = yb[1:]
+    N.check(lib.zx_int8_legacy_dequant(N.ptr(q), N.ptr(s), kv._DT[s.dtype], q.numel(), N.ptr(y), N.stream_ptr(dev)),
+            "int8_legacy_dequant")
+    np.testing.assert_array_equal(raw(y), O.int8_legacy_dequant(wq, wsc))
 
 
 def test_int8_legacy_empty_raises(dev):

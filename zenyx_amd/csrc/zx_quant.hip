@@ -73,91 +73,127 @@ template <> struct Dt<ZX_F32> {
 
 // For all three formats the integer order of |x| bit patterns is the float order, with
 // NaN patterns above infinity, so an integer max is the float amax (NaN-propagating).
-template <int DT>
-__global__ void legacy_amax_kernel(const void *x, int64_t n, uint32_t *amax_bits) {
-  uint32_t m = 0;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    m = max(m, Dt<DT>::absbits(x, i));
-  m = block_max(m);
-  if (threadIdx.x == 0) atomicMax(amax_bits, m);
-}
+// Quantisation follows precision.py:10-11 with torch's CPU arithmetic: every intermediate
+// is rounded to the storage dtype, division is IEEE fp32 division, round() is
+// half-to-even.
 
-// precision.py:10-11 with torch's CPU arithmetic: every intermediate is rounded to the
-// storage dtype, division is IEEE fp32 division, round() is half-to-even.
-template <int DT>
-__global__ void legacy_quant_kernel(const void *x, int64_t n, const uint32_t *amax_bits, int8_t *q,
-                                    void *scale_out) {
-  float a = Dt<DT>::from_absbits(*amax_bits);
-  const float lo = Dt<DT>::round(1e-8f);
-  if (a < lo) a = lo;
-  const float s = Dt<DT>::round(a / 127.0f);
-  if (blockIdx.x == 0 && threadIdx.x == 0) Dt<DT>::store(scale_out, s);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    float v = __builtin_rintf(Dt<DT>::round(Dt<DT>::load(x, i) / s));
-    int8_t o;
-    if (v != v) o = 0;  // int8 of NaN is not defined by the reference; 0 is torch CPU's
-    else o = (int8_t)fminf(fmaxf(v, -127.0f), 127.0f);
-    q[i] = o;
+// The same functions applied to n_slabs equal slabs in one launch (one scale per slab;
+// the per-tensor entry points are the case n_slabs = 1): grid.y = slab, grid.x blocks
+// stride through the slab.  VEC: 16-byte lane loads (W = 8 16-bit or 4 fp32 elements;
+// int8 codes stored as W-byte words, bf16 dequant output as 16-byte words), which needs
+// 16-byte aligned slabs; a slab's last n % W elements go element by element.
+template <int DT> struct LegacyVec {
+  static constexpr int W = DT == ZX_F32 ? 4 : 8;
+  static constexpr int ES = DT == ZX_F32 ? 4 : 2;
+  __device__ static uint32_t absmax(uint4 v) {
+    if constexpr (DT == ZX_F32) {
+      return max(max(v.x & 0x7FFFFFFFu, v.y & 0x7FFFFFFFu), max(v.z & 0x7FFFFFFFu, v.w & 0x7FFFFFFFu));
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      uint32_t m = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = max(m, max(w[i] & 0x7FFFu, (w[i] >> 16) & 0x7FFFu));
+      return m;
+    }
   }
-}
-
-template <int DT>
-__global__ void legacy_dequant_kernel(const int8_t *q, const void *scale, int64_t n, uint16_t *y) {
-  const float s = Dt<DT>::load(scale, 0);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    __bf16 h = (__bf16)((float)q[i] * s);
-    y[i] = __builtin_bit_cast(uint16_t, h);
+  __device__ static float elem(uint4 v, int j) {  // element j of the vector, as float
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    if constexpr (DT == ZX_F32) {
+      return __uint_as_float(w[j]);
+    } else {
+      const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+      return Dt<DT>::load(&h, 0);
+    }
   }
+};
+
+template <int DT>
+__device__ __forceinline__ int8_t legacy_code(float xv, float s) {
+  const float v = __builtin_rintf(Dt<DT>::round(xv / s));
+  return v != v ? (int8_t)0 : (int8_t)fminf(fmaxf(v, -127.0f), 127.0f);  // NaN -> 0, as torch CPU
 }
 
-// The same functions applied to n_slabs equal slabs in one launch (one scale per slab):
-// grid.y = slab, grid.x blocks stride through the slab.
-template <int DT>
+template <int DT, bool VEC>
 __global__ void legacy_amax_slabs_kernel(const void *x, int64_t slab_len, uint32_t *amax_bits) {
+  using V = LegacyVec<DT>;
   const int64_t base = (int64_t)blockIdx.y * slab_len;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
   uint32_t m = 0;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < slab_len; i += (int64_t)gridDim.x * blockDim.x)
-    m = max(m, Dt<DT>::absbits(x, base + i));
+  int64_t done = 0;
+  if constexpr (VEC) {
+    const uint4 *xv = reinterpret_cast<const uint4 *>((const char *)x + base * V::ES);
+    const int64_t nv = slab_len / V::W;
+    for (int64_t v = t0; v < nv; v += stride) m = max(m, V::absmax(xv[v]));
+    done = nv * V::W;
+  }
+  for (int64_t i = done + t0; i < slab_len; i += stride) m = max(m, Dt<DT>::absbits(x, base + i));
   m = block_max(m);
   if (threadIdx.x == 0) atomicMax(&amax_bits[blockIdx.y], m);
 }
 
-template <int DT>
+template <int DT, bool VEC>
 __global__ void legacy_quant_slabs_kernel(const void *x, int64_t slab_len, const uint32_t *amax_bits, int8_t *q,
                                           void *scales) {
+  using V = LegacyVec<DT>;
   const int64_t base = (int64_t)blockIdx.y * slab_len;
   float a = Dt<DT>::from_absbits(amax_bits[blockIdx.y]);
   const float lo = Dt<DT>::round(1e-8f);
   if (a < lo) a = lo;
   const float s = Dt<DT>::round(a / 127.0f);
-  if (blockIdx.x == 0 && threadIdx.x == 0)
-    Dt<DT>::store((char *)scales + (DT == ZX_F32 ? 4 : 2) * (int64_t)blockIdx.y, s);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < slab_len; i += (int64_t)gridDim.x * blockDim.x) {
-    float v = __builtin_rintf(Dt<DT>::round(Dt<DT>::load(x, base + i) / s));
-    int8_t o;
-    if (v != v) o = 0;
-    else o = (int8_t)fminf(fmaxf(v, -127.0f), 127.0f);
-    q[base + i] = o;
+  if (blockIdx.x == 0 && threadIdx.x == 0) Dt<DT>::store((char *)scales + V::ES * (int64_t)blockIdx.y, s);
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t done = 0;
+  if constexpr (VEC) {
+    const uint4 *xv = reinterpret_cast<const uint4 *>((const char *)x + base * V::ES);
+    const int64_t nv = slab_len / V::W;
+    for (int64_t v = t0; v < nv; v += stride) {
+      const uint4 xw = xv[v];
+      uint32_t c[V::W / 4];
+#pragma unroll
+      for (int k = 0; k < V::W / 4; ++k) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w |= (uint32_t)(uint8_t)legacy_code<DT>(V::elem(xw, 4 * k + j), s) << (8 * j);
+        c[k] = w;
+      }
+      if constexpr (V::W == 8)
+        reinterpret_cast<uint2 *>(q + base)[v] = make_uint2(c[0], c[1]);
+      else
+        reinterpret_cast<uint32_t *>(q + base)[v] = c[0];
+    }
+    done = nv * V::W;
   }
+  for (int64_t i = done + t0; i < slab_len; i += stride) q[base + i] = legacy_code<DT>(Dt<DT>::load(x, base + i), s);
 }
 
-template <int DT>
+template <int DT, bool VEC>
 __global__ void legacy_dequant_slabs_kernel(const int8_t *q, const void *scales, int64_t slab_len, uint16_t *y) {
   const int64_t base = (int64_t)blockIdx.y * slab_len;
   const float s = Dt<DT>::load(scales, blockIdx.y);
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < slab_len; i += (int64_t)gridDim.x * blockDim.x) {
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t done = 0;
+  if constexpr (VEC) {  // 8 codes -> 8 bf16 per lane
+    const uint2 *qv = reinterpret_cast<const uint2 *>(q + base);
+    uint4 *yv = reinterpret_cast<uint4 *>(y + base);
+    const int64_t nv = slab_len / 8;
+    for (int64_t v = t0; v < nv; v += stride) {
+      const uint2 c = qv[v];
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t w = k < 2 ? c.x : c.y;
+        const int8_t c0 = (int8_t)(w >> (16 * (k & 1))), c1 = (int8_t)(w >> (16 * (k & 1) + 8));
+        o[k] = pack_bf16((float)c0 * s, (float)c1 * s);
+      }
+      typedef unsigned int lq_v4u __attribute__((ext_vector_type(4)));
+      __builtin_nontemporal_store(lq_v4u{o[0], o[1], o[2], o[3]}, reinterpret_cast<lq_v4u *>(yv + v));
+    }
+    done = nv * 8;
+  }
+  for (int64_t i = done + t0; i < slab_len; i += stride) {
     __bf16 h = (__bf16)((float)q[base + i] * s);
     y[base + i] = __builtin_bit_cast(uint16_t, h);
   }
-}
-
-static unsigned grid_for(int64_t n, int per_thread = 1) {
-  int64_t want = ceil_div(n, 256LL * per_thread);
-  int64_t cap = (int64_t)num_cus() * 16;
-  return (unsigned)(want < 1 ? 1 : (want > cap ? cap : want));
 }
 
 // ================================================================== FP8 per (outer, head)
@@ -436,37 +472,78 @@ using namespace zx;
 
 // ================================================================== C ABI
 
+namespace {
+// blocks per slab: ~16 per CU over all slabs, at most one per 8 K elements of a slab
+unsigned legacy_blocks_per_slab(int64_t n_slabs, int64_t slab_len) {
+  const int64_t bps = ceil_div((int64_t)num_cus() * 16, n_slabs);
+  int64_t cap = ceil_div(slab_len, 256LL * 32);
+  if (cap < 1) cap = 1;
+  return (unsigned)(bps < 1 ? 1 : (bps > cap ? cap : bps));
+}
+
+template <int DT>
+int legacy_quant_launch(const void *x, int64_t n_slabs, int64_t slab_len, int8_t *q, void *scales, uint32_t *amax,
+                        hipStream_t st) {
+  using V = LegacyVec<DT>;
+  const bool vec = (uintptr_t)x % 16 == 0 && (uintptr_t)q % V::W == 0 &&
+                   (n_slabs == 1 || (slab_len * V::ES) % 16 == 0);
+  const dim3 grid(legacy_blocks_per_slab(n_slabs, slab_len), (unsigned)n_slabs);
+  int rc;
+  if (vec) {
+    legacy_amax_slabs_kernel<DT, true><<<grid, 256, 0, st>>>(x, slab_len, amax);
+    if ((rc = check_launch("legacy_amax"))) return rc;
+    legacy_quant_slabs_kernel<DT, true><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
+  } else {
+    legacy_amax_slabs_kernel<DT, false><<<grid, 256, 0, st>>>(x, slab_len, amax);
+    if ((rc = check_launch("legacy_amax"))) return rc;
+    legacy_quant_slabs_kernel<DT, false><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
+  }
+  return check_launch("legacy_quant");
+}
+
+template <int DT>
+int legacy_dequant_launch(const int8_t *q, const void *scales, int64_t n_slabs, int64_t slab_len, uint16_t *y,
+                          hipStream_t st) {
+  const bool vec = (uintptr_t)q % 8 == 0 && (uintptr_t)y % 16 == 0 && (n_slabs == 1 || slab_len % 8 == 0);
+  const dim3 grid(legacy_blocks_per_slab(n_slabs, slab_len), (unsigned)n_slabs);
+  if (vec)
+    legacy_dequant_slabs_kernel<DT, true><<<grid, 256, 0, st>>>(q, scales, slab_len, y);
+  else
+    legacy_dequant_slabs_kernel<DT, false><<<grid, 256, 0, st>>>(q, scales, slab_len, y);
+  return check_launch("legacy_dequant");
+}
+
+int legacy_quant_any(const void *x, int dtype, int64_t n_slabs, int64_t slab_len, int8_t *q, void *scales,
+                     void *workspace, hipStream_t st, const char *what) {
+  uint32_t *amax = reinterpret_cast<uint32_t *>(workspace);
+  int rc = fill_u32(amax, n_slabs, 0, st);
+  if (rc) return rc;
+  switch (dtype) {
+    case ZX_BF16: return legacy_quant_launch<ZX_BF16>(x, n_slabs, slab_len, q, scales, amax, st);
+    case ZX_F16: return legacy_quant_launch<ZX_F16>(x, n_slabs, slab_len, q, scales, amax, st);
+    case ZX_F32: return legacy_quant_launch<ZX_F32>(x, n_slabs, slab_len, q, scales, amax, st);
+    default: return fail(ZX_ERR_INVALID, "%s: unknown dtype %d", what, dtype);
+  }
+}
+
+int legacy_dequant_any(const int8_t *q, const void *scales, int dtype, int64_t n_slabs, int64_t slab_len, uint16_t *y,
+                       hipStream_t st, const char *what) {
+  switch (dtype) {
+    case ZX_BF16: return legacy_dequant_launch<ZX_BF16>(q, scales, n_slabs, slab_len, y, st);
+    case ZX_F16: return legacy_dequant_launch<ZX_F16>(q, scales, n_slabs, slab_len, y, st);
+    case ZX_F32: return legacy_dequant_launch<ZX_F32>(q, scales, n_slabs, slab_len, y, st);
+    default: return fail(ZX_ERR_INVALID, "%s: unknown dtype %d", what, dtype);
+  }
+}
+}  // namespace
+
 extern "C" int zx_int8_legacy_quant(const void *x, int dtype, int64_t n, int8_t *q, void *scale,
                                     void *workspace, size_t workspace_bytes, zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(x && q && scale, "int8_legacy_quant: null pointer");
   ZX_REQUIRE(n > 0, "int8_legacy_quant: empty tensor (the reference raises on amax of an empty tensor)");
   if (!workspace || workspace_bytes < 256) return fail(ZX_ERR_WORKSPACE, "int8_legacy_quant: workspace < 256 bytes");
-  hipStream_t st = as_stream(stream);
-  uint32_t *amax = reinterpret_cast<uint32_t *>(workspace);
-  int rc = fill_u32(amax, 1, 0, st);
-  if (rc) return rc;
-  unsigned grid = grid_for(n, 8);
-  switch (dtype) {
-    case ZX_BF16:
-      legacy_amax_kernel<ZX_BF16><<<grid, 256, 0, st>>>(x, n, amax);
-      if ((rc = check_launch("legacy_amax"))) return rc;
-      legacy_quant_kernel<ZX_BF16><<<grid, 256, 0, st>>>(x, n, amax, q, scale);
-      break;
-    case ZX_F16:
-      legacy_amax_kernel<ZX_F16><<<grid, 256, 0, st>>>(x, n, amax);
-      if ((rc = check_launch("legacy_amax"))) return rc;
-      legacy_quant_kernel<ZX_F16><<<grid, 256, 0, st>>>(x, n, amax, q, scale);
-      break;
-    case ZX_F32:
-      legacy_amax_kernel<ZX_F32><<<grid, 256, 0, st>>>(x, n, amax);
-      if ((rc = check_launch("legacy_amax"))) return rc;
-      legacy_quant_kernel<ZX_F32><<<grid, 256, 0, st>>>(x, n, amax, q, scale);
-      break;
-    default:
-      return fail(ZX_ERR_INVALID, "int8_legacy_quant: unknown dtype %d", dtype);
-  }
-  return check_launch("legacy_quant");
+  return legacy_quant_any(x, dtype, 1, n, q, scale, workspace, as_stream(stream), "int8_legacy_quant");
 }
 
 extern "C" size_t zx_int8_legacy_quant_slabs_workspace_bytes(int64_t n_slabs) {
@@ -483,34 +560,8 @@ extern "C" int zx_int8_legacy_quant_slabs(const void *x, int dtype, int64_t n_sl
   if (!workspace || workspace_bytes < zx_int8_legacy_quant_slabs_workspace_bytes(n_slabs))
     return fail(ZX_ERR_WORKSPACE, "int8_legacy_quant_slabs: workspace < %zu bytes",
                 zx_int8_legacy_quant_slabs_workspace_bytes(n_slabs));
-  hipStream_t st = as_stream(stream);
-  uint32_t *amax = reinterpret_cast<uint32_t *>(workspace);
-  int rc = fill_u32(amax, n_slabs, 0, st);
-  if (rc) return rc;
-  // blocks per slab: enough for ~16 per CU over all slabs, at least one
-  int64_t bps = ceil_div((int64_t)num_cus() * 16, n_slabs);
-  bps = bps < 1 ? 1 : (bps > ceil_div(slab_len, 256LL * 8) ? ceil_div(slab_len, 256LL * 8) : bps);
-  const dim3 grid((unsigned)bps, (unsigned)n_slabs);
-  switch (dtype) {
-    case ZX_BF16:
-      legacy_amax_slabs_kernel<ZX_BF16><<<grid, 256, 0, st>>>(x, slab_len, amax);
-      if ((rc = check_launch("legacy_amax_slabs"))) return rc;
-      legacy_quant_slabs_kernel<ZX_BF16><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
-      break;
-    case ZX_F16:
-      legacy_amax_slabs_kernel<ZX_F16><<<grid, 256, 0, st>>>(x, slab_len, amax);
-      if ((rc = check_launch("legacy_amax_slabs"))) return rc;
-      legacy_quant_slabs_kernel<ZX_F16><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
-      break;
-    case ZX_F32:
-      legacy_amax_slabs_kernel<ZX_F32><<<grid, 256, 0, st>>>(x, slab_len, amax);
-      if ((rc = check_launch("legacy_amax_slabs"))) return rc;
-      legacy_quant_slabs_kernel<ZX_F32><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
-      break;
-    default:
-      return fail(ZX_ERR_INVALID, "int8_legacy_quant_slabs: unknown dtype %d", dtype);
-  }
-  return check_launch("legacy_quant_slabs");
+  return legacy_quant_any(x, dtype, n_slabs, slab_len, q, scales, workspace, as_stream(stream),
+                          "int8_legacy_quant_slabs");
 }
 
 extern "C" int zx_int8_legacy_dequant_slabs(const int8_t *q, const void *scales, int scale_dtype, int64_t n_slabs,
@@ -519,34 +570,17 @@ extern "C" int zx_int8_legacy_dequant_slabs(const int8_t *q, const void *scales,
   ZX_REQUIRE(q && scales && y, "int8_legacy_dequant_slabs: null pointer");
   ZX_REQUIRE(n_slabs >= 0 && n_slabs <= 65535 && slab_len >= 0, "int8_legacy_dequant_slabs: bad sizes");
   if (n_slabs == 0 || slab_len == 0) return ZX_OK;
-  hipStream_t st = as_stream(stream);
-  int64_t bps = ceil_div((int64_t)num_cus() * 16, n_slabs);
-  bps = bps < 1 ? 1 : (bps > ceil_div(slab_len, 256LL * 8) ? ceil_div(slab_len, 256LL * 8) : bps);
-  const dim3 grid((unsigned)bps, (unsigned)n_slabs);
-  switch (scale_dtype) {
-    case ZX_BF16: legacy_dequant_slabs_kernel<ZX_BF16><<<grid, 256, 0, st>>>(q, scales, slab_len, y); break;
-    case ZX_F16: legacy_dequant_slabs_kernel<ZX_F16><<<grid, 256, 0, st>>>(q, scales, slab_len, y); break;
-    case ZX_F32: legacy_dequant_slabs_kernel<ZX_F32><<<grid, 256, 0, st>>>(q, scales, slab_len, y); break;
-    default: return fail(ZX_ERR_INVALID, "int8_legacy_dequant_slabs: unknown dtype %d", scale_dtype);
-  }
-  return check_launch("legacy_dequant_slabs");
+  return legacy_dequant_any(q, scales, scale_dtype, n_slabs, slab_len, y, as_stream(stream),
+                            "int8_legacy_dequant_slabs");
 }
 
-extern "C" int zx_int8_legacy_dequant(const int8_t *q, const void *scale, int scale_dtype, int64_t n,
-                                      uint16_t *y, zx_stream_t stream) {
+extern "C" int zx_int8_legacy_dequant(const int8_t *q, const void *scale, int scale_dtype, int64_t n, uint16_t *y,
+                                      zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(q && scale && y, "int8_legacy_dequant: null pointer");
   ZX_REQUIRE(n >= 0, "int8_legacy_dequant: negative size");
   if (n == 0) return ZX_OK;
-  hipStream_t st = as_stream(stream);
-  unsigned grid = grid_for(n, 8);
-  switch (scale_dtype) {
-    case ZX_BF16: legacy_dequant_kernel<ZX_BF16><<<grid, 256, 0, st>>>(q, scale, n, y); break;
-    case ZX_F16: legacy_dequant_kernel<ZX_F16><<<grid, 256, 0, st>>>(q, scale, n, y); break;
-    case ZX_F32: legacy_dequant_kernel<ZX_F32><<<grid, 256, 0, st>>>(q, scale, n, y); break;
-    default: return fail(ZX_ERR_INVALID, "int8_legacy_dequant: unknown dtype %d", scale_dtype);
-  }
-  return check_launch("legacy_dequant");
+  return legacy_dequant_any(q, scale, scale_dtype, 1, n, y, as_stream(stream), "int8_legacy_dequant");
 }
 
 extern "C" int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_heads,
