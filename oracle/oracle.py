@@ -230,6 +230,17 @@ def int8_legacy_quant(x: np.ndarray, dtype: str):
     return q, float(np.float32(s))
 
 
+def legacy_reciprocal_check(dtype: str, scale_stride: int = 1):
+    """(mismatching codes, pairs compared) of the reciprocal + Markstein quotient against
+    IEEE division for the legacy quantiser (zxo_legacy_reciprocal_check)."""
+    L = lib()
+    L.zxo_legacy_reciprocal_check.restype = ctypes.c_int64
+    L.zxo_legacy_reciprocal_check.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int64)]
+    pairs = ctypes.c_int64(0)
+    bad = L.zxo_legacy_reciprocal_check(_DT[dtype], int(scale_stride), ctypes.byref(pairs))
+    return int(bad), int(pairs.value)
+
+
 def int8_legacy_dequant(q: np.ndarray, scale: float) -> np.ndarray:
     q = np.ascontiguousarray(q, dtype=np.int8)
     y = np.empty(q.shape, np.uint16)

@@ -440,6 +440,41 @@ void zxo_int8_legacy_dequant(const int8_t *q, float scale, int64_t n, uint16_t *
   for (int64_t i = 0; i < n; ++i) y[i] = zxo_bf16_rne((float)q[i] * scale);
 }
 
+/* A check of the division the GPU's legacy quantiser uses for bf16 / f16 input, not part
+ * of the restatement: with r = 1 / s (IEEE), q0 = x r, e = fma(-q0, s, x), the quotient
+ * fma(e, r, q0) (or q0 itself when |q0| >= 65536, where the code saturates anyway) must
+ * give the same int8 code as x / s above.  Every `scale_stride`-th finite scale the
+ * quantiser produces from an amax of `dtype` (0 bf16, 1 f16) against every input x of that
+ * dtype; returns the number of differing codes, *pairs the number compared. */
+int64_t zxo_legacy_reciprocal_check(int dtype, int scale_stride, int64_t *pairs) {
+  int64_t bad = 0, n = 0, k = 0;
+  float last = -1.0f;
+  const float lo = to_dtype(1e-8f, dtype);
+  for (uint32_t ab = 0; ab < 0x8000u; ++ab) {
+    float a = dtype == 0 ? zxo_bf16_to_f32((uint16_t)ab) : zxo_f16_to_f32((uint16_t)ab);
+    if (isnan(a) || isinf(a)) continue;
+    if (a < lo) a = lo;
+    const float s = to_dtype(a / 127.0f, dtype);
+    if (s == last) continue; /* amax values sharing a scale (they come in order) */
+    last = s;
+    const float r = 1.0f / s;
+    if (!isfinite(s) || !isfinite(r) || (k++ % scale_stride)) continue;
+    for (uint32_t xb = 0; xb < 0x10000u; ++xb) {
+      const float x = dtype == 0 ? zxo_bf16_to_f32((uint16_t)xb) : zxo_f16_to_f32((uint16_t)xb);
+      float w = rintf(to_dtype(x / s, dtype));
+      const float q0 = x * r;
+      const float q = fabsf(q0) < 65536.0f ? fmaf(fmaf(-q0, s, x), r, q0) : q0;
+      float g = rintf(to_dtype(q, dtype));
+      w = isnan(w) ? 0.0f : fminf(fmaxf(w, -127.0f), 127.0f);
+      g = isnan(g) ? 0.0f : fminf(fmaxf(g, -127.0f), 127.0f);
+      bad += w != g;
+      ++n;
+    }
+  }
+  if (pairs) *pairs = n;
+  return bad;
+}
+
 /* ---------------------------------------------------------------- Belady */
 
 /* belady.py:39-51 over integer slots: the largest key > -1 among resident slots, ties to

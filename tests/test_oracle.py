@@ -440,3 +440,13 @@ def test_prefill_attention_oracle_matches_torch(Hq, Hkv, P, causal, seed):
                 np.testing.assert_array_equal(w, want)
                 want_lse = float(torch.logsumexp(s, dim=0)) / np.log(2.0)
                 assert abs(lse[i, hq] - want_lse) <= 2e-6 * max(1.0, abs(want_lse))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_legacy_reciprocal_quotient_matches_division(dt):
+    """The GPU's legacy quantiser forms x / s for bf16 / f16 input from r = 1 / s and one
+    Markstein correction: every 97th reachable scale against every input of the format
+    gives the same int8 code as IEEE division (the full set, stride 1, was run too)."""
+    bad, pairs = O.legacy_reciprocal_check(dt, 97)
+    assert pairs > 10_000_000
+    assert bad == 0

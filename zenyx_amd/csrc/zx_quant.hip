@@ -82,6 +82,7 @@ template <> struct Dt<ZX_F32> {
 // stride through the slab.  VEC: 16-byte lane loads (W = 8 16-bit or 4 fp32 elements;
 // int8 codes stored as W-byte words, bf16 dequant output as 16-byte words), which needs
 // 16-byte aligned slabs; a slab's last n % W elements go element by element.
+constexpr int LEGACY_U = 4;  // vectors per thread per round in the vector loops
 template <int DT> struct LegacyVec {
   static constexpr int W = DT == ZX_F32 ? 4 : 8;
   static constexpr int ES = DT == ZX_F32 ? 4 : 2;
@@ -107,9 +108,21 @@ template <int DT> struct LegacyVec {
   }
 };
 
-template <int DT>
-__device__ __forceinline__ int8_t legacy_code(float xv, float s) {
-  const float v = __builtin_rintf(Dt<DT>::round(xv / s));
+// FAST: the quotient from r = 1 / s and one Markstein correction instead of a division
+// (q0 = x r, e = fma(-q0, s, x), q = fma(e, r, q0); q0 itself when |q0| >= 65536, where the
+// code saturates).  For bf16 / f16 input it gives the same int8 code as IEEE division for
+// every input and every finite scale the quantiser can produce from such an amax: checked
+// exhaustively on the CPU (2,886,336,512 pairs).  fp32 input and non-finite scales divide.
+template <int DT, bool FAST>
+__device__ __forceinline__ int8_t legacy_code(float xv, float s, float r) {
+  float qv;
+  if constexpr (FAST) {
+    const float q0 = xv * r;
+    qv = fabsf(q0) < 65536.0f ? __builtin_fmaf(__builtin_fmaf(-q0, s, xv), r, q0) : q0;
+  } else {
+    qv = xv / s;
+  }
+  const float v = __builtin_rintf(Dt<DT>::round(qv));
   return v != v ? (int8_t)0 : (int8_t)fminf(fmaxf(v, -127.0f), 127.0f);  // NaN -> 0, as torch CPU
 }
 
@@ -123,12 +136,65 @@ __global__ void legacy_amax_slabs_kernel(const void *x, int64_t slab_len, uint32
   if constexpr (VEC) {
     const uint4 *xv = reinterpret_cast<const uint4 *>((const char *)x + base * V::ES);
     const int64_t nv = slab_len / V::W;
-    for (int64_t v = t0; v < nv; v += stride) m = max(m, V::absmax(xv[v]));
+    for (int64_t v0 = t0; v0 < nv; v0 += LEGACY_U * stride) {
+      uint4 xw[LEGACY_U];
+#pragma unroll
+      for (int u = 0; u < LEGACY_U; ++u) {
+        const int64_t v = v0 + u * stride;
+        xw[u] = v < nv ? xv[v] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < LEGACY_U; ++u) m = max(m, V::absmax(xw[u]));
+    }
     done = nv * V::W;
   }
   for (int64_t i = done + t0; i < slab_len; i += stride) m = max(m, Dt<DT>::absbits(x, base + i));
   m = block_max(m);
   if (threadIdx.x == 0) atomicMax(&amax_bits[blockIdx.y], m);
+}
+
+template <int DT, bool VEC, bool FAST>
+__device__ __forceinline__ void legacy_quant_range(const void *x, int64_t base, int64_t slab_len, int8_t *q, float s,
+                                                   float r) {
+  using V = LegacyVec<DT>;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t done = 0;
+  if constexpr (VEC) {
+    const uint4 *xv = reinterpret_cast<const uint4 *>((const char *)x + base * V::ES);
+    const int64_t nv = slab_len / V::W;
+    // LEGACY_U vectors per thread per round, all loaded before any is encoded (loads in
+    // flight); vectors past nv load nothing and store nothing
+    for (int64_t v0 = t0; v0 < nv; v0 += LEGACY_U * stride) {
+      uint4 xw[LEGACY_U];
+#pragma unroll
+      for (int u = 0; u < LEGACY_U; ++u) {
+        const int64_t v = v0 + u * stride;
+        xw[u] = v < nv ? xv[v] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < LEGACY_U; ++u) {
+        const int64_t v = v0 + u * stride;
+        uint32_t c[V::W / 4];
+#pragma unroll
+        for (int k = 0; k < V::W / 4; ++k) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            w |= (uint32_t)(uint8_t)legacy_code<DT, FAST>(V::elem(xw[u], 4 * k + j), s, r) << (8 * j);
+          c[k] = w;
+        }
+        if (v < nv) {
+          if constexpr (V::W == 8)
+            reinterpret_cast<uint2 *>(q + base)[v] = make_uint2(c[0], c[1]);
+          else
+            reinterpret_cast<uint32_t *>(q + base)[v] = c[0];
+        }
+      }
+    }
+    done = nv * V::W;
+  }
+  for (int64_t i = done + t0; i < slab_len; i += stride)
+    q[base + i] = legacy_code<DT, FAST>(Dt<DT>::load(x, base + i), s, r);
 }
 
 template <int DT, bool VEC>
@@ -141,29 +207,11 @@ __global__ void legacy_quant_slabs_kernel(const void *x, int64_t slab_len, const
   if (a < lo) a = lo;
   const float s = Dt<DT>::round(a / 127.0f);
   if (blockIdx.x == 0 && threadIdx.x == 0) Dt<DT>::store((char *)scales + V::ES * (int64_t)blockIdx.y, s);
-  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t done = 0;
-  if constexpr (VEC) {
-    const uint4 *xv = reinterpret_cast<const uint4 *>((const char *)x + base * V::ES);
-    const int64_t nv = slab_len / V::W;
-    for (int64_t v = t0; v < nv; v += stride) {
-      const uint4 xw = xv[v];
-      uint32_t c[V::W / 4];
-#pragma unroll
-      for (int k = 0; k < V::W / 4; ++k) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w |= (uint32_t)(uint8_t)legacy_code<DT>(V::elem(xw, 4 * k + j), s) << (8 * j);
-        c[k] = w;
-      }
-      if constexpr (V::W == 8)
-        reinterpret_cast<uint2 *>(q + base)[v] = make_uint2(c[0], c[1]);
-      else
-        reinterpret_cast<uint32_t *>(q + base)[v] = c[0];
-    }
-    done = nv * V::W;
-  }
-  for (int64_t i = done + t0; i < slab_len; i += stride) q[base + i] = legacy_code<DT>(Dt<DT>::load(x, base + i), s);
+  const float r = 1.0f / s;
+  if (DT != ZX_F32 && __builtin_isfinite(s) && __builtin_isfinite(r))  // uniform per slab
+    legacy_quant_range<DT, VEC, DT != ZX_F32>(x, base, slab_len, q, s, r);
+  else
+    legacy_quant_range<DT, VEC, false>(x, base, slab_len, q, s, r);
 }
 
 template <int DT, bool VEC>
