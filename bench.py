@@ -532,6 +532,30 @@ def configs0_leg(torch, dev, steps, warmup):
                                  "fp8_GBps": gb(cpu[1][0]), "int8_GBps": gb(cpu[1][1])},
                    "kind": "torch ATen on the host, same semantics (median of 5 after a warm-up)"},
            "gpu_equals_cpu": {"fp8_codes_scales_dequant": bool(same), "int8_all_288_slabs": bool(same_i8)}}
+    # the same functions at size: one 1 Gi-element bf16 tensor (2 GiB), per tensor (the
+    # reference's precision.py API) and per head (FP8, 64 x 4 x 8 slabs of 512 K elements)
+    big = torch.randn((64, 4, 8, 1 << 19), device=dev, generator=torch.Generator(device=dev).manual_seed(4))
+    big = big.to(torch.bfloat16)
+    nb = big.numel()
+    q8, s8 = kv.int8_legacy_quant(big)
+    ms_lq, _, _ = time_steps(torch, lambda: kv.int8_legacy_quant(big), steps, warmup)
+    ms_ld, _, _ = time_steps(torch, lambda: kv.int8_legacy_dequant(q8, s8), steps, warmup)
+    del q8
+    c8, sc8 = kv.fp8_quant_heads(big)
+    ms_hq, _, _ = time_steps(torch, lambda: kv.fp8_quant_heads(big), steps, warmup)
+    ms_hd, _, _ = time_steps(torch, lambda: kv.fp8_dequant_heads(c8, sc8), steps, warmup)
+    del c8, big
+    torch.cuda.empty_cache()
+    tb = lambda b_el, ms: round(b_el * nb / (ms * 1e-3) / 1e12, 3)  # noqa: E731
+    res["at_size"] = {
+        "elements": nb, "dtype": "bf16",
+        "int8_legacy_quant": {"ms": round(ms_lq, 4), "TBps_alg": tb(3, ms_lq), "TBps_moved": tb(5, ms_lq)},
+        "int8_legacy_dequant": {"ms": round(ms_ld, 4), "TBps_alg": tb(3, ms_ld)},
+        "fp8_quant_heads": {"ms": round(ms_hq, 4), "TBps_alg": tb(3, ms_hq), "TBps_moved": tb(5, ms_hq)},
+        "fp8_dequant_heads": {"ms": round(ms_hd, 4), "TBps_alg": tb(3, ms_hd)},
+        "note": "quant = amax pass (2 B/el) + quant pass (2 B/el read, 1 written): 5 B/el moved, 3 B/el algorithmic"}
+    log(f"configs[0] functions at 1 Gi elements: int8 quant {ms_lq:.3f} ms, dequant {ms_ld:.3f} ms; fp8 heads quant "
+        f"{ms_hq:.3f} ms, dequant {ms_hd:.3f} ms")
     log(f"configs[0]: GPU fp8 {ms_f:.4f} ms, int8 per slab {ms_i:.4f} ms (loop {ms_il:.3f} ms); CPU {threads} threads fp8 "
         f"{cpu[threads][0]:.3f} s, 1 thread {cpu[1][0]:.3f} s; GPU == CPU: {same}, {same_i8}")
     return res
