@@ -15,8 +15,10 @@ tiers, HBM / pinned DRAM / a file, planned on the GPU and replayed for three win
 and gather GB/s, D2H / H2D GB/s), and configs[0] (the reference's CPU-runnable cache:
 quant + dequant on the GPU and in torch on the host cores).
 
-The CPU baseline is the C oracle (oracle/zx_oracle.c, one thread) timed on a bounded
-sample of the same workload on this machine's host cores.
+The CPU baseline is the oracle's CPU restatement timed on this machine's host cores: for
+the append and the gather its torch form (all of torch's threads, and one thread beside
+it; bit-identical to the C oracle), elsewhere the C oracle; each on a bounded sample of
+the same workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
                     [--only append|gather|ring|belady|tiers|weights|configs4|configs0|copy|all]
@@ -128,56 +130,86 @@ def time_steps(torch, fn, steps, warmup):
     return sum(per) / steps, per, wall
 
 
-def cpu_baseline_append(W, budget_s=20.0):
-    """C oracle (1 thread) on a bounded sample: whole sequences of layer 0 appended until
-    about budget_s of CPU work; GB/s at 3 B per element."""
+def _median_time(fn, reps=5):
+    import statistics
+
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_baseline_append(W, budget_s=8.0):
+    """CPU baseline of the append: the torch restatement (oracle.kv_quant_append_torch,
+    bit-identical to the C oracle) on all of layer 0, with all of torch's threads and with
+    one (median of 5 after a warm-up), plus the scalar C oracle on a bounded sample."""
     import numpy as np
+    import torch
 
     from oracle import oracle as O
 
-    x0 = W["x"][0].cpu().view(__import__("torch").int16).numpy().view(np.uint16)  # [T, 2, H, D]
+    x0 = W["x"][0].cpu()  # [T, 2, H, D] bf16
     lens, P, H, D = W["lens"], W["P"], W["H"], W["D"]
-    cu = W["cu_host"].numpy()
-    bt = W["bt_host"].numpy()
+    cu, bt = W["cu_host"].numpy(), W["bt_host"].numpy()
+    n_layer = x0.numel()
+    threads = torch.get_num_threads()
+    res = {}
+    for nt in (threads, 1):
+        torch.set_num_threads(nt)
+        res[nt] = _median_time(lambda: O.kv_quant_append_torch(x0, cu, bt, W["n_pages"], P))
+    torch.set_num_threads(threads)
+    # the C oracle (scalar, one thread): whole sequences of layer 0 until about budget_s
+    xb = x0.view(torch.int16).numpy().view(np.uint16)
     pool = np.zeros((1, W["n_pages"], 2, H, P, D), np.uint8)
     done_tok, elapsed, b = 0, 0.0, 0
     while b < len(lens) and elapsed < budget_s:
-        xs = np.ascontiguousarray(x0[cu[b]:cu[b + 1]])[None]
-        cub = np.array([0, lens[b]], np.int32)
+        xs = np.ascontiguousarray(xb[cu[b]:cu[b + 1]])[None]
         t0 = time.perf_counter()
-        O.kv_quant_append(xs, cub, None, bt[b:b + 1], pool, P)
+        O.kv_quant_append(xs, np.array([0, lens[b]], np.int32), None, bt[b:b + 1], pool, P)
         elapsed += time.perf_counter() - t0
         done_tok += lens[b]
         b += 1
-    n = done_tok * 2 * H * D
-    return {"value": round(3 * n / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"C oracle zxo_kv_quant_append (scalar, 1 thread) on layer 0, sequences 0..{b - 1} "
-                      f"({done_tok} tokens, {n} elements), dynamic per-head scales; {elapsed:.1f} s"}
+    gb = lambda sec: round(3 * n_layer / sec / 1e9, 4)  # noqa: E731
+    return {"value": gb(res[threads]), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"torch restatement of the append (oracle.kv_quant_append_torch, bit-identical to the C "
+                      f"oracle) on all of layer 0 ({W['T']} tokens, {n_layer} elements), {threads} threads, median "
+                      f"of 5: {res[threads]:.3f} s",
+            "one_thread": {"value": gb(res[1]), "seconds": round(res[1], 3)},
+            "c_oracle_one_thread": {"value": round(3 * done_tok * 2 * H * D / elapsed / 1e9, 4),
+                                    "sample": f"sequences 0..{b - 1} of layer 0, {elapsed:.1f} s"}}
 
 
-def cpu_baseline_gather(W, budget_s=10.0):
-    import numpy as np
+def cpu_baseline_gather(W, n_seq=4):
+    """CPU baseline of the gather: the torch restatement (oracle.kv_gather_dequant_torch)
+    on n_seq whole sequences of the layer with all of torch's threads and on one with a
+    single thread (median of 5 after a warm-up)."""
+    import torch
 
     from oracle import oracle as O
 
-    torch = __import__("torch")
-    H, D, P = W["H"], W["D"], W["P"]
-    bt = W["bt_host"]
-    sc = W["scales_host"][W["layer"]].numpy()
-    elapsed, n, b = 0.0, 0, 0
-    while b < W["B"] and elapsed < budget_s:
-        pages = bt[b]
-        sub = W["pool"][pages.long().to(W["pool"].device)].cpu().numpy()  # the sequence's pages
-        loc = np.arange(len(pages), dtype=np.int32)[None]
-        t0 = time.perf_counter()
-        O.kv_gather_dequant(sub, sc, loc, np.array([W["T"]], np.int32), W["T"])
-        elapsed += time.perf_counter() - t0
-        n += W["T"] * 2 * H * D
-        b += 1
-    del torch
-    return {"value": round(3 * n / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"C oracle zxo_kv_gather_dequant (1 thread), {b} of {W['B']} sequences of one layer; "
-                      f"{elapsed:.1f} s"}
+    H, D, T = W["H"], W["D"], W["T"]
+    bt = W["bt_host"][:n_seq]
+    pages = torch.unique(bt.reshape(-1)).long()
+    remap = torch.full((int(pages.max()) + 1,), -1, dtype=torch.int64)
+    remap[pages] = torch.arange(len(pages))
+    sub = W["pool"][pages.to(W["pool"].device)].cpu()  # only the sampled sequences' pages
+    btl = remap[bt.long()]
+    sc = W["scales_host"][W["layer"]]
+    threads = torch.get_num_threads()
+    t_all = _median_time(lambda: O.kv_gather_dequant_torch(sub, sc, btl, [T] * n_seq, T))
+    torch.set_num_threads(1)
+    t_one = _median_time(lambda: O.kv_gather_dequant_torch(sub, sc, btl[:1], [T], T))
+    torch.set_num_threads(threads)
+    n_all, n_one = n_seq * T * 2 * H * D, T * 2 * H * D
+    return {"value": round(3 * n_all / t_all / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"torch restatement of the gather (oracle.kv_gather_dequant_torch, bit-identical to the C "
+                      f"oracle), {n_seq} of {W['B']} sequences of one layer ({n_all} elements), {threads} threads, "
+                      f"median of 5: {t_all:.3f} s",
+            "one_thread": {"value": round(3 * n_one / t_one / 1e9, 4), "sample": "one sequence", "seconds":
+                           round(t_one, 3)}}
 
 
 def belady_leg(torch, dev, skip_cpu):

@@ -167,6 +167,50 @@ def kv_quant_append(x_bits, cu_seqlens, start_pos, block_tables, pool, page_size
     return sc, int(err)
 
 
+def kv_quant_append_torch(x, cu_seqlens, block_tables, n_pages, page_size):
+    """The paged append of one layer restated in torch on the CPU (the multi-threaded CPU
+    baseline; same results as zxo_kv_quant_append, checked in tests/test_oracle.py):
+    x bf16 [n_tok, 2, H, D] (CPU tensor) -> (scales fp32 [2, H], pool uint8 [n_pages, 2, H, P, D])
+    with scale = max(amax, 1e-8) / 448 per (kv, head) and the e4m3 codes of x / scale at
+    page block_tables[b, pos // P], slot pos % P."""
+    import torch
+
+    n_tok, _, H, D = x.shape
+    cu = torch.as_tensor(np.asarray(cu_seqlens), dtype=torch.int64)
+    lens = cu[1:] - cu[:-1]
+    tok_b = torch.repeat_interleave(torch.arange(len(lens)), lens)
+    pos = torch.arange(n_tok) - cu[:-1][tok_b]
+    bt = torch.as_tensor(np.asarray(block_tables), dtype=torch.int64)
+    page, slot = bt[tok_b, pos // page_size], pos % page_size
+    xf = x.float()
+    sc = xf.abs().amax(dim=(0, 3)).clamp_min(1e-8) / 448.0
+    codes = (xf / sc[None, :, :, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    pool = torch.zeros((n_pages, 2, H, page_size, D), dtype=torch.uint8)
+    pool[page, :, :, slot, :] = codes
+    return sc, pool
+
+
+def kv_gather_dequant_torch(pool_layer, scales_layer, block_tables, seq_lens, out_len):
+    """The paged gather + dequant of one layer restated in torch on the CPU (the
+    multi-threaded CPU baseline; same results as zxo_kv_gather_dequant): -> (k, v) bf16
+    [B, H, out_len, D], zeros past each sequence's length."""
+    import torch
+
+    n_pages, _, H, P, D = pool_layer.shape
+    bt = torch.as_tensor(np.asarray(block_tables), dtype=torch.int64)
+    B = bt.shape[0]
+    k = torch.zeros((B, H, out_len, D), dtype=torch.bfloat16)
+    v = torch.zeros((B, H, out_len, D), dtype=torch.bfloat16)
+    for b in range(B):
+        n = min(int(seq_lens[b]), out_len)
+        t = torch.arange(n)
+        codes = pool_layer[bt[b, t // P], :, :, t % P, :]  # [n, 2, H, D]
+        vals = (codes.view(torch.float8_e4m3fn).float() * scales_layer[None, :, :, None]).to(torch.bfloat16)
+        k[b, :, :n] = vals[:, 0].transpose(0, 1)
+        v[b, :, :n] = vals[:, 1].transpose(0, 1)
+    return k, v
+
+
 def kv_gather_dequant(pool_layer, scales_layer, block_tables, seq_lens, out_len):
     """pool_layer [n_pages, 2, H, P, D] -> (k, v) bf16 bits [B, H, out_len, D], err."""
     pool_layer = np.ascontiguousarray(pool_layer, dtype=np.uint8)

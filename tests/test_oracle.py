@@ -450,3 +450,34 @@ def test_legacy_reciprocal_quotient_matches_division(dt):
     bad, pairs = O.legacy_reciprocal_check(dt, 97)
     assert pairs > 10_000_000
     assert bad == 0
+
+
+def test_torch_restatements_of_append_and_gather_match_c():
+    """The torch CPU restatements bench.py times as the multi-threaded CPU baseline give
+    the C oracle's scales, pool bytes and gathered values bit for bit."""
+    g = torch.Generator().manual_seed(12)
+    H, D, P = 4, 128, 16
+    lens = [37, 16, 100]
+    nb = [(n + P - 1) // P for n in lens]
+    n_pages = sum(nb) + 3
+    perm = torch.randperm(n_pages, generator=g).numpy().astype(np.int32)
+    bt = np.full((3, max(nb)), -1, np.int32)
+    k = 0
+    for b in range(3):
+        bt[b, :nb[b]] = perm[k:k + nb[b]]
+        k += nb[b]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    x = (torch.randn((sum(lens), 2, H, D), generator=g) * 3).to(torch.bfloat16)
+    x[5, 1, 2] *= 40
+    sc, pool = O.kv_quant_append_torch(x, cu, bt, n_pages, P)
+    wpool = np.zeros((1, n_pages, 2, H, P, D), np.uint8)
+    wsc, err = O.kv_quant_append(x.view(torch.int16).numpy().view(np.uint16)[None], cu, None, bt, wpool, P)
+    assert err == 0
+    np.testing.assert_array_equal(sc.numpy().view(np.uint32), wsc[0].view(np.uint32))
+    np.testing.assert_array_equal(pool.numpy(), wpool[0])
+    out_len = max(nb) * P
+    kt, vt = O.kv_gather_dequant_torch(pool, sc, bt, lens, out_len)
+    wk, wv, gerr = O.kv_gather_dequant(wpool[0], wsc[0], bt, np.array(lens, np.int32), out_len)
+    assert gerr == 0
+    np.testing.assert_array_equal(kt.view(torch.int16).numpy().view(np.uint16), wk)
+    np.testing.assert_array_equal(vt.view(torch.int16).numpy().view(np.uint16), wv)
