@@ -3,10 +3,11 @@ and the weight streaming that shares its transfer engine.
 
 Kept names: ``quantize_to_fp8_storage``, ``dequantize_for_bf16_compute``,
 ``BeladyApproxCache``, ``KVTierManager``, ``KVBlockRef``, ``build_ring_timeline``,
-``ParameterStore``, ``LayerWeightStreamer``, ``LayerBlock``, and the caller that drives
-them, ``StreamingExecutionEngine`` / ``StreamingConfig``.  The reference's bandwidth
-throttle is not part of this path and is not provided.
+``ParameterStore``, ``LayerWeightStreamer``, ``LayerBlock``, the caller that drives
+them, ``StreamingExecutionEngine`` / ``StreamingConfig``, and the throttle rule
+``BandwidthAwareScheduler`` / ``BandwidthSample`` (host logic).
 """
+from .bandwidth import BandwidthAwareScheduler, BandwidthSample
 from .belady import AccessEvent, BeladyApproxCache
 from .engine import StreamingConfig, StreamingExecutionEngine
 from .kv_tiering import KVBlockRef, KVTierManager, build_ring_timeline
@@ -15,6 +16,8 @@ from .precision import dequantize_for_bf16_compute, quantize_to_fp8_storage
 
 __all__ = [
     "AccessEvent",
+    "BandwidthAwareScheduler",
+    "BandwidthSample",
     "BeladyApproxCache",
     "KVBlockRef",
     "KVTierManager",

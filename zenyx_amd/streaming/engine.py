@@ -14,10 +14,10 @@ keep the reference's call order, which is what this path has to reproduce:
   each block found in T2 is prefetched to T0 and evicted again (engine.py:96-101).
 
 The layers compute with their own parameters, as in the reference (the streamed copy
-is fetched but not bound into the module).  The reference's bandwidth throttle
-(bandwidth.py, a host sleep when a fetch takes longer than the layer's compute) is
-left out: ``get`` here never blocks the host, so its fetch time is ~0 and the throttle
-would never sleep.
+is fetched but not bound into the module).  The engine holds the reference's
+``BandwidthAwareScheduler`` as ``bandwidth`` (engine.py:46) but does not sleep on it (the
+host sleep of engine.py:79-85): ``get`` here never blocks the host, so its fetch time is
+~0 and the rule would never ask for a delay.
 """
 from __future__ import annotations
 
@@ -27,6 +27,7 @@ from typing import Callable
 import torch
 import torch.nn as nn
 
+from .bandwidth import BandwidthAwareScheduler
 from .belady import BeladyApproxCache
 from .kv_tiering import KVTierManager, build_ring_timeline
 from .parameter_streamer import LayerWeightStreamer, ParameterStore
@@ -60,6 +61,7 @@ class StreamingExecutionEngine:
                                                    max_resident_layers=self.config.max_hbm_layers)
         self.kv_manager = KVTierManager(t0_capacity=self.config.kv_t0_blocks, t1_capacity=self.config.kv_t1_blocks)
         self.cache = BeladyApproxCache(capacity=self.config.max_hbm_layers)
+        self.bandwidth = BandwidthAwareScheduler(max_fetch_to_compute_ratio=1.0)
 
     def run_forward_backward(self, x: torch.Tensor, target: torch.Tensor,
                              loss_fn: Callable[[torch.Tensor, torch.Tensor], torch.Tensor]) -> float:
