@@ -334,15 +334,17 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
                             kv_end: torch.Tensor, causal: bool = True, sm_scale: float | None = None,
                             o_acc: torch.Tensor | None = None, lse2: torch.Tensor | None = None,
                             first: bool = True, out: torch.Tensor | None = None, write_bf16: bool = True,
-                            max_q_per_seq: int | None = None, check: bool = False):
+                            max_q_per_seq: int | None = None, check: bool = False,
+                            err: torch.Tensor | None = None):
     """One ring step of attention over the FP8 pages (zx_paged_attention_prefill).
 
     ``q`` [n_q, Hq, 128] bf16 rows of all sequences (``cu_q`` [B+1] int32 offsets,
     ``q_pos0`` [B] int32 position of each sequence's first query row); keys
     [kv_begin[b], kv_end[b]) of the pool layer through the block tables.  With ``o_acc``
     / ``lse2`` (fp32 [n_q, Hq, 128] / [n_q, Hq]) the step merges into them (``first``
-    overwrites); with ``write_bf16`` the (merged) rows go to ``out`` as bf16.  Returns
-    ``out`` (or None)."""
+    overwrites); with ``write_bf16`` the (merged) rows go to ``out`` as bf16.  ``err`` (int32
+    [1], zeroed by the caller) collects the kernel's input-error bits across several calls;
+    by default each call uses a fresh one.  Returns ``out`` (or None)."""
     N.require_device(q, "q")
     if q.dtype != torch.bfloat16 or q.dim() != 3:
         raise ValueError("q must be [n_q, n_q_heads, head_dim] bfloat16")
@@ -385,7 +387,10 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
                                                                 else 0) | (N.ZX_PREFILL_BF16 if write_bf16 else 0)
     sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
     dev = q.device
-    err = _err_word(dev)
+    if err is None:
+        err = _err_word(dev)
+    elif err.dtype != torch.int32 or err.numel() < 1 or err.device != dev:
+        raise ValueError("err must be an int32 tensor on q's device")
     N.check(N.load().zx_paged_attention_prefill(
         N.ptr(q), n_q, N.ptr(cu_q), N.ptr(q_pos0), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer),
         N.ptr(block_tables), block_tables.shape[1], N.ptr(kv_begin), N.ptr(kv_end), B, int(max_q_per_seq),
@@ -411,14 +416,22 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     o_acc = torch.empty((n_q, Hq, D), dtype=torch.float32, device=q.device)
     lse2 = torch.empty((n_q, Hq), dtype=torch.float32, device=q.device)
     out = torch.empty_like(q)
-    kl = kv_len.to(torch.int64)
     mq = int((cu_q[1:] - cu_q[:-1]).max().item()) if cu_q.numel() > 1 else 0
+    # Shard r covers keys [kv_len * r // R, kv_len * (r + 1) // R): all bounds in one go,
+    # so the loop below only launches the ring steps (rows padded to 16 bytes, the
+    # alignment every pointer of the C ABI needs).
+    B = kv_len.numel()
+    steps = torch.arange(ring_degree + 1, dtype=torch.int64, device=kv_len.device)
+    bounds = torch.empty((ring_degree + 1, (B + 3) // 4 * 4), dtype=torch.int32, device=kv_len.device)
+    bounds[:, :B] = kv_len.to(torch.int64)[None, :] * steps[:, None] // ring_degree
+    err = _err_word(q.device)
     for r in range(ring_degree):
-        kb = (kl * r // ring_degree).to(torch.int32)
-        ke = (kl * (r + 1) // ring_degree).to(torch.int32)
-        paged_attention_prefill(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables, kb, ke, causal=causal,
-                                sm_scale=sm_scale, o_acc=o_acc, lse2=lse2, first=r == 0, out=out,
-                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, check=check)
+        paged_attention_prefill(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables, bounds[r, :B],
+                                bounds[r + 1, :B],
+                                causal=causal, sm_scale=sm_scale, o_acc=o_acc, lse2=lse2, first=r == 0, out=out,
+                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, err=err)
+    if check:
+        _raise_kernel_error(err, "ring_attention_fp8")
     return out
 
 
