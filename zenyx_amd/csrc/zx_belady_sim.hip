@@ -10,7 +10,7 @@
 // i.e. the lowest set bit.  Per-4096-bit block counts (kept in LDS) find the first E set
 // bits quickly.
 //
-// Windows.  One persistent workgroup walks the trace in windows [t0, t1) of up to 2048
+// Windows.  One persistent workgroup walks the trace in windows [t0, t1) of up to 8192
 // accesses.  Inside a window:
 //   * an access that is not the page's first in the window is a hit, and a page's first
 //     access misses iff the page is not resident -- provided at least E resident pages
@@ -193,6 +193,64 @@ __device__ void select_first(const SimArgs &a, SimShared &sh, int E) {
   __syncthreads();
 }
 
+// v[j] = src[j] for j < n_valid, fill beyond.  A thread's trace positions are contiguous,
+// so a whole run is read as 16-byte loads (4-byte aligned: window starts are arbitrary
+// positions); only the thread that holds the window's end takes the element path.
+typedef int32_t bs_i4 __attribute__((ext_vector_type(4)));
+typedef bs_i4 bs_i4_a4 __attribute__((aligned(4)));
+template <int N>
+__device__ __forceinline__ void load_run(const int32_t *src, int n_valid, int32_t fill, int32_t (&v)[N]) {
+  static_assert(N % 4 == 0, "runs are read 4 elements at a time");
+  if (n_valid >= N) {
+#pragma unroll
+    for (int k = 0; k < N / 4; ++k) {
+      const bs_i4 x = *reinterpret_cast<const bs_i4_a4 *>(src + 4 * k);
+      v[4 * k] = x.x;
+      v[4 * k + 1] = x.y;
+      v[4 * k + 2] = x.z;
+      v[4 * k + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = j < n_valid ? src[j] : fill;
+  }
+}
+
+// cnt[b] += c for every lane of the wave (c == 0: nothing), one LDS atomic per distinct
+// block: a window's bits fall into a few blocks, and same-address LDS atomics from many
+// lanes would serialise.  Called by every lane of the wave.
+__device__ __forceinline__ void wave_cnt_add(uint32_t *cnt, int32_t b, int32_t c) {
+  unsigned long long pend = __ballot(c != 0);
+  while (pend) {
+    const int leader = __ffsll((long long)pend) - 1;
+    const int32_t b0 = __shfl(b, leader, 64);
+    const bool mine = c != 0 && b == b0;
+    int32_t v = mine ? c : 0;
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63) == leader) atomicAdd(&cnt[b0], (uint32_t)v);
+    pend &= ~__ballot(mine);
+    if (mine) c = 0;
+  }
+}
+
+// Segmented OR over the lanes of a wave that hold the same word wd (wd < 0: nothing).
+// Returns true on the lane that issues the word's atomic, with m = the OR of its run.
+// A thread's items are consecutive trace positions whose bits are mostly consecutive
+// too, so neighbouring lanes share words; one atomic per run instead of one per lane
+// keeps same-address atomics (serialised in the cache) off the window's critical path.
+// Runs are contiguous lanes in the usual case; equal words in separate runs just give
+// one atomic per run (OR is idempotent, no bit is lost).  Called by every lane.
+__device__ __forceinline__ bool wave_word_or(int64_t wd, unsigned long long &m) {
+  const int lane = threadIdx.x & 63;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t ow = __shfl_down(wd, off, 64);
+    const unsigned long long om = __shfl_down(m, off, 64);
+    if (lane + off < 64 && ow == wd) m |= om;
+  }
+  const int64_t pw = __shfl_up(wd, 1, 64);
+  return wd >= 0 && (lane == 0 || pw != wd);
+}
+
 // Makes this wave's global stores and atomics complete, then joins the workgroup, so
 // later reads by any wave of the workgroup observe them.
 __device__ __forceinline__ void sync_global() {
@@ -222,21 +280,14 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
       sh.win_clr[q - wlo] = 0;
     }
     // thread-major items: thread tid owns window offsets [tid * BS_IPT, (tid + 1) * BS_IPT)
-    int32_t p[BS_IPT], nu[BS_IPT];
+    int32_t p[BS_IPT], nu[BS_IPT], pu[BS_IPT];
     bool first[BS_IPT];
     const int i0 = threadIdx.x * BS_IPT;
+    load_run<BS_IPT>(a.trace + t0 + i0, w - i0, 0, p);
+    load_run<BS_IPT>(a.next_use + t0 + i0, w - i0, ZX_NEVER, nu);
+    load_run<BS_IPT>(a.prev_use + t0 + i0, w - i0, 0, pu);
 #pragma unroll
-    for (int j = 0; j < BS_IPT; ++j) {
-      const int i = i0 + j;
-      p[j] = 0;
-      nu[j] = ZX_NEVER;
-      first[j] = false;
-      if (i < w) {
-        p[j] = a.trace[t0 + i];
-        nu[j] = a.next_use[t0 + i];
-        first[j] = a.prev_use[t0 + i] < t0;
-      }
-    }
+    for (int j = 0; j < BS_IPT; ++j) first[j] = i0 + j < w && pu[j] < t0;
     __syncthreads();
     uint32_t missm = 0, hitm = 0, lastm = 0;  // bit j: item j
     int mc = 0, hc = 0;
@@ -388,18 +439,38 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
     }
     w_lim = w_lim < BS_W ? w_lim * 2 : BS_W;
     // admissions, and hits on pages resident since before the window (their bits are
-    // cleared in the LDS copy first, then one atomic per word)
+    // cleared in the LDS copy first, then one atomic per word).  A thread's hits have
+    // consecutive bits, so its LDS updates go out once per word, and its first block's
+    // count goes through the wave-level sum (later blocks, rare, directly).
+    {
+      int64_t cw = -1;
+      int32_t cb = -1, cc = 0;
+      unsigned long long cm = 0;
 #pragma unroll
-    for (int j = 0; j < BS_IPT; ++j) {
-      const int i = i0 + j;
-      if (i >= w) continue;
-      if ((missm >> j) & 1) a.resident[p[j]] = 1;
-      if ((hitm >> j) & 1) {
-        const int64_t idx = top - (t0 + i);
-        atomicOr(&sh.win_clr[(idx >> 6) - wlo], 1ull << (idx & 63));
-        atomicSub(&sh.cnt[idx / BS_BLOCK_BITS], 1u);
+      for (int j = 0; j < BS_IPT; ++j) {
+        const int i = i0 + j;
+        if (i >= w) continue;
+        if ((missm >> j) & 1) a.resident[p[j]] = 1;
+        if ((hitm >> j) & 1) {
+          const int64_t idx = top - (t0 + i);
+          if ((idx >> 6) != cw) {
+            if (cw >= 0) atomicOr(&sh.win_clr[cw - wlo], cm);
+            cw = idx >> 6;
+            cm = 0;
+          }
+          cm |= 1ull << (idx & 63);
+          const int32_t b = (int32_t)(idx / BS_BLOCK_BITS);
+          if (cc == 0 || b == cb) {
+            cb = b;
+            ++cc;
+          } else {
+            atomicSub(&sh.cnt[b], 1u);
+          }
+        }
+        if (a.miss_flags) a.miss_flags[t0 + i] = (missm >> j) & 1;
       }
-      if (a.miss_flags) a.miss_flags[t0 + i] = (missm >> j) & 1;
+      if (wave_word_or(cw, cm)) atomicOr(&sh.win_clr[cw - wlo], cm);
+      wave_cnt_add(sh.cnt, cb, -cc);
     }
     __syncthreads();
     for (int64_t q = wlo + threadIdx.x; q <= whi; q += BS_THREADS) {
@@ -434,12 +505,27 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
         if (lane == 0 && removed) atomicSub(&sh.cnt[b], (uint32_t)removed);
       }
     }
-    sync_global();
+    // The bulk clear above must land before the new keys are set (it clears every bit up
+    // to the last static victim).  Without evictions the two phases touch disjoint bits
+    // (hits clear bits of this window's positions, new keys lie beyond it), whose atomics
+    // commute, so the workgroup only joins; the end of the window waits for everything.
+    if (E > 0) sync_global();
+    else __syncthreads();
     // pages still resident after their last access in the window get their new key; a
     // thread's consecutive items often share a word, so their bits go out together
     {
       int64_t cur_w = -1;
       unsigned long long cur_m = 0;
+      int32_t kb = -1, kc = 0;  // first block's count, summed over the wave at the end
+      auto add_cnt = [&](int64_t word, int32_t n) {
+        const int32_t b = (int32_t)((word * 64) / BS_BLOCK_BITS);
+        if (kc == 0 || b == kb) {
+          kb = b;
+          kc += n;
+        } else {
+          atomicAdd(&sh.cnt[b], (uint32_t)n);
+        }
+      };
 #pragma unroll
       for (int j = 0; j < BS_IPT; ++j) {
         if (!((lastm >> j) & 1) || ((takenm >> j) & 1)) continue;
@@ -448,17 +534,16 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
         if ((idx >> 6) != cur_w) {
           if (cur_w >= 0) {
             atomicOr(&a.bits[cur_w], cur_m);
-            atomicAdd(&sh.cnt[(cur_w * 64) / BS_BLOCK_BITS], (uint32_t)__popcll(cur_m));
+            add_cnt(cur_w, __popcll(cur_m));
           }
           cur_w = idx >> 6;
           cur_m = 0;
         }
         cur_m |= 1ull << (idx & 63);
       }
-      if (cur_w >= 0) {
-        atomicOr(&a.bits[cur_w], cur_m);
-        atomicAdd(&sh.cnt[(cur_w * 64) / BS_BLOCK_BITS], (uint32_t)__popcll(cur_m));
-      }
+      if (cur_w >= 0) add_cnt(cur_w, __popcll(cur_m));
+      if (wave_word_or(cur_w, cur_m)) atomicOr(&a.bits[cur_w], cur_m);
+      wave_cnt_add(sh.cnt, kb, kc);
     }
     if (threadIdx.x == 0) {
       st[0] = count0 + M - E;
