@@ -74,14 +74,16 @@ __device__ __forceinline__ int block_scan(int v, int *total, int *ws /* [BS_THRE
   }
   if (lane == 63) ws[wid] = x;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int i = 0; i < BS_THREADS / 64; ++i) {
-      const int t = ws[i];
-      ws[i] = acc;
-      acc += t;
+  if (wid == 0) {  // exclusive scan of the wave totals by the first wave
+    constexpr int NW = BS_THREADS / 64;
+    const int t = lane < NW ? ws[lane] : 0;
+    int u = t;
+    for (int off = 1; off < NW; off <<= 1) {
+      const int y = __shfl_up(u, off, 64);
+      if (lane >= off) u += y;
     }
-    ws[BS_THREADS / 64] = acc;
+    if (lane < NW) ws[lane] = u - t;
+    if (lane == NW - 1) ws[NW] = u;
   }
   __syncthreads();
   const int r = ws[wid] + x - v;
@@ -477,40 +479,44 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
       const unsigned long long c = sh.win_clr[q - wlo];
       if (c) atomicAnd(&a.bits[q], ~c);
     }
-    // evictions: records, residency, and the static victims' bits -- those are exactly
-    // the first sp set bits of B, so every word up to the last one is cleared with a
-    // single atomic
+
+    // Without evictions there are no records and no bulk clear, and the hit clears above
+    // touch bits disjoint from the new keys (this window's positions against positions
+    // beyond it; atomics on disjoint bits commute): go straight to the new keys, the end
+    // of the window waits for everything.
     const int64_t ev0 = st[1];
-    const int sp = E - (E > 0 ? sh.n_dyn_victims : 0);
-    for (int k = threadIdx.x; k < E; k += BS_THREADS) {
-      const int32_t page = sh.ev_vpage[k];
-      a.resident[page] = 0;
-      if (ev0 + k < a.evict_cap) {
-        a.evict_pos[ev0 + k] = (int32_t)(t0 + sh.ev_t[k]);
-        a.evict_page[ev0 + k] = page;
+    if (E > 0) {
+      // evictions: records, residency, and the static victims' bits -- those are exactly
+      // the first sp set bits of B, so every word up to the last one is cleared with a
+      // single atomic
+      const int sp = E - sh.n_dyn_victims;
+      for (int k = threadIdx.x; k < E; k += BS_THREADS) {
+        const int32_t page = sh.ev_vpage[k];
+        a.resident[page] = 0;
+        if (ev0 + k < a.evict_cap) {
+          a.evict_pos[ev0 + k] = (int32_t)(t0 + sh.ev_t[k]);
+          a.evict_page[ev0 + k] = page;
+        }
       }
-    }
-    if (sp > 0) {
-      const int64_t bound = sh.s_idx[sp - 1];
-      for (int li = wid; li < sh.n_list; li += BS_THREADS / 64) {
-        if (sh.blk_before[li] >= sp) continue;
-        const int b = sh.blk_list[li];
-        const int64_t q = (int64_t)b * (BS_BLOCK_BITS / 64) + lane;
-        const int64_t lo = q * 64;
-        unsigned long long mask = 0;
-        if (lo <= bound && lo < a.nbits) mask = lo + 63 <= bound ? ~0ull : ((2ull << (bound - lo)) - 1);
-        int removed = 0;
-        if (mask) removed = __popcll(atomicAnd(&a.bits[q], ~mask) & mask);
-        for (int off = 32; off >= 1; off >>= 1) removed += __shfl_xor(removed, off, 64);
-        if (lane == 0 && removed) atomicSub(&sh.cnt[b], (uint32_t)removed);
+      if (sp > 0) {
+        const int64_t bound = sh.s_idx[sp - 1];
+        for (int li = wid; li < sh.n_list; li += BS_THREADS / 64) {
+          if (sh.blk_before[li] >= sp) continue;
+          const int b = sh.blk_list[li];
+          const int64_t q = (int64_t)b * (BS_BLOCK_BITS / 64) + lane;
+          const int64_t lo = q * 64;
+          unsigned long long mask = 0;
+          if (lo <= bound && lo < a.nbits) mask = lo + 63 <= bound ? ~0ull : ((2ull << (bound - lo)) - 1);
+          int removed = 0;
+          if (mask) removed = __popcll(atomicAnd(&a.bits[q], ~mask) & mask);
+          for (int off = 32; off >= 1; off >>= 1) removed += __shfl_xor(removed, off, 64);
+          if (lane == 0 && removed) atomicSub(&sh.cnt[b], (uint32_t)removed);
+        }
       }
+      // The bulk clear above must land before the new keys are set (it clears every bit up
+      // to the last static victim).
+      sync_global();
     }
-    // The bulk clear above must land before the new keys are set (it clears every bit up
-    // to the last static victim).  Without evictions the two phases touch disjoint bits
-    // (hits clear bits of this window's positions, new keys lie beyond it), whose atomics
-    // commute, so the workgroup only joins; the end of the window waits for everything.
-    if (E > 0) sync_global();
-    else __syncthreads();
     // pages still resident after their last access in the window get their new key; a
     // thread's consecutive items often share a word, so their bits go out together
     {
