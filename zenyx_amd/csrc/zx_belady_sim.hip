@@ -439,7 +439,10 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
           ++rr;
         }
     }
-    w_lim = w_lim < BS_W ? w_lim * 2 : BS_W;
+    // Grow the window again only if this one left room for twice its evictions: in a
+    // stretch where every access misses, a doubled window would exceed BS_EMAX evictions
+    // and be retried at this size anyway.
+    if (2 * E <= BS_EMAX) w_lim = w_lim < BS_W ? w_lim * 2 : BS_W;
     // admissions, and hits on pages resident since before the window (their bits are
     // cleared in the LDS copy first, then one atomic per word).  A thread's hits have
     // consecutive bits, so its LDS updates go out once per word, and its first block's
