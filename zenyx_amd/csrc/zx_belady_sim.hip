@@ -321,6 +321,80 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
       continue;
     }
 
+    if (E == 0) {
+      // No eviction: admissions, hit clears, miss flags and new keys are independent of
+      // one another (hits clear the bits of this window's positions, new keys lie beyond
+      // it; atomics on disjoint bits commute), so they go out in one pass and the window
+      // waits for memory once.
+      int64_t hw = -1, kw = -1;
+      unsigned long long hm = 0, km = 0;
+      int32_t hb = -1, hc = 0, kb = -1, kc = 0;
+#pragma unroll
+      for (int j = 0; j < BS_IPT; ++j) {
+        const int i = i0 + j;
+        if (i >= w) continue;
+        if ((missm >> j) & 1) a.resident[p[j]] = 1;
+        if ((hitm >> j) & 1) {
+          const int64_t idx = top - (t0 + i);
+          if ((idx >> 6) != hw) {
+            if (hw >= 0) atomicAnd(&a.bits[hw], ~hm);
+            hw = idx >> 6;
+            hm = 0;
+          }
+          hm |= 1ull << (idx & 63);
+          const int32_t b = (int32_t)(idx / BS_BLOCK_BITS);
+          if (hc == 0 || b == hb) {
+            hb = b;
+            ++hc;
+          } else {
+            atomicSub(&sh.cnt[b], 1u);
+          }
+        }
+        if (a.miss_flags) a.miss_flags[t0 + i] = (missm >> j) & 1;
+        if ((lastm >> j) & 1) {
+          const int64_t idx = item_idx(a, p[j], nu[j]);
+          a.key[p[j]] = nu[j];
+          if ((idx >> 6) != kw) {
+            if (kw >= 0) {
+              atomicOr(&a.bits[kw], km);
+              const int32_t b = (int32_t)((kw * 64) / BS_BLOCK_BITS);
+              if (kc == 0 || b == kb) {
+                kb = b;
+                kc += __popcll(km);
+              } else {
+                atomicAdd(&sh.cnt[b], (uint32_t)__popcll(km));
+              }
+            }
+            kw = idx >> 6;
+            km = 0;
+          }
+          km |= 1ull << (idx & 63);
+        }
+      }
+      if (kw >= 0) {
+        const int32_t b = (int32_t)((kw * 64) / BS_BLOCK_BITS);
+        if (kc == 0 || b == kb) {
+          kb = b;
+          kc += __popcll(km);
+        } else {
+          atomicAdd(&sh.cnt[b], (uint32_t)__popcll(km));
+        }
+      }
+      if (wave_word_or(hw, hm)) atomicAnd(&a.bits[hw], ~hm);
+      if (wave_word_or(kw, km)) atomicOr(&a.bits[kw], km);
+      wave_cnt_add(sh.cnt, hb, -hc);
+      wave_cnt_add(sh.cnt, kb, kc);
+      if (threadIdx.x == 0) {
+        st[0] = count0 + M;
+        st[2] += M;
+        st[3] += w - M;
+      }
+      w_lim = w_lim < BS_W ? w_lim * 2 : BS_W;
+      sync_global();
+      t0 = t1;
+      continue;
+    }
+
     uint32_t takenm = 0;  // bit j: item j's dynamic candidate was evicted
     int dbase = 0;
     if (E > 0) {
