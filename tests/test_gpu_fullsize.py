@@ -11,6 +11,9 @@
   oracle within the stated tolerance (one bf16 ulp plus 2^-17 max|V|).
 * ring attention at bench.py's ring workload (4 x 8,192 causal): sampled rows against the
   oracle at ring degree 1 and 8, and ring 8 against ring 1 on every output.
+* configs[3] (1M tokens, 80 layers, ring 8, 64 GB budget: 20,971,520 accesses): the whole
+  Belady schedule of the GPU simulator -- every eviction's position and page, and the
+  miss flags of every access -- against the C heap oracle.
 """
 import numpy as np
 import pytest
@@ -143,3 +146,19 @@ def test_ring_attention_bench_shape(dev):
         bad = np.abs(a - c) > tol
         assert not bad.any(), f"sequence {b}: {bad.sum()} elements of ring 8 differ from ring 1 beyond tolerance"
     print("ring 8 == ring 1 within tolerance on all 33.5 M outputs", flush=True)
+
+
+def test_configs3_full_belady_schedule(dev):
+    from zenyx_amd.train.belayd_kv_cache_tiering import BeladyKVCacheTieringManager
+
+    m = BeladyKVCacheTieringManager(num_devices=8, context_length=2**20, num_layers=80, num_kv_heads=8,
+                                    head_dim=128, page_tokens=64, hbm_budget_bytes=64e9, device=dev)
+    print(f"configs[3]: {len(m.sequence)} accesses, {m.n_pages} pages, capacity {m.capacity}", flush=True)
+    stats = m.plan()
+    trace = m.sequence.trace("cpu").numpy()
+    pos, page, st, miss = O.belady_simulate(trace, m.n_pages, m.capacity, miss_flags=True)
+    assert {k: stats[k] for k in ("evictions", "misses", "hits", "resident")} == st
+    gpos, gpage = m.sim.evictions()
+    np.testing.assert_array_equal(gpos.numpy(), pos)
+    np.testing.assert_array_equal(gpage.numpy(), page)
+    np.testing.assert_array_equal(m.sim.miss_flags.cpu().numpy(), miss)
