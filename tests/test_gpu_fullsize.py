@@ -14,6 +14,9 @@
 * configs[3] (1M tokens, 80 layers, ring 8, 64 GB budget: 20,971,520 accesses): the whole
   Belady schedule of the GPU simulator -- every eviction's position and page, and the
   miss flags of every access -- against the C heap oracle.
+* the ring curriculum of bench.py (ring 2 / 256k, 4 / 512k, 8 / 1M tokens, 80 layers:
+  27,525,120 accesses): the GPU-built page trace against the oracle's, and the whole
+  Belady schedule over it against the C heap oracle.
 """
 import numpy as np
 import pytest
@@ -162,3 +165,24 @@ def test_configs3_full_belady_schedule(dev):
     np.testing.assert_array_equal(gpos.numpy(), pos)
     np.testing.assert_array_equal(gpage.numpy(), page)
     np.testing.assert_array_equal(m.sim.miss_flags.cpu().numpy(), miss)
+
+
+def test_curriculum_full_trace_and_schedule(dev):
+    from zenyx_amd.train.dynamic_ring_curriculum import CurriculumPhase, RingDegreeScheduler
+
+    L, pt, page_bytes = 80, 64, 64 * 8 * 128 * 2
+    s = RingDegreeScheduler([CurriculumPhase("ring2", 2, 1 << 18, 1), CurriculumPhase("ring4", 4, 1 << 19, 1),
+                             CurriculumPhase("ring8", 8, 1 << 20)], num_devices=8)
+    n_pages, cap = L * s.layer_stride(pt), int(64e9 // page_bytes)
+    trace = s.access_trace([0, 1, 2], L, page_tokens=pt, device=dev)
+    want = O.ring_curriculum_trace([2, 4, 8], [4096, 8192, 16384], L, s.layer_stride(pt))
+    print(f"curriculum: {want.size} accesses, {n_pages} pages, capacity {cap}", flush=True)
+    np.testing.assert_array_equal(trace.cpu().numpy(), want)
+    sim = kv.BeladyTraceSim(trace, n_pages, cap, record_misses=True)
+    sim.run()
+    pos, page, st, miss = O.belady_simulate(want, n_pages, cap, miss_flags=True)
+    assert sim.stats() == st
+    gpos, gpage = sim.evictions()
+    np.testing.assert_array_equal(gpos.numpy(), pos)
+    np.testing.assert_array_equal(gpage.numpy(), page)
+    np.testing.assert_array_equal(sim.miss_flags.cpu().numpy(), miss)
