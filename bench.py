@@ -255,6 +255,7 @@ def belady_leg(torch, dev, skip_cpu):
                          "wall_ms": round(r["wall_ms"], 3)}
     log(f"tier moves: {r['d2h_pages']} D2H pages at {r['d2h_GBps']:.1f} GB/s, {r['h2d_pages']} H2D pages at "
         f"{r['h2d_GBps']:.1f} GB/s")
+    out["dropin_cache"] = dropin_belady_leg(torch, dev, m.capacity, len(m.sequence))
     out["curriculum"] = curriculum_leg(torch, dev, skip_cpu)
     if not skip_cpu:
         import numpy as np
@@ -284,6 +285,41 @@ def belady_leg(torch, dev, skip_cpu):
         out["reference_linear_scan_evictions_per_s"] = round(k / (time.perf_counter() - t0), 3)
     del m
     return out
+
+
+def dropin_belady_leg(torch, dev, capacity, n_positions, seconds=2.0):
+    """The drop-in BeladyApproxCache (belady.py:14-55's interface) at configs[3]'s resident
+    set: ``capacity`` ids resident with random next uses, then a stream of new ids, each an
+    update_future + touch that misses and evicts the farthest next use.  Evictions per
+    second over ~``seconds`` (host bookkeeping, the slot-update and argmax kernels and one
+    stream synchronisation per eviction)."""
+    import numpy as np
+
+    from zenyx_amd.streaming import BeladyApproxCache
+
+    rng = np.random.default_rng(0)
+    keys = rng.integers(0, n_positions, capacity + 200_000)
+    cache = BeladyApproxCache(capacity, device=dev)
+    for i in range(capacity):
+        cache.update_future(i, int(keys[i]))
+        cache.touch(i)
+    nxt = capacity
+    for _ in range(3):  # warm-up: the first miss uploads every slot
+        cache.update_future(nxt, int(keys[nxt]))
+        cache.touch(nxt)
+        nxt += 1
+    t0 = time.perf_counter()
+    k = 0
+    while k % 64 or time.perf_counter() - t0 < seconds:
+        cache.update_future(nxt, int(keys[nxt]))
+        assert len(cache.touch(nxt)) == 1
+        nxt += 1
+        k += 1
+    dt = time.perf_counter() - t0
+    log(f"drop-in BeladyApproxCache at {capacity} resident ids: {k / dt:.0f} evictions/s")
+    return {"workload": f"BeladyApproxCache(capacity={capacity}): {capacity} resident ids with random next uses, "
+                        "then update_future + touch of new ids, each evicting one",
+            "evictions": k, "seconds": round(dt, 3), "evictions_per_s": round(k / dt, 1)}
 
 
 def curriculum_leg(torch, dev, skip_cpu):
@@ -680,93 +716,73 @@ def make_c5_layer(torch, dev, layer, out, seed=5, chunk=65536):
     return out
 
 
-def configs4_leg(torch, dev):
-    """70B-shape share, 80 layers x (4 x 128k tokens), streamed.  Forward:
-    each layer's KV is generated, appended (dynamic per-head FP8) into an HBM slot; with
-    60 slots, layer l >= 60 takes the slot of layer l - 60, the resident layer whose next
-    use in the backward sweep is farthest (Belady).  Victims are written back to pinned
-    host memory on a side stream right after their own append (write-behind), so the
-    eviction only has to wait for that copy.  Backward (79 -> 0): every layer is gathered
-    + dequantised; the slot a gather frees immediately receives the H2D prefetch of the
-    evicted layer 60 positions later in the sweep.  Per-kernel times come from HIP events
-    on the compute stream; tier moves from events on the side stream."""
-    from zenyx_amd import kv
+def configs4_setup(torch, dev, timing=False):
+    """configs[4]'s buffers: block tables (seed 5), the per-layer input, the gather outputs
+    and the 80-layer cache streamed through 60 HBM slots and pinned DRAM."""
+    from zenyx_amd.train.kv_layer_stream import LayerStreamedKVCache
 
     L, H, D, P, B, Tb, S = (C5[k] for k in ("L", "H", "D", "P", "B", "Tb", "hbm_layers"))
     T = B * Tb
     n_pages = T // P
-    slot_bytes = n_pages * 2 * H * P * D
     g = torch.Generator().manual_seed(5)
-    bt = torch.randperm(n_pages, generator=g).to(torch.int32).view(B, Tb // P).to(dev)
-    cu = torch.arange(0, T + 1, Tb, dtype=torch.int32, device=dev)
-    sl = torch.full((B,), Tb, dtype=torch.int32, device=dev)
-    x = torch.empty((T, 2, H, D), dtype=torch.bfloat16, device=dev)
-    slots = torch.empty((S, n_pages, 2, H, P, D), dtype=torch.uint8, device=dev)
-    host = torch.empty((L - S, n_pages, 2, H, P, D), dtype=torch.uint8, pin_memory=True)
-    scales = torch.empty((L, 2, H), dtype=torch.float32, device=dev)
-    kout = torch.empty((B, H, Tb, D), dtype=torch.bfloat16, device=dev)
-    vout = torch.empty_like(kout)
-    comp, side = torch.cuda.current_stream(dev), torch.cuda.Stream(dev)
+    bt_h = torch.randperm(n_pages, generator=g).to(torch.int32).view(B, Tb // P)
+    return dict(bt_host=bt_h, bt=bt_h.to(dev), cu=torch.arange(0, T + 1, Tb, dtype=torch.int32, device=dev),
+                sl=torch.full((B,), Tb, dtype=torch.int32, device=dev),
+                x=torch.empty((T, 2, H, D), dtype=torch.bfloat16, device=dev),
+                kout=torch.empty((B, H, Tb, D), dtype=torch.bfloat16, device=dev),
+                vout=torch.empty((B, H, Tb, D), dtype=torch.bfloat16, device=dev),
+                cache=LayerStreamedKVCache(L, S, n_pages, H, D, P, device=dev, timing=timing),
+                T=T, n_pages=n_pages)
+
+
+def configs4_step(torch, dev, c, on_gather=None):
+    """One configs[4] step: forward (generate layer l's KV on the device, append it) for
+    l = 0 .. 79, then backward (gather + dequant) for l = 79 .. 0, through the streamed
+    cache; ``on_gather(l, k, v)`` runs on the compute stream after each gather."""
+    cache = c["cache"]
+    cache.reset()
+    for l in range(C5["L"]):
+        make_c5_layer(torch, dev, l, c["x"])
+        cache.append_layer(l, c["x"], c["cu"], c["bt"])
+    for l in range(C5["L"] - 1, -1, -1):
+        k, v = cache.gather_layer(l, c["bt"], c["sl"], C5["Tb"], out=(c["kout"], c["vout"]))
+        if on_gather is not None:
+            on_gather(l, k, v)
+
+
+def configs4_leg(torch, dev):
+    """70B-shape share, 80 layers x (4 x 128k tokens), streamed through 60 HBM
+    layer slots and pinned DRAM (zenyx_amd.train.kv_layer_stream.LayerStreamedKVCache).
+    Forward: each layer's KV is generated, appended (dynamic per-head FP8) into its slot;
+    layers 0-19 (the Belady victims of the backward sweep) are written back to pinned host
+    memory on a side stream right after their own append, and layer l >= 60 reuses layer
+    l - 60's slot once that copy is done.  Backward (79 -> 0): every layer is gathered +
+    dequantised; the slot a gather frees immediately receives the H2D prefetch of the
+    spilled layer 60 positions later in the sweep.  Per-kernel times come from HIP events
+    on the compute stream; tier moves from events on the side stream."""
+    L, H, D, P, B, Tb, S = (C5[k] for k in ("L", "H", "D", "P", "B", "Tb", "hbm_layers"))
+    c = configs4_setup(torch, dev, timing=True)
+    T, n_pages, cache = c["T"], c["n_pages"], c["cache"]
     N = T * 2 * H * D
     alg_append = 3 * N + 4 * 2 * H + 4 * n_pages + 4 * (B + 1)
     alg_gather = 3 * N + 4 * n_pages + 4 * 2 * H + 4 * B
-    E = lambda: torch.cuda.Event(enable_timing=True)
-
-    def run():
-        app_ev, gat_ev, d2h_ev, h2d_ev = [], [], {}, {}
-        slot_of = {}
-        for l in range(L):  # forward
-            make_c5_layer(torch, dev, l, x)
-            if l >= S:  # the slot of layer l - S (farthest next use), already written back
-                comp.wait_event(d2h_ev[l - S][1])
-                slot_of[l] = slot_of.pop(l - S)
-            else:
-                slot_of[l] = l
-            e0, e1 = E(), E()
-            e0.record(comp)
-            kv.kv_quant_append(x, cu, bt, slots[slot_of[l]], scales=scales[l:l + 1])
-            e1.record(comp)
-            app_ev.append((e0, e1))
-            if l < L - S:  # a future victim: write it back now (write-behind)
-                d0, d1 = E(), E()
-                side.wait_event(e1)
-                d0.record(side)
-                kv.tier_copy_runs(host[l], slots[slot_of[l]], [0], [0], slot_bytes, stream=side)
-                d1.record(side)
-                d2h_ev[l] = (d0, d1)
-        for l in range(L - 1, -1, -1):  # backward
-            if l < L - S:
-                comp.wait_event(h2d_ev[l][1])
-            e0, e1 = E(), E()
-            e0.record(comp)
-            kv.kv_gather_dequant(slots[slot_of[l]], scales[l], bt, sl, Tb, out=(kout, vout))
-            e1.record(comp)
-            gat_ev.append((e0, e1))
-            s = slot_of.pop(l)
-            if 0 <= l - S < L - S:  # prefetch the evicted layer l - S into the slot just freed
-                h0, h1 = E(), E()
-                side.wait_event(e1)
-                h0.record(side)
-                kv.tier_copy_runs(slots[s], host[l - S], [0], [0], slot_bytes, stream=side)
-                h1.record(side)
-                h2d_ev[l - S] = (h0, h1)
-                slot_of[l - S] = s
-        return app_ev, gat_ev, list(d2h_ev.values()), list(h2d_ev.values())
 
     log("configs[4]: warm-up step (80 layers forward + backward)")
-    run()
+    configs4_step(torch, dev, c)
     torch.cuda.synchronize(dev)
+    cache.check_errors()
     log("configs[4]: timed step")
     t0 = time.perf_counter()
-    app_ev, gat_ev, d2h_ev, h2d_ev = run()
+    configs4_step(torch, dev, c)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
-    ms = lambda evs: [a.elapsed_time(b) for a, b in evs]
-    app_ms, gat_ms, d2h_ms, h2d_ms = ms(app_ev), ms(gat_ev), ms(d2h_ev), ms(h2d_ev)
+    ms = lambda evs: [a.elapsed_time(b) for a, b in evs]  # noqa: E731
+    app_ms, gat_ms = ms(cache.events["append"]), ms(cache.events["gather"])
+    d2h_ms, h2d_ms = ms(cache.events["d2h"]), ms(cache.events["h2d"])
     a_gbps = L * alg_append / (sum(app_ms) * 1e-3) / 1e9
     g_gbps = L * alg_gather / (sum(gat_ms) * 1e-3) / 1e9
-    moved = (L - S) * slot_bytes
-    med = lambda v: sorted(v)[len(v) // 2]
+    moved = (L - S) * cache.layer_bytes
+    med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
     out = {"workload": "configs[4]: 80 layers, 8 KV heads, D=128, 4 x 131072 tokens, Student-t(3) KV x "
                        "per-channel 10**U(-2,2); 60 layer slots in HBM, 20 layers spilled to pinned DRAM",
            "append_GBps": round(a_gbps, 2), "append_frac": round(a_gbps / HBM_PEAK_GBPS, 4),
@@ -783,7 +799,7 @@ def configs4_leg(torch, dev):
         f"({100 * g_gbps / HBM_PEAK_GBPS:.1f}%), D2H {out['d2h_GBps']} GB/s, H2D {out['h2d_GBps']} GB/s, "
         f"step {wall:.2f} s; per layer append median {med(app_ms):.3f} ms (min {min(app_ms):.3f}), gather median "
         f"{med(gat_ms):.3f} ms (min {min(gat_ms):.3f})")
-    del x, slots, host, kout, vout
+    del c, cache
     torch.cuda.empty_cache()
     return out
 

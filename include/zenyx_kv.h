@@ -51,6 +51,9 @@ enum zx_kernel_error {
   ZX_KERR_PAGE_RANGE = 1, /* a block-table entry outside [0, n_pages) */
   ZX_KERR_POS_RANGE = 2,  /* a token position beyond max_blocks * page_size */
   ZX_KERR_SPIN = 4,       /* a bounded inter-workgroup wait ran out (kernel exited early) */
+  ZX_KERR_OVERFLOW = 8,   /* static FP8 scales only: a finite input's quotient x / s rounded
+                             beyond the e4m3 range (|x / s| > 464), so its code is the NaN
+                             code S.1111.111 (or +-448 with ZX_APPEND_SATURATE) */
 };
 
 /* Message describing the last failing call on this thread ("" if none). */
@@ -92,8 +95,20 @@ int zx_int8_legacy_dequant_slabs(const int8_t *q, const void *scales, int scale_
  * [L][2][B][H][T][D]: n_outer = 2L, run = T*D).  scales: [n_outer][n_heads] fp32,
  * written by quant, read by dequant.  run must be a multiple of 16.
  */
+#define ZX_HEADS_TWO_PASS 1 /* flag: amax pass + encode pass instead of the single pass */
+size_t zx_fp8_quant_heads_workspace_bytes(int64_t n_outer, int64_t n_batch, int64_t n_heads, int64_t run);
+/* The slab (outer, head) is read once: each of its n_batch runs is cut into shares held in
+ * registers by one workgroup each, the workgroups of a slab exchange their maxima through
+ * the workspace, then encode what they hold (cooperative launch; every wait is bounded and
+ * a timeout sets ZX_KERR_SPIN in *err, device int32, may be NULL).  A slab needing more
+ * workgroups than the device holds (n_batch * ceil(run / 46080) > compute units), an
+ * input below 256 MiB (whose second read the Infinity Cache serves, making two passes
+ * faster), or ZX_HEADS_TWO_PASS take two passes (same results).
+ * workspace: zx_fp8_quant_heads_workspace_bytes() device bytes (unused with two passes,
+ * may then be NULL). */
 int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_heads,
-                       int64_t run, uint8_t *codes, float *scales, zx_stream_t stream);
+                       int64_t run, uint8_t *codes, float *scales, int32_t flags, int32_t *err,
+                       void *workspace, size_t workspace_bytes, zx_stream_t stream);
 int zx_fp8_dequant_heads(const uint8_t *codes, const float *scales, int64_t n_outer,
                          int64_t n_batch, int64_t n_heads, int64_t run, uint16_t *y,
                          zx_stream_t stream);
@@ -121,6 +136,11 @@ size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32
                                           int32_t head_dim);
 
 #define ZX_APPEND_STATIC_SCALES 1 /* flag: use `scales` as given instead of computing them */
+#define ZX_APPEND_SATURATE 4      /* flag, with ZX_APPEND_STATIC_SCALES: a finite input whose
+                                     quotient overflows the e4m3 range (ZX_KERR_OVERFLOW) is
+                                     stored as +-448 (code S.1111.110, the sign of x / s)
+                                     instead of the NaN code; slabs whose static scale is not
+                                     finite are unaffected */
 #define ZX_APPEND_TWO_PASS 2      /* flag: compute dynamic scales in a separate amax pass
                                      instead of the single-pass cooperative kernel (same
                                      results).  Without the flag the library picks: one
@@ -131,10 +151,16 @@ size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32
 
 /* Paged append with fused FP8 quantisation.  Without
  * ZX_APPEND_STATIC_SCALES the scales are computed from this batch (amax over all
- * of its tokens) and written to `scales`.  Static scales may be normal fp32 numbers of
- * either sign, +-inf (treated as +inf) or NaN; zero and subnormal static scales are
- * outside the contract (dynamic scales are always >= 1e-8/448).  Rows whose page id is
- * out of range are skipped and flagged in *err (device int32, may be NULL). */
+ * of its tokens) and written to `scales`; then |x / s| <= 448 (1 + 2^-23) for every
+ * finite x and no code overflows (a NaN input makes its slab's scale, and so every code
+ * of the slab, NaN, as torch's amax does).  Static scales (a decode step reusing the
+ * prefill's scales) may be normal fp32 numbers of either sign, +-inf (treated as +inf)
+ * or NaN; zero and subnormal static scales are outside the contract.  With a finite
+ * static scale a token larger than 464 |s| does not fit e4m3: its code is the NaN code
+ * (the torch cast's result) and ZX_KERR_OVERFLOW is set in *err, or, with
+ * ZX_APPEND_SATURATE, the code is +-448 (and the bit is still set).  Rows whose page id
+ * is out of range are skipped and flagged in *err (device int32, may be NULL).  Bits
+ * are ORed into *err, never cleared. */
 int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
                        int64_t n_tok, int32_t n_heads, int32_t head_dim,
                        const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
@@ -181,6 +207,14 @@ int zx_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, const uint8_
 size_t zx_belady_argmax_workspace_bytes(int64_t n_slots);
 int zx_belady_argmax(const int64_t *keys, const uint8_t *resident, int64_t n_slots, int64_t *out,
                      void *workspace, size_t workspace_bytes, zx_stream_t stream);
+
+/* Slot updates of the drop-in cache's device tables (BeladyApproxCache.update_future and
+ * .touch, belady.py:22-37): for i < n, keys[slot[i]] = key[i] and resident[slot[i]] = res[i];
+ * each slot at most once per call.  slot / key / res may live in pinned host memory (the
+ * kernel reads them directly) and must stay valid until the update has run.  A slot
+ * outside [0, n_slots) is skipped and sets ZX_KERR_PAGE_RANGE in *err (may be NULL). */
+int zx_belady_update_slots(int64_t *keys, uint8_t *resident, int64_t n_slots, const int64_t *slot,
+                           const int64_t *key, const uint8_t *res, int64_t n, int32_t *err, zx_stream_t stream);
 
 /* Next/previous use of every trace position: next_use[i] = smallest j > i with
  * trace[j] == trace[i], else ZX_NEVER; prev_use[i] = largest j < i, else -1.

@@ -1,0 +1,459 @@
+// stream_ceiling.hip -- measures the HBM ceilings that bound the KV append and gather on
+// this device, with no arithmetic, no scale exchange and no page indirection:
+//
+//   plain    plain streams (one 16-byte vector per thread, nontemporal loads and stores)
+//            with the read:write mixes of the append (2:1) and the gather (1:2), at the
+//            byte counts of BASELINE configs[1] / configs[2];
+//   pages    reads of random 2 KiB runs (one (page, K/V, head) run of a 16-token FP8 page)
+//            out of a 300,000-page pool, the pattern of the paged gather and of decode
+//            attention (4.29 GB read), read-only and with the gather's
+//            2 bytes written per byte read;
+//   append   the access pattern the single-pass append is forced into: a layer of token
+//            rows of 4 KiB (2 x 8 heads x 128 bf16) cannot stay on chip (302 MB at
+//            configs[1] versus ~170 MB of registers + LDS on 256 CUs), and a slab's scale
+//            needs its amax over all tokens, so each step reads one 256-byte slab of every
+//            row, with NB = 4 steps in flight per workgroup, and writes 128 bytes per row.
+//            Run as a persistent grid (one 1024-thread workgroup per CU) with the token
+//            share of every workgroup fixed (as the fused append does) and with chunks of
+//            64 tokens dealt out per slab by an atomic counter;
+//   columns  the same column blocks (W = 256 B .. 2 KiB of every 4 KiB row, W / 2 bytes
+//            written per row) read by ordinary launches at full occupancy (256-thread
+//            workgroups, one launch per column block), which separates the cost of the
+//            pattern from the cost of the persistent structure;
+//   cache    whether the memory-side Infinity Cache (256 MB) serves a second read: a
+//            buffer of C MiB is read once after a 1 GiB flush, then read again, with
+//            default-policy (temporal) and nontemporal loads on the first read;
+//   chunked  the two-pass design that would rely on it: 1 Gi bf16 elements (2 GiB) as
+//            chunks of C MiB, each read twice (a max pass, then a pass that writes 1 byte
+//            per element), against the same passes over the whole buffer.
+//
+// Usage: stream_ceiling [plain|pages|append|columns|cache|chunked|all] (default all).
+// Prints one line per measurement.  Every access is in bounds; nothing waits on another
+// workgroup.  Built by __graft_entry__.build() into measure/bin/stream_ceiling.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#define SC_CHECK(x)                                                                     \
+  do {                                                                                  \
+    hipError_t e_ = (x);                                                                \
+    if (e_ != hipSuccess) {                                                             \
+      fprintf(stderr, "HIP error %s at line %d\n", hipGetErrorString(e_), __LINE__);   \
+      exit(1);                                                                          \
+    }                                                                                   \
+  } while (0)
+
+typedef unsigned int sc_v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int sc_v2u __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- 1. plain streams
+
+// RB bytes read and WB bytes written per thread (16 or 8), n threads.
+template <int RB, int WB>
+__global__ void plain_stream(const char *__restrict__ src, char *__restrict__ dst, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  unsigned a, b, c, d;
+  if (RB == 16) {
+    const sc_v4u v = __builtin_nontemporal_load(reinterpret_cast<const sc_v4u *>(src) + i);
+    a = v.x, b = v.y, c = v.z, d = v.w;
+  } else {
+    const sc_v2u v = __builtin_nontemporal_load(reinterpret_cast<const sc_v2u *>(src) + i);
+    a = v.x, b = v.y, c = v.x ^ 1u, d = v.y ^ 1u;
+  }
+  if (WB == 16) {
+    const sc_v4u o = {a, b ^ 1u, c, d ^ a};
+    __builtin_nontemporal_store(o, reinterpret_cast<sc_v4u *>(dst) + i);
+  } else {
+    const sc_v2u o = {a ^ b, c ^ d};
+    __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(dst) + i);
+  }
+}
+
+// ---------------------------------------------------------------- 2. random page runs
+
+// Workgroup w reads runs w*R .. w*R + R - 1 of the list (2 KiB each, 8 bytes per lane per
+// run); with WRITE it stores 16 bytes per lane per run contiguously (the bf16 output).
+template <bool WRITE>
+__global__ void __launch_bounds__(256) page_runs(const char *__restrict__ pool, const long *__restrict__ runs,
+                                                 long n_runs, char *__restrict__ out, unsigned *sink) {
+  constexpr int R = 4;
+  unsigned acc = 0;
+  sc_v2u v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long k = (long)blockIdx.x * R + r;
+    v[r] = k < n_runs ? __builtin_nontemporal_load(reinterpret_cast<const sc_v2u *>(pool + runs[k]) + threadIdx.x)
+                      : sc_v2u{0, 0};
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long k = (long)blockIdx.x * R + r;
+    if (WRITE && k < n_runs) {
+      const sc_v4u o = {v[r].x, v[r].y ^ 1u, v[r].x ^ 2u, v[r].y ^ 3u};
+      __builtin_nontemporal_store(o, reinterpret_cast<sc_v4u *>(out + k * 4096) + threadIdx.x);
+    }
+    acc ^= v[r].x ^ v[r].y;
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+// ---------------------------------------------------------------- 3. append pattern
+
+constexpr int SC_TPB = 1024;
+constexpr int SC_CT = 64;  // tokens per chunk: 64 x 16 vectors = one 16-byte vector per lane
+constexpr int SC_K = 6;    // chunks a workgroup holds per slab
+constexpr int SC_NB = 4;   // slabs in flight per workgroup
+constexpr int SC_ROW = 4096, SC_SLAB = 256, SC_SLABS_PER_ROW = SC_ROW / SC_SLAB;
+
+struct PatternArgs {
+  const char *x;  // [L][T][4096 B]
+  char *out;      // [L * 16][T][128 B]
+  long T;
+  int n_slabs, n_chunks, dynamic;
+  unsigned *counter;  // [n_slabs], zero at launch (dynamic only)
+};
+
+__device__ __forceinline__ sc_v4u pat_load(const PatternArgs &a, int s, int c, int tid) {
+  const long tok = (long)c * SC_CT + tid / 16;
+  if (c < 0 || s >= a.n_slabs || tok >= a.T) return sc_v4u{0, 0, 0, 0};
+  const int l = s / SC_SLABS_PER_ROW, j = s % SC_SLABS_PER_ROW;
+  return __builtin_nontemporal_load(
+      reinterpret_cast<const sc_v4u *>(a.x + ((long)l * a.T + tok) * SC_ROW + j * SC_SLAB + (tid % 16) * 16));
+}
+
+__device__ __forceinline__ void pat_store(const PatternArgs &a, int s, int c, int tid, sc_v4u v) {
+  const long tok = (long)c * SC_CT + tid / 16;
+  if (c < 0 || s >= a.n_slabs || tok >= a.T) return;
+  const sc_v2u o = {v.x ^ v.y, v.z ^ v.w};
+  __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(a.out + ((long)s * a.T + tok) * 128 + (tid % 16) * 8));
+}
+
+__global__ void __launch_bounds__(SC_TPB) append_pattern(PatternArgs a) {
+  __shared__ int base[SC_NB];
+  const int tid = threadIdx.x, w = blockIdx.x, G = gridDim.x;
+  sc_v4u buf[SC_NB][SC_K];
+  int cid[SC_NB][SC_K];
+  // chunk ids of slab s for buffer i (the same on every lane of the workgroup)
+  auto assign = [&](int s, int i) {
+    if (!a.dynamic) {
+      const int c0 = (int)((long)w * a.n_chunks / G), c1 = (int)((long)(w + 1) * a.n_chunks / G);
+#pragma unroll
+      for (int k = 0; k < SC_K; ++k) cid[i][k] = c0 + k < c1 ? c0 + k : -1;
+    } else {
+      __syncthreads();
+      if (tid == 0) base[i] = s < a.n_slabs ? (int)atomicAdd(&a.counter[s], (unsigned)SC_K) : a.n_chunks;
+      __syncthreads();
+      const int b = base[i];
+#pragma unroll
+      for (int k = 0; k < SC_K; ++k) cid[i][k] = b + k < a.n_chunks ? b + k : -1;
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < SC_NB; ++i) {
+    assign(i, i);
+#pragma unroll
+    for (int k = 0; k < SC_K; ++k) buf[i][k] = pat_load(a, i, cid[i][k], tid);
+  }
+  const int s_pad = (a.n_slabs + SC_NB - 1) / SC_NB * SC_NB;
+  for (int s0 = 0; s0 < s_pad; s0 += SC_NB) {
+#pragma unroll
+    for (int i = 0; i < SC_NB; ++i) {
+      const int s = s0 + i;
+#pragma unroll
+      for (int k = 0; k < SC_K; ++k) pat_store(a, s, cid[i][k], tid, buf[i][k]);
+      assign(s + SC_NB, i);
+#pragma unroll
+      for (int k = 0; k < SC_K; ++k) buf[i][k] = pat_load(a, s + SC_NB, cid[i][k], tid);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- 4. column blocks, full occupancy
+
+// One launch per column block j: reads bytes [j W, (j + 1) W) of every 4 KiB row and writes
+// W / 2 bytes per row (out: this block's [row][W / 2]).  256 threads cover 256 / (W / 16)
+// rows per step, U steps per workgroup, all loads issued before the stores.
+template <int U, int POL>
+__global__ void __launch_bounds__(256) column_block(const char *__restrict__ x, char *__restrict__ out, long rows,
+                                                   int W, int j) {
+  const int lpr = W / 16;
+  const int rpb = 256 / lpr;
+  const long r0 = (long)blockIdx.x * U * rpb + threadIdx.x / lpr;
+  const int c = threadIdx.x % lpr;
+  sc_v4u v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const long r = r0 + (long)u * rpb;
+    const sc_v4u *p = reinterpret_cast<const sc_v4u *>(x + r * 4096 + (long)j * W) + c;
+    v[u] = r < rows ? (POL ? __builtin_nontemporal_load(p) : *p) : sc_v4u{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const long r = r0 + (long)u * rpb;
+    if (r < rows) {
+      const sc_v2u o = {v[u].x ^ v[u].y, v[u].z ^ v[u].w};
+      __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(out + r * (W / 2)) + c);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- 5./6. cache reuse, chunked passes
+
+// Grid-stride read of n 16-byte vectors (4 in flight per thread), folded into a value that
+// is stored only if it matches a constant (so the loads are kept).  POL 0: default cache
+// policy; POL 1: nontemporal.
+template <int POL>
+__global__ void __launch_bounds__(256) read_fold(const sc_v4u *__restrict__ x, long n, unsigned *sink) {
+  const long stride = (long)gridDim.x * 256;
+  unsigned m = 0;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += 4 * stride) {
+    sc_v4u v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long k = i + u * stride;
+      v[u] = k < n ? (POL ? __builtin_nontemporal_load(x + k) : x[k]) : sc_v4u{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) m = max(m, max(v[u].x ^ v[u].y, v[u].z ^ v[u].w));
+  }
+  if (m == 0x9E3779B9u) sink[0] = m;
+}
+
+// Grid-stride read of n vectors, 8 bytes written per 16 read (nontemporal stores).
+template <int POL>
+__global__ void __launch_bounds__(256) read_write_half(const sc_v4u *__restrict__ x, sc_v2u *__restrict__ out,
+                                                       long n) {
+  const long stride = (long)gridDim.x * 256;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += 4 * stride) {
+    sc_v4u v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long k = i + u * stride;
+      v[u] = k < n ? (POL ? __builtin_nontemporal_load(x + k) : x[k]) : sc_v4u{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long k = i + u * stride;
+      if (k < n) __builtin_nontemporal_store(sc_v2u{v[u].x ^ v[u].y, v[u].z ^ v[u].w}, out + k);
+    }
+  }
+}
+
+static unsigned grid_for(long n_vec) {
+  const long g = (n_vec + 1023) / 1024;
+  return (unsigned)(g < 1 ? 1 : (g > 16384 ? 16384 : g));
+}
+
+// ---------------------------------------------------------------- host
+
+template <typename F>
+static float best_ms(F launch, int reps) {
+  hipEvent_t e0, e1;
+  SC_CHECK(hipEventCreate(&e0));
+  SC_CHECK(hipEventCreate(&e1));
+  float best = 1e30f;
+  for (int r = 0; r < reps; ++r) {
+    SC_CHECK(hipEventRecord(e0));
+    launch();
+    SC_CHECK(hipEventRecord(e1));
+    SC_CHECK(hipEventSynchronize(e1));
+    float ms = 0;
+    SC_CHECK(hipEventElapsedTime(&ms, e0, e1));
+    best = std::min(best, ms);
+  }
+  SC_CHECK(hipEventDestroy(e0));
+  SC_CHECK(hipEventDestroy(e1));
+  return best;
+}
+
+static bool want(const char *sel, const char *group) { return !strcmp(sel, "all") || !strcmp(sel, group); }
+
+int main(int argc, char **argv) {
+  const char *sel = argc > 1 ? argv[1] : "all";
+  // configs[1] with seed 1: 32 layers x 74,902 tokens x 4 KiB rows
+  const int L = 32;
+  const long T = 74902;
+  const long in_bytes = (long)L * T * SC_ROW;  // 9.82 GB
+  const long out_bytes = in_bytes / 2;
+  char *x = nullptr, *out = nullptr;
+  unsigned *counter = nullptr;
+  SC_CHECK(hipMalloc(&x, in_bytes));
+  SC_CHECK(hipMalloc(&out, in_bytes));  // large enough for the 1:2 stream too
+  SC_CHECK(hipMalloc(&counter, 4096 * sizeof(unsigned)));
+  SC_CHECK(hipMemset(x, 0x11, in_bytes));
+  int ncu = 0;
+  SC_CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, 0));
+  printf("device CUs: %d\n", ncu);
+  fflush(stdout);
+
+  if (want(sel, "plain")) {  // 2:1 stream over the append's bytes
+    const long n = in_bytes / 16;
+    float ms = best_ms([&] { plain_stream<16, 8><<<(unsigned)((n + 255) / 256), 256>>>(x, out, n); }, 5);
+    printf("plain stream 2:1 (read %.3f GB, write %.3f GB): %.3f ms, %.1f GB/s\n", in_bytes / 1e9, out_bytes / 1e9,
+           ms, (in_bytes + out_bytes) / ms / 1e6);
+    // 1:2 stream over the gather's bytes (configs[2]: 4.29 GB codes in, 8.59 GB bf16 out)
+    const long n2 = 4294967296L / 8;
+    ms = best_ms([&] { plain_stream<8, 16><<<(unsigned)((n2 + 255) / 256), 256>>>(x, out, n2); }, 5);
+    printf("plain stream 1:2 (read %.3f GB, write %.3f GB): %.3f ms, %.1f GB/s\n", n2 * 8 / 1e9, n2 * 16 / 1e9, ms,
+           n2 * 24.0 / ms / 1e6);
+    fflush(stdout);
+  }
+  if (want(sel, "pages")) {  // random 2 KiB runs of a 300,000-page pool (32 KiB pages: K and V x 8 heads x 2 KiB)
+    const long n_pool_pages = 300000, page = 32768;
+    const long pool_bytes = n_pool_pages * page;  // 9.83 GB
+    char *pool = nullptr;
+    SC_CHECK(hipMalloc(&pool, pool_bytes));
+    SC_CHECK(hipMemset(pool, 0x22, pool_bytes));
+    // 64 sequences x 2048 pages x 2 (K, V) x 8 heads runs, pages drawn at random
+    const long n_runs = 64L * 2048 * 2 * 8;
+    long *runs_h = (long *)malloc(n_runs * sizeof(long));
+    unsigned long long r = 88172645463325252ull;
+    for (long i = 0; i < n_runs / 16; ++i) {
+      r ^= r << 13, r ^= r >> 7, r ^= r << 17;
+      const long pg = (long)(r % (unsigned long long)n_pool_pages);
+      for (int j = 0; j < 16; ++j) runs_h[i * 16 + j] = pg * page + j * 2048;  // K and V runs of 8 heads
+    }
+    long *runs = nullptr;
+    SC_CHECK(hipMalloc(&runs, n_runs * sizeof(long)));
+    SC_CHECK(hipMemcpy(runs, runs_h, n_runs * sizeof(long), hipMemcpyHostToDevice));
+    free(runs_h);
+    unsigned *sink = counter;
+    const unsigned blocks = (unsigned)((n_runs + 3) / 4);
+    float ms = best_ms([&] { page_runs<false><<<blocks, 256>>>(pool, runs, n_runs, out, sink); }, 5);
+    printf("random 2 KiB page runs, read only (%.3f GB): %.3f ms, %.1f GB/s\n", n_runs * 2048 / 1e9, ms,
+           n_runs * 2048.0 / ms / 1e6);
+    ms = best_ms([&] { page_runs<true><<<blocks, 256>>>(pool, runs, n_runs, out, sink); }, 5);
+    printf("random 2 KiB page runs + 2 B written per byte read (%.3f GB moved): %.3f ms, %.1f GB/s\n",
+           n_runs * 6144 / 1e9, ms, n_runs * 6144.0 / ms / 1e6);
+    fflush(stdout);
+    SC_CHECK(hipFree(pool));
+    SC_CHECK(hipFree(runs));
+  }
+  if (want(sel, "append")) {
+    const int chunks = (int)((T + SC_CT - 1) / SC_CT);
+    if ((long)ncu * SC_K < chunks) {
+      printf("append pattern skipped: %d CUs x %d chunks < %d chunks per slab\n", ncu, SC_K, chunks);
+    } else {
+      for (int dyn = 0; dyn < 2; ++dyn) {
+        PatternArgs a{x, out, T, L * SC_SLABS_PER_ROW, chunks, dyn, counter};
+        const float ms = best_ms(
+            [&] {
+              SC_CHECK(hipMemsetAsync(counter, 0, 4096 * sizeof(unsigned)));
+              append_pattern<<<ncu, SC_TPB>>>(a);
+            },
+            5);
+        printf("append pattern, %s shares (256 B of each 4 KiB row per step, %d steps in flight): %.3f ms, %.1f "
+               "GB/s\n",
+               dyn ? "dynamic" : "static", SC_NB, ms, (in_bytes + out_bytes) / ms / 1e6);
+        fflush(stdout);
+      }
+    }
+  }
+  if (want(sel, "columns")) {
+    const long rows = (long)L * T;
+    for (int pol = 1; pol >= 0; --pol) {
+      for (int W = 256; W <= 2048; W *= 2) {
+        const int lpr = W / 16, rpb = 256 / lpr;
+        constexpr int U = 4;
+        const unsigned blocks = (unsigned)((rows + (long)U * rpb - 1) / ((long)U * rpb));
+        const float ms = best_ms(
+            [&] {
+              for (int j = 0; j < 4096 / W; ++j) {
+                if (pol)
+                  column_block<U, 1><<<blocks, 256>>>(x, out + (long)j * rows * (W / 2), rows, W, j);
+                else
+                  column_block<U, 0><<<blocks, 256>>>(x, out + (long)j * rows * (W / 2), rows, W, j);
+              }
+            },
+            3);
+        printf("column blocks of %d B per 4 KiB row, one launch per block (%d launches), %s loads: %.3f ms, %.1f "
+               "GB/s\n",
+               W, 4096 / W, pol ? "nontemporal" : "default", ms, (in_bytes + out_bytes) / ms / 1e6);
+        fflush(stdout);
+      }
+    }
+  }
+  if (want(sel, "cache")) {
+    const long flush_bytes = 1L << 30;
+    char *flush = out;  // a region disjoint from the probed one
+    unsigned *sink = counter;
+    hipEvent_t e0, e1;
+    SC_CHECK(hipEventCreate(&e0));
+    SC_CHECK(hipEventCreate(&e1));
+    const long sizes_mib[] = {16, 32, 64, 128, 192, 256, 384};
+    for (int pol = 0; pol < 2; ++pol) {
+      for (long mib : sizes_mib) {
+        const long bytes = mib << 20, n = bytes / 16;
+        float best1 = 1e30f, best2 = 1e30f;
+        for (int rep = 0; rep < 3; ++rep) {
+          read_fold<0><<<grid_for(flush_bytes / 16), 256>>>(reinterpret_cast<const sc_v4u *>(flush),
+                                                             flush_bytes / 16, sink);
+          float t1 = 0, t2 = 0;
+          SC_CHECK(hipEventRecord(e0));
+          if (pol)
+            read_fold<1><<<grid_for(n), 256>>>(reinterpret_cast<const sc_v4u *>(x), n, sink);
+          else
+            read_fold<0><<<grid_for(n), 256>>>(reinterpret_cast<const sc_v4u *>(x), n, sink);
+          SC_CHECK(hipEventRecord(e1));
+          SC_CHECK(hipEventSynchronize(e1));
+          SC_CHECK(hipEventElapsedTime(&t1, e0, e1));
+          SC_CHECK(hipEventRecord(e0));
+          read_fold<0><<<grid_for(n), 256>>>(reinterpret_cast<const sc_v4u *>(x), n, sink);
+          SC_CHECK(hipEventRecord(e1));
+          SC_CHECK(hipEventSynchronize(e1));
+          SC_CHECK(hipEventElapsedTime(&t2, e0, e1));
+          best1 = std::min(best1, t1);
+          best2 = std::min(best2, t2);
+        }
+        printf("cache reuse, %ld MiB: first read (%s loads, after a 1 GiB flush) %.4f ms = %.1f GB/s; second read "
+               "(default loads) %.4f ms = %.1f GB/s\n",
+               mib, pol ? "nontemporal" : "default", best1, bytes / best1 / 1e6, best2, bytes / best2 / 1e6);
+        fflush(stdout);
+      }
+    }
+    SC_CHECK(hipEventDestroy(e0));
+    SC_CHECK(hipEventDestroy(e1));
+  }
+  if (want(sel, "chunked")) {
+    const long total = 2L << 30;  // 1 Gi bf16 elements
+    const sc_v4u *xv = reinterpret_cast<const sc_v4u *>(x);
+    sc_v2u *ov = reinterpret_cast<sc_v2u *>(out);
+    unsigned *sink = counter;
+    {
+      const long n = total / 16;
+      const float ms = best_ms([&] { read_write_half<1><<<grid_for(n), 256>>>(xv, ov, n); }, 5);
+      printf("chunked: one pass 2:1 over 2 GiB (read 2 GiB, write 1 GiB): %.4f ms, %.1f GB/s of 3 GiB\n", ms,
+             3.0 * (1L << 30) / ms / 1e6);
+    }
+    const long chunk_mib[] = {32, 64, 128, 256, 2048};
+    for (int pol = 0; pol < 2; ++pol) {
+      for (long mib : chunk_mib) {
+        const long c = std::min(total, mib << 20), n = c / 16;
+        const float ms = best_ms(
+            [&] {
+              for (long off = 0; off < total; off += c) {
+                const long v0 = off / 16;
+                if (pol)
+                  read_fold<1><<<grid_for(n), 256>>>(xv + v0, n, sink);
+                else
+                  read_fold<0><<<grid_for(n), 256>>>(xv + v0, n, sink);
+                read_write_half<1><<<grid_for(n), 256>>>(xv + v0, ov + v0, n);
+              }
+            },
+            3);
+        printf("chunked two passes, chunks of %ld MiB (%ld launches), first pass %s loads: %.4f ms, %.1f GB/s of "
+               "3 GiB algorithmic\n",
+               mib, 2 * (total / c), pol ? "nontemporal" : "default", ms, 3.0 * (1L << 30) / ms / 1e6);
+        fflush(stdout);
+      }
+    }
+  }
+  SC_CHECK(hipFree(x));
+  SC_CHECK(hipFree(out));
+  SC_CHECK(hipFree(counter));
+  return 0;
+}

@@ -150,8 +150,10 @@ def kv_scales(x_bits: np.ndarray) -> np.ndarray:
 
 
 def kv_quant_append(x_bits, cu_seqlens, start_pos, block_tables, pool, page_size,
-                    scales=None):
-    """In-place paged append into pool [L, n_pages, 2, H, P, D]; returns (scales, err)."""
+                    scales=None, saturate=False):
+    """In-place paged append into pool [L, n_pages, 2, H, P, D]; returns (scales, err).
+    With ``scales`` given they are static; ``saturate`` then stores overflowing finite
+    inputs as +-448 instead of the NaN code (err bit 8 is set either way)."""
     x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
     L, n_tok, _, H, D = x_bits.shape
     cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
@@ -163,7 +165,7 @@ def kv_quant_append(x_bits, cu_seqlens, start_pos, block_tables, pool, page_size
     sc = np.ascontiguousarray(scales, np.float32).copy() if static else np.empty((L, 2, H), np.float32)
     err = lib().zxo_kv_quant_append(_p(x_bits), n_tok * 2 * H * D, L, n_tok, H, D, _p(cu), _p(sp),
                                     len(cu) - 1, _p(bt), bt.shape[1], page_size, _p(pool),
-                                    pool[0].size, n_pages, _p(sc), int(static))
+                                    pool[0].size, n_pages, _p(sc), int(static) | (4 if saturate and static else 0))
     return sc, int(err)
 
 

@@ -196,14 +196,19 @@ void zxo_kv_scales(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, 
     }
 }
 
-/* Paged append; returns the OR of ZX_KERR_* bits (1 page range, 2 position range). */
+/* Paged append; returns the OR of ZX_KERR_* bits (1 page range, 2 position range,
+ * 8 overflow).  flags: 1 static scales (scales are input), 4 saturate (with static
+ * scales: a finite x whose code under a finite scale is the NaN code, i.e. whose
+ * quotient rounds beyond 448, sets bit 8 and is stored as +-448, the quotient's sign;
+ * without it the NaN code stays and bit 8 is still set). */
 int32_t zxo_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
                             int64_t n_tok, int32_t n_heads, int32_t head_dim,
                             const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
                             const int32_t *block_tables, int32_t max_blocks, int32_t page_size,
                             uint8_t *pool, int64_t pool_layer_stride, int64_t n_pages,
-                            float *scales, int32_t static_scales) {
+                            float *scales, int32_t flags) {
   int32_t err = 0;
+  const int static_scales = flags & 1, saturate = flags & 4;
   if (!static_scales) zxo_kv_scales(x, x_layer_stride, n_layers, n_tok, n_heads, head_dim, scales);
   int64_t row = 2LL * n_heads * head_dim;
   for (int32_t l = 0; l < n_layers; ++l)
@@ -219,7 +224,15 @@ int32_t zxo_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n
           const uint16_t *src = x + l * x_layer_stride + t * row + (int64_t)s * head_dim;
           uint8_t *dst = pool + l * pool_layer_stride +
                          ((page * 2 * n_heads + s) * page_size + slot) * head_dim;
-          for (int32_t d = 0; d < head_dim; ++d) dst[d] = zxo_fp8_code(zxo_bf16_to_f32(src[d]), sc);
+          for (int32_t d = 0; d < head_dim; ++d) {
+            const float xv = zxo_bf16_to_f32(src[d]);
+            uint8_t c = zxo_fp8_code(xv, sc);
+            if (static_scales && isfinite(sc) && isfinite(xv) && (c & 0x7F) == 0x7F) {
+              err |= 8;
+              if (saturate) c = (uint8_t)((c & 0x80) | 0x7E);
+            }
+            dst[d] = c;
+          }
         }
       }
   return err;

@@ -1,4 +1,6 @@
-"""configs[4] (70B-shape share, 4 x 131,072 tokens per layer) parity on sampled layers.
+"""configs[4] (70B-shape share, 4 x 131,072 tokens per layer) parity on sampled layers,
+appended and gathered on their own, and the whole streamed step bench.py times (80 layers
+through 60 HBM slots and pinned DRAM) checked after the backward gather.
 
 Each sampled layer is generated on the device exactly as bench.py's configs[4] leg does
 (Student-t(3) x per-channel 10**U(-2, 2)), appended with dynamic scales (the library takes
@@ -67,3 +69,70 @@ def test_configs4_sampled_layer(dev, layer):
         w_nan = (want_kv & 0x7FFF) > 0x7F80
         np.testing.assert_array_equal(g_nan, w_nan)
         np.testing.assert_array_equal(got_kv[~g_nan], want_kv[~w_nan])
+
+
+def _oracle_rows(xb, wsc, tok, P):
+    """Oracle codes [S, 2, H, D] of token rows xb[tok] under the layer scales wsc [1, 2, H]
+    (appended into a compact pool, one position per sampled row) and their dequantised
+    bf16 bits [2, H, S, D]."""
+    S = len(tok)
+    _, _, H, D = xb.shape
+    compact = np.zeros((1, S // P, 2, H, P, D), np.uint8)
+    _, werr = O.kv_quant_append(np.ascontiguousarray(xb[tok])[None], np.array([0, S], np.int32), None,
+                                np.arange(S // P, dtype=np.int32)[None], compact, P, scales=wsc)
+    assert werr == 0
+    want = compact[0].transpose(0, 3, 1, 2, 4).reshape(S, 2, H, D)
+    codes = np.ascontiguousarray(want.transpose(1, 2, 0, 3)).reshape(2, 1, H, S * D)
+    return want, O.fp8_dequant_heads(codes, wsc[0]).reshape(2, H, S, D)
+
+
+def _assert_bf16_bits(got, want):
+    g_nan = (got & 0x7FFF) > 0x7F80
+    w_nan = (want & 0x7FFF) > 0x7F80
+    np.testing.assert_array_equal(g_nan, w_nan)
+    np.testing.assert_array_equal(got[~g_nan], want[~w_nan])
+
+
+def test_configs4_streamed_step(dev):
+    """bench.py's configs[4] step end to end (bench.configs4_step over
+    LayerStreamedKVCache): layers 0, 7 and 19 are written back to pinned DRAM after their
+    append, their slots reused by layers 60, 67 and 79, and prefetched back into slots the
+    backward gathers freed; layers 60 and 79 stay resident.  For each, after the backward
+    gather: the layer's 16 scales and 2,048 sampled (sequence, position) rows of the
+    gathered K and V (all heads and channels) bit-exact against the oracle."""
+    C = bench.C5
+    H, D, P, B, Tb = C["H"], C["D"], C["P"], C["B"], C["Tb"]
+    c = bench.configs4_setup(torch, dev)
+    cache = c["cache"]
+    assert cache.n_spill == 20 and cache.S == 60
+    sample = (0, 7, 19, 60, 79)
+    rng = np.random.default_rng(17)
+    S = 2048
+    picks = {l: (rng.integers(0, B, S), rng.integers(0, Tb, S)) for l in sample}
+    got = {}
+
+    def on_gather(layer, k, v):
+        if layer in picks:
+            b, pos = (torch.from_numpy(a).to(dev) for a in picks[layer])
+            got[layer] = (k[b, :, pos].clone(), v[b, :, pos].clone())  # [S, H, D]
+
+    print("configs[4] streamed step: 80 layers forward + backward", flush=True)
+    bench.configs4_step(torch, dev, c, on_gather)
+    torch.cuda.synchronize()
+    cache.check_errors()
+    scales = cache.scales.cpu().numpy()
+    x = c["x"]
+    for layer in sample:
+        bench.make_c5_layer(torch, dev, layer, x)
+        xb = bits16(x)
+        wsc = O.kv_scales(xb[None])
+        np.testing.assert_array_equal(scales[layer].view(np.uint32), wsc[0].view(np.uint32))
+        b, pos = picks[layer]
+        _, deq = _oracle_rows(xb, wsc, b * Tb + pos, P)
+        gk, gv = (bits16(t) for t in got[layer])
+        _assert_bf16_bits(gk, deq[0].transpose(1, 0, 2))
+        _assert_bf16_bits(gv, deq[1].transpose(1, 0, 2))
+        where = "spilled to pinned DRAM and prefetched back" if layer < cache.n_spill else "resident"
+        print(f"layer {layer} ({where}): scales and {S} gathered rows bit-exact", flush=True)
+    del c, cache, x, got
+    torch.cuda.empty_cache()

@@ -1,10 +1,10 @@
 """Parity at BASELINE's full sizes, on the exact workloads bench.py times.
 
 * configs[1] (seed 1: 32 layers x 74,902 tokens, 8 KV heads, D = 128, page 16, outlier
-  heads x50): one fused append of all layers; for sampled layers every scale is checked
-  bit-exact against the oracle's amax over the whole layer, and the codes of 2,048
-  sampled token rows (all K/V, heads and channels) bit-exact against the oracle's
-  append of those rows with the oracle's scales.
+  heads x50): one fused append of all layers; all 512 scales bit-exact against the
+  oracle's amax over each whole layer, one whole layer's pool (every code) against the
+  oracle's torch restatement, and 2,048 sampled token rows of three more layers (all K/V,
+  heads and channels) against the C oracle's append of those rows.
 * configs[2] (64 x 32,768 positions, 300,000-page pool): the full gather; 4,096 sampled
   positions of every (sequence, head) checked bit-exact against the oracle's dequant.
 * the decode attention over the same pool, two whole sequences checked against the
@@ -34,18 +34,33 @@ def bits16(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def test_configs1_full_append_sampled_layers(dev):
+def test_configs1_full_append(dev):
+    """configs[1]: all 32 layers' 16 scales against the oracle's amax over each whole layer;
+    one whole layer's pool (4,688 pages, every code) against the torch restatement of the
+    append (bit-identical to the C oracle, tests/test_oracle.py); 2,048 sampled rows of
+    three more layers against the C oracle."""
     W = bench.make_append_workload(torch, dev, seed=1)
     print(f"configs[1]: {W['T']} tokens x {W['L']} layers", flush=True)
     sc = kv.kv_quant_append(W["x"], W["cu"], W["bt"], W["pool"], check=True)
     torch.cuda.synchronize()
     L, H, D, P, T = W["L"], W["H"], W["D"], W["P"], W["T"]
     cu, bt = W["cu_host"].numpy(), W["bt_host"].numpy()
-    rng = np.random.default_rng(11)
-    for layer in (0, 13, 31):
+    got_sc = sc.cpu().numpy()
+    for layer in range(L):
         xb = bits16(W["x"][layer])  # [T, 2, H, D]
         wsc = O.kv_scales(xb[None])[0]
-        np.testing.assert_array_equal(sc[layer].cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+        np.testing.assert_array_equal(got_sc[layer].view(np.uint32), wsc.view(np.uint32))
+    print(f"all {L * 2 * H} scales bit-exact", flush=True)
+    whole = 22
+    wsc_t, wpool = O.kv_quant_append_torch(W["x"][whole].cpu(), cu, bt, W["n_pages"], P)
+    np.testing.assert_array_equal(got_sc[whole].view(np.uint32), wsc_t.numpy().view(np.uint32))
+    gpool = W["pool"][whole].cpu()
+    assert torch.equal(gpool, wpool), f"layer {whole}: {(gpool != wpool).sum().item()} codes differ"
+    print(f"layer {whole}: the whole pool ({gpool.numel()} codes) bit-exact", flush=True)
+    rng = np.random.default_rng(11)
+    for layer in (0, 13, 31):
+        xb = bits16(W["x"][layer])
+        wsc = O.kv_scales(xb[None])[0]
         S = 2048
         tok = np.sort(rng.choice(T, S, replace=False))
         b = np.searchsorted(cu, tok, side="right") - 1
@@ -58,7 +73,7 @@ def test_configs1_full_append_sampled_layers(dev):
         assert werr == 0
         want = compact[0].transpose(0, 3, 1, 2, 4).reshape(S, 2, H, D)
         np.testing.assert_array_equal(got, want)
-        print(f"layer {layer}: scales and {S} rows bit-exact", flush=True)
+        print(f"layer {layer}: {S} rows bit-exact", flush=True)
 
 
 def test_configs2_full_gather_and_attention(dev):
@@ -158,7 +173,8 @@ def test_configs3_full_belady_schedule(dev):
                                     head_dim=128, page_tokens=64, hbm_budget_bytes=64e9, device=dev)
     print(f"configs[3]: {len(m.sequence)} accesses, {m.n_pages} pages, capacity {m.capacity}", flush=True)
     stats = m.plan()
-    trace = m.sequence.trace("cpu").numpy()
+    trace = O.ring_trace(80, 8, m.pages_per_shard)
+    np.testing.assert_array_equal(m.sim.trace.cpu().numpy(), trace)
     pos, page, st, miss = O.belady_simulate(trace, m.n_pages, m.capacity, miss_flags=True)
     assert {k: stats[k] for k in ("evictions", "misses", "hits", "resident")} == st
     gpos, gpage = m.sim.evictions()

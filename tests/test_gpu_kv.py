@@ -79,6 +79,45 @@ def test_fp8_quant_dequant_heads_bit_exact(dev, shape, seed):
     assert_bf16_equal(bits16(y), O.fp8_dequant_heads(wc, ws))
 
 
+@pytest.mark.parametrize("two_pass", [False, True])
+@pytest.mark.parametrize("shape", [(4, 1, 3, 16), (2, 3, 2, 30720 * 8 + 5 * 16), (3, 7, 3, 4000),
+                                   (1, 1, 2, 64), (2, 300, 1, 16), (5, 2, 5, 61440 * 8)])
+def test_fp8_heads_single_and_two_pass(dev, shape, two_pass):
+    """Both quantiser paths against the oracle: runs split into several shares with a
+    ragged last one, more batches than shares, spare groups (more groups than slabs), a slab
+    needing more workgroups than the device has (falls back to two passes), several steps per
+    group; special values in one slab of every shape."""
+    n_outer, B, H, run = shape
+    g = torch.Generator().manual_seed(run + B)
+    x = (torch.randn((n_outer, B, H, run), generator=g) * torch.rand((n_outer, 1, H, 1), generator=g) * 9)
+    x[0, B - 1, H - 1, 3] = float("inf")
+    x[n_outer - 1, 0, 0, run - 1] = -3.0e4
+    x = x.to(torch.bfloat16)
+    err = torch.zeros(1, dtype=torch.int32)
+    codes, scales = kv.fp8_quant_heads(x.to(dev), two_pass=two_pass, check=True)
+    wc, ws = O.fp8_quant_heads(bits16(x))
+    np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+    np.testing.assert_array_equal(codes.cpu().numpy(), wc)
+    del err
+
+
+def test_fp8_heads_single_pass_at_size(dev):
+    """The bench's 1 Gi-element shape [64, 4, 8, 2^19]: single pass equal to the two-pass path
+    on every code and scale, and four whole slabs against the oracle."""
+    x = torch.randn((64, 4, 8, 1 << 19), device=dev, generator=torch.Generator(device=dev).manual_seed(4))
+    x = x.to(torch.bfloat16)
+    c1, s1 = kv.fp8_quant_heads(x, check=True)
+    c2, s2 = kv.fp8_quant_heads(x, two_pass=True)
+    assert torch.equal(s1.view(torch.int32), s2.view(torch.int32))
+    assert torch.equal(c1, c2)
+    for o, h in ((0, 0), (17, 3), (40, 7), (63, 5)):
+        wc, ws = O.fp8_quant_heads(bits16(x[o:o + 1, :, h:h + 1].contiguous()))
+        assert s1[o, h].cpu().numpy().view(np.uint32) == ws.view(np.uint32)[0, 0]
+        np.testing.assert_array_equal(c1[o:o + 1, :, h:h + 1].cpu().numpy(), wc)
+    del x, c1, c2
+    torch.cuda.empty_cache()
+
+
 def test_fp8_heads_special_slabs(dev):
     """Zero slab (scale clamps to 1e-8/448), +-inf slab, NaN slab, subnormal bf16 inputs."""
     x = torch.randn((4, 1, 4, 64), dtype=torch.float32).to(torch.bfloat16)
@@ -143,15 +182,17 @@ def test_kv_quant_append_static_scales_decode_positions(dev):
     L, H, D, P = 2, 4, 128, 16
     lens = [1, 1, 3]
     x, cu, bt, n_pages, sp = make_append_case(L, H, D, P, lens, seed=11, start=[15, 40, 7])
-    scales = torch.rand((L, 2, H), dtype=torch.float32) * 0.05 + 1e-3
+    scales = torch.rand((L, 2, H), dtype=torch.float32, generator=torch.Generator().manual_seed(12)) * 0.05 + 1e-3
     pool = torch.randint(0, 255, (L, n_pages, 2, H, P, D), dtype=torch.uint8)
     wpool = pool.numpy().copy()
     _, werr = O.kv_quant_append(bits16(x), cu.numpy(), sp.numpy(), bt.numpy(), wpool, P,
                                 scales=scales.numpy())
-    assert werr == 0
+    assert werr == 8  # N(0,1) tokens under scales down to 1e-3: some exceed 464 x their scale
     pool_d = pool.to(dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
     kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, scales=scales.to(dev),
-                       start_pos=sp.to(dev), static_scales=True, check=True)
+                       start_pos=sp.to(dev), static_scales=True, err=err)
+    assert int(err.item()) == werr
     np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
 
 
@@ -260,10 +301,12 @@ def test_kv_quant_append_static_special_scales(dev):
     pool = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8)
     wpool = pool.numpy().copy()
     _, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, P, scales=scales.numpy())
-    assert werr == 0
+    assert werr == 8  # the 1e-3 slab overflows; the +-inf and NaN slabs never flag
     pool_d = pool.to(dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
     kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, scales=scales.to(dev), static_scales=True,
-                       check=True)
+                       err=err)
+    assert int(err.item()) == werr
     np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
 
 

@@ -197,6 +197,65 @@ def test_paged_append_and_gather_match_brute_force_indexing():
         assert not kk[b, :, n:].any() and not vv[b, :, n:].any()
 
 
+def _small_tables(rng, lens, P):
+    B = len(lens)
+    maxb = max((n + P - 1) // P for n in lens)
+    n_pages = sum((n + P - 1) // P for n in lens) + 2
+    perm = rng.permutation(n_pages).astype(np.int32)
+    bt = np.full((B, maxb), -1, np.int32)
+    k = 0
+    for b, n in enumerate(lens):
+        nb = (n + P - 1) // P
+        bt[b, :nb] = perm[k:k + nb]
+        k += nb
+    return bt, n_pages
+
+
+@pytest.mark.parametrize("saturate", [False, True])
+def test_static_append_overflow_matches_torch(saturate):
+    """Static scales: a finite token beyond 464 |s| gets the torch cast's NaN code and
+    sets bit 8; with saturation it gets clamp(x / s, -448, 448)'s code instead.  Slabs
+    with a non-finite scale keep the plain cast either way.  Pinned by torch's division
+    and float8_e4m3fn cast (and torch.clamp for saturation)."""
+    rng = np.random.default_rng(11)
+    L, H, D, P = 2, 3, 64, 4
+    lens = [3, 6, 1]
+    bt, n_pages = _small_tables(rng, lens, P)
+    T = sum(lens)
+    x = torch.randn((L, T, 2, H, D), generator=torch.Generator().manual_seed(11)) * 8
+    x[0, 0, 0, 0, :4] = torch.tensor([float("inf"), -float("inf"), float("nan"), -3.0e4])
+    x[0, 1, 0, 1, :3] = torch.tensor([float("inf"), -float("inf"), float("nan")])  # negative scale below
+    x = x.to(torch.bfloat16)
+    x.view(torch.int16)[0, 2, 0, 1, 3] = -63  # 0xFFC1: a NaN with the sign bit set
+    sc = torch.tensor([[[0.01, -0.02, 0.5], [1.0, float("inf"), -0.004]],
+                       [[0.03, 2.0, -0.1], [0.007, 1e3, -1e-3]]], dtype=torch.float32)
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pool = np.zeros((L, n_pages, 2, H, P, D), np.uint8)
+    got_sc, err = O.kv_quant_append(xb, cu, None, bt, pool, P, scales=sc.numpy(), saturate=saturate)
+    np.testing.assert_array_equal(f32_bits(got_sc), f32_bits(sc.numpy()))  # static: unchanged
+    xf = x.float()
+    q = xf / sc[:, None, :, :, None]
+    finite = torch.isfinite(xf) & torch.isfinite(sc)[:, None, :, :, None]
+    plain = q.to(torch.float8_e4m3fn).view(torch.uint8)
+    over = finite & ((plain & 0x7F) == 0x7F)
+    assert over.any() and not over.all()
+    assert err == (8 if over.any() else 0)
+    codes = (torch.where(finite, q.clamp(-448.0, 448.0), q) if saturate else q).to(torch.float8_e4m3fn)
+    codes = codes.view(torch.uint8).numpy()
+    want = np.zeros_like(pool)
+    seq = np.repeat(np.arange(len(lens)), lens)
+    pos = np.concatenate([np.arange(n) for n in lens])
+    for l in range(L):
+        want[l, bt[seq, pos // P], :, :, pos % P, :] = codes[l]
+    np.testing.assert_array_equal(pool, want)
+    # dynamic scales never overflow a finite input
+    x2 = (torch.randn((L, T, 2, H, D), generator=torch.Generator().manual_seed(12)) * 1e4).to(torch.bfloat16)
+    pool2 = np.zeros_like(pool)
+    _, err2 = O.kv_quant_append(x2.view(torch.int16).numpy().view(np.uint16), cu, None, bt, pool2, P)
+    assert err2 == 0 and not ((pool2 & 0x7F) == 0x7F).any()
+
+
 # ------------------------------------------------------------------ legacy int8 vs torch
 
 def torch_reference_expr(x: torch.Tensor):

@@ -21,12 +21,14 @@ ZX_ERR_UNSUPPORTED = -3
 ZX_ERR_WORKSPACE = -4
 
 ZX_BF16, ZX_F16, ZX_F32 = 0, 1, 2
-ZX_KERR_PAGE_RANGE, ZX_KERR_POS_RANGE, ZX_KERR_SPIN = 1, 2, 4
+ZX_KERR_PAGE_RANGE, ZX_KERR_POS_RANGE, ZX_KERR_SPIN, ZX_KERR_OVERFLOW = 1, 2, 4, 8
 ZX_APPEND_STATIC_SCALES = 1
 ZX_APPEND_TWO_PASS = 2
+ZX_APPEND_SATURATE = 4
 ZX_PREFILL_MERGE, ZX_PREFILL_INIT, ZX_PREFILL_BF16 = 1, 2, 4
+ZX_HEADS_TWO_PASS = 1
 ZX_NEVER = 0x7FFFFFFF
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I64, _I32, _SZ, _INT = ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t, ctypes.c_int
@@ -40,7 +42,8 @@ SIGNATURES = {
     "zx_int8_legacy_quant_slabs_workspace_bytes": (_SZ, [_I64]),
     "zx_int8_legacy_quant_slabs": (_INT, [_P, _INT, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "zx_int8_legacy_dequant_slabs": (_INT, [_P, _P, _INT, _I64, _I64, _P, _P]),
-    "zx_fp8_quant_heads": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "zx_fp8_quant_heads_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
+    "zx_fp8_quant_heads": (_INT, [_P, _I64, _I64, _I64, _I64, _P, _P, _I32, _P, _P, _SZ, _P]),
     "zx_fp8_dequant_heads": (_INT, [_P, _P, _I64, _I64, _I64, _I64, _P, _P]),
     "zx_fp8_encode_f32": (_INT, [_P, _I64, _P, _P]),
     "zx_kv_scales": (_INT, [_P, _I64, _I32, _I64, _I32, _I32, _P, _P]),
@@ -51,6 +54,7 @@ SIGNATURES = {
                                     _P, _P, _P]),
     "zx_belady_argmax_workspace_bytes": (_SZ, [_I64]),
     "zx_belady_argmax": (_INT, [_P, _P, _I64, _P, _P, _SZ, _P]),
+    "zx_belady_update_slots": (_INT, [_P, _P, _I64, _P, _P, _P, _I64, _P, _P]),
     "zx_belady_next_use_workspace_bytes": (_SZ, [_I64, _I32]),
     "zx_belady_next_use": (_INT, [_P, _I64, _I32, _P, _P, _P, _P, _SZ, _P]),
     "zx_belady_simulate_workspace_bytes": (_SZ, [_I64, _I32]),

@@ -2,8 +2,7 @@
 
 Every translation unit is compiled to its own object (in parallel), then linked into
 zenyx_amd/lib/libzenyx_kv.so, which is written atomically so a concurrent loader never
-sees a half-written file.  The measurement programs under diag/ (HBM ceilings of the
-kernels' access patterns, quoted by the profiles) become executables in the same folder.
+sees a half-written file.
 """
 from __future__ import annotations
 
@@ -15,7 +14,6 @@ import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-DIAG = os.path.join(HERE, "diag")
 LIB_DIR = os.path.join(HERE, "lib")
 OBJ_DIR = os.path.join(LIB_DIR, "_build")
 LIB = os.path.join(LIB_DIR, "libzenyx_kv.so")
@@ -49,31 +47,15 @@ def _compile(src: str) -> str:
     return obj
 
 
-def _compile_diag(src: str) -> str:
-    exe = os.path.join(LIB_DIR, "zx_" + os.path.splitext(os.path.basename(src))[0])
-    tmp = exe + f".tmp{os.getpid()}"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, src]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, exe)
-    return exe
-
-
 def build(verbose: bool = False) -> str:
-    """Compile every csrc/*.hip and link libzenyx_kv.so (returns its path); build the
-    diag/*.hip measurement programs."""
+    """Compile every csrc/*.hip and link libzenyx_kv.so (returns its path)."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    diags = sorted(glob.glob(os.path.join(DIAG, "*.hip")))
-    workers = min(len(sources) + len(diags), max(1, (os.cpu_count() or 4) // 2), 8)
+    workers = min(len(sources), max(1, (os.cpu_count() or 4) // 2), 8)
     with cf.ThreadPoolExecutor(workers) as ex:
-        diag_jobs = [ex.submit(_compile_diag, d) for d in diags]
         objs = list(ex.map(_compile, sources))
-        for j in diag_jobs:
-            j.result()
     tmp = LIB + f".tmp{os.getpid()}"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -81,6 +81,21 @@ argmax_final_kernel(const Best *part, int n_part, int64_t *out) {
   }
 }
 
+// Slot updates of the drop-in cache: keys[slot[i]] = key[i], resident[slot[i]] = res[i]
+// (the host passes each slot once).  The update arrays may live in pinned host memory.
+__global__ void update_slots_kernel(int64_t *keys, uint8_t *resident, int64_t n_slots, const int64_t *slot,
+                                    const int64_t *key, const uint8_t *res, int64_t n, int32_t *err) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t s = slot[i];
+  if (s < 0 || s >= n_slots) {
+    if (err) atomicOr(err, ZX_KERR_PAGE_RANGE);
+    return;
+  }
+  keys[s] = key[i];
+  resident[s] = res[i];
+}
+
 static int argmax_blocks(int64_t n) {
   int64_t b = ceil_div(n, (int64_t)AM_THREADS * 8);
   if (b < 1) b = 1;
@@ -147,6 +162,18 @@ extern "C" int zx_belady_argmax(const int64_t *keys, const uint8_t *resident, in
   if (rc) return rc;
   argmax_final_kernel<<<1, AM_THREADS, 0, st>>>(part, nb, out);
   return check_launch("belady_argmax_final");
+}
+
+extern "C" int zx_belady_update_slots(int64_t *keys, uint8_t *resident, int64_t n_slots, const int64_t *slot,
+                                      const int64_t *key, const uint8_t *res, int64_t n, int32_t *err,
+                                      zx_stream_t stream) {
+  clear_error();
+  ZX_REQUIRE(n >= 0 && n_slots >= 0, "belady_update_slots: negative size");
+  if (n == 0) return ZX_OK;
+  ZX_REQUIRE(keys && resident && slot && key && res, "belady_update_slots: null pointer");
+  update_slots_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, as_stream(stream)>>>(keys, resident, n_slots, slot, key,
+                                                                                res, n, err);
+  return check_launch("belady_update_slots");
 }
 
 extern "C" size_t zx_belady_next_use_workspace_bytes(int64_t n, int32_t n_pages) {

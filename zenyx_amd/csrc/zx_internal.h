@@ -21,4 +21,11 @@ int append_fused(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, in
                  int32_t head_dim, const int64_t *tok_off, uint8_t *pool, int64_t pool_layer_stride,
                  int32_t page_size, float *scales, int32_t *err, void *ws, hipStream_t st);
 
+// Single-pass FP8 quantisation per (outer, head) slab (zx_heads_fused.hip).  Returns
+// ZX_ERR_UNSUPPORTED when the shape or the device does not allow it (the caller then uses
+// two passes).
+size_t heads_fused_workspace_bytes(int64_t n_outer, int64_t n_batch, int64_t n_heads, int64_t run);
+int heads_fused(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_heads, int64_t run, uint8_t *codes,
+                float *scales, int32_t *err, void *ws, size_t ws_bytes, hipStream_t st);
+
 }  // namespace zx

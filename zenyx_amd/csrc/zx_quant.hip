@@ -408,17 +408,58 @@ kv_amax_rows_kernel(const uint16_t *x, RowGeom8 g, uint32_t *amax_bits /* [L][2H
   if (c % g.lps == 0 && mx) atomicMax(&amax_bits[(int64_t)layer * g.n_slabs + c / g.lps], mx << 16);
 }
 
+// 0x80 in each byte of w whose low 7 bits are all set (an e4m3 NaN code), else 0.
+__device__ __forceinline__ uint32_t nan_code_bytes(uint32_t w) { return ((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u; }
+
+// NaN codes of 8 inputs v under a finite static scale (sign bit s_sign, 0 or 0x80).  The
+// code is the NaN code S.1111.111 when the quotient x / s is NaN or rounds beyond the e4m3
+// range; its sign is that of the IEEE quotient: the sign of x for a NaN x, else
+// sign(x) ^ sign(s).  (div_by_scale's correction step turns an infinite quotient into a
+// NaN whose sign is the device's default, so the sign is set here.)  A finite x with a
+// NaN code overflowed: MODE 1 flags it, MODE 2 also stores +-448 (S.1111.110).  The
+// per-element look runs only when some code is a NaN code.
+template <int MODE>
+__device__ __forceinline__ uint2 static_overflow(uint4 v, uint2 cd, uint32_t s_sign, int32_t *err) {
+  if (!(nan_code_bytes(cd.x) | nan_code_bytes(cd.y))) return cd;
+  const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+  uint32_t c[2] = {cd.x, cd.y};
+  bool hit = false;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t bits = (in[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+    const uint32_t mag = bits & 0x7FFFu, x_sign = (bits >> 8) & 0x80u;
+    const int sh = 8 * (k & 3);
+    const uint32_t code = (c[k >> 2] >> sh) & 0xFFu;
+    if ((code & 0x7Fu) == 0x7Fu) {
+      const uint32_t sign = mag > 0x7F80u ? x_sign : (x_sign ^ s_sign);
+      uint32_t fixed = sign | 0x7Fu;
+      if (mag < 0x7F80u) {
+        hit = true;
+        if (MODE == 2) fixed = sign | 0x7Eu;
+      }
+      c[k >> 2] = (c[k >> 2] & ~(0xFFu << sh)) | (fixed << sh);
+    }
+  }
+  if (hit && err) atomicOr(err, ZX_KERR_OVERFLOW);
+  return make_uint2(c[0], c[1]);
+}
+
 // Pass 2: encode and scatter.  Block b takes rows [r0, r0 + U*rpb) with tiles taken from
 // the end of the batch first.  A row without a page (tok_off < 0) is not stored.
-template <int U>
+// MODE 0: dynamic scales (no code can overflow, and a slab holding a non-finite input has a
+// non-finite scale); 1: static scales, NaN codes signed as the IEEE quotient and overflow
+// flagged in *err; 2: as 1, with overflow saturated.
+template <int U, int MODE>
 __global__ void __launch_bounds__(1024)
 kv_quant_rows_kernel(const uint16_t *x, RowGeom8 g, const int64_t *tok_off, const float *scales,
-                     uint8_t *pool, int64_t pool_layer_stride, int32_t page_size, int32_t head_dim) {
+                     uint8_t *pool, int64_t pool_layer_stride, int32_t page_size, int32_t head_dim, int32_t *err) {
   const int t = threadIdx.x;
   const int c = t % g.vpr8, rs = t / g.vpr8;
   const int slab = c / g.lps;
   const int layer = blockIdx.y;
-  const QuantScale q = quant_scale(scales[(int64_t)layer * g.n_slabs + slab]);
+  const float sc = scales[(int64_t)layer * g.n_slabs + slab];
+  const QuantScale q = quant_scale(sc);
+  const uint32_t s_sign = (__float_as_uint(sc) >> 24) & 0x80u;
   const int64_t tile = (int64_t)gridDim.x - 1 - blockIdx.x;
   const int64_t r0 = tile * U * g.rpb;
   const char *xl = reinterpret_cast<const char *>(x + (int64_t)layer * g.x_layer_stride);
@@ -438,7 +479,8 @@ kv_quant_rows_kernel(const uint16_t *x, RowGeom8 g, const int64_t *tok_off, cons
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     if (off[k] < 0) continue;
-    const uint2 cd = quant8(v[k], q);
+    uint2 cd = quant8(v[k], q);
+    if (MODE != 0 && q.nan_fix == 0) cd = static_overflow<MODE>(v[k], cd, s_sign, err);
     typedef unsigned int v2u __attribute__((ext_vector_type(2)));
     const v2u w2 = {cd.x, cd.y};
     __builtin_nontemporal_store(w2, reinterpret_cast<v2u *>(pl + off[k]));
@@ -631,15 +673,34 @@ extern "C" int zx_int8_legacy_dequant(const int8_t *q, const void *scale, int sc
   return legacy_dequant_any(q, scale, scale_dtype, 1, n, y, as_stream(stream), "int8_legacy_dequant");
 }
 
+extern "C" size_t zx_fp8_quant_heads_workspace_bytes(int64_t n_outer, int64_t n_batch, int64_t n_heads,
+                                                     int64_t run) {
+  return heads_fused_workspace_bytes(n_outer, n_batch, n_heads, run);
+}
+
 extern "C" int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_heads,
-                                  int64_t run, uint8_t *codes, float *scales, zx_stream_t stream) {
+                                  int64_t run, uint8_t *codes, float *scales, int32_t flags, int32_t *err,
+                                  void *workspace, size_t workspace_bytes, zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(x && codes && scales, "fp8_quant_heads: null pointer");
+  ZX_REQUIRE(!(flags & ~ZX_HEADS_TWO_PASS), "fp8_quant_heads: unknown flag bits 0x%x", (unsigned)flags);
   HeadsGeom g;
   int64_t nb;
   int rc = heads_geom(n_outer, n_batch, n_heads, run, g, nb);
   if (rc) return rc;
   hipStream_t st = as_stream(stream);
+  // Below the 256 MiB Infinity Cache the two passes' second read is served from it and two
+  // passes are faster (MI355X: 0.069 vs 0.091 ms at configs[0]'s 151 MB); above it the
+  // single pass saves the second HBM read (1 Gi elements: 0.66 vs 1.02 ms).
+  const bool large = (double)n_outer * n_batch * n_heads * run * 2 >= (double)(256 << 20);
+  if (!(flags & ZX_HEADS_TWO_PASS) && large) {
+    const size_t need = heads_fused_workspace_bytes(n_outer, n_batch, n_heads, run);
+    if (!workspace || workspace_bytes < need)
+      return fail(ZX_ERR_WORKSPACE, "fp8_quant_heads: workspace %zu < %zu bytes", workspace_bytes, need);
+    rc = heads_fused(x, n_outer, n_batch, n_heads, run, codes, scales, err, workspace, workspace_bytes, st);
+    if (rc != ZX_ERR_UNSUPPORTED) return rc;
+    clear_error();  // shape or device outside the single pass: two passes below
+  }
   int64_t ns = n_outer * n_heads;
   if ((rc = fill_u32(reinterpret_cast<uint32_t *>(scales), ns, 0, st))) return rc;
   heads_amax_kernel<<<(unsigned)nb, QH_THREADS, 0, st>>>(reinterpret_cast<const uint4 *>(x), g,
@@ -711,6 +772,8 @@ extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int
   size_t need = zx_kv_quant_append_workspace_bytes(n_layers, n_tok, n_heads, head_dim);
   if (!workspace || workspace_bytes < need)
     return fail(ZX_ERR_WORKSPACE, "kv_quant_append: workspace %zu < %zu bytes", workspace_bytes, need);
+  ZX_REQUIRE(!(flags & ~(ZX_APPEND_STATIC_SCALES | ZX_APPEND_TWO_PASS | ZX_APPEND_SATURATE)),
+             "kv_quant_append: unknown flag bits 0x%x", (unsigned)flags);
   hipStream_t st = as_stream(stream);
   const bool dynamic = !(flags & ZX_APPEND_STATIC_SCALES);
   if (n_tok == 0) return dynamic ? kv_scales_impl(x, g, n_layers, scales, st) : ZX_OK;
@@ -730,8 +793,17 @@ extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int
   const RowGeom8 r = row_geom8(g);
   const int64_t tiles = ceil_div(n_tok, (int64_t)KQ_U * r.rpb);
   if (tiles >= (1LL << 31)) return fail(ZX_ERR_UNSUPPORTED, "kv_quant_append: too many rows");
-  kv_quant_rows_kernel<KQ_U><<<dim3((unsigned)tiles, n_layers), r.vpr8 * r.rpb, 0, st>>>(
-      x, r, tok_off, scales, pool, pool_layer_stride, page_size, head_dim);
+  const dim3 grid((unsigned)tiles, n_layers);
+  const int threads = r.vpr8 * r.rpb;
+  if (dynamic)
+    kv_quant_rows_kernel<KQ_U, 0><<<grid, threads, 0, st>>>(x, r, tok_off, scales, pool, pool_layer_stride,
+                                                            page_size, head_dim, err);
+  else if (flags & ZX_APPEND_SATURATE)
+    kv_quant_rows_kernel<KQ_U, 2><<<grid, threads, 0, st>>>(x, r, tok_off, scales, pool, pool_layer_stride,
+                                                            page_size, head_dim, err);
+  else
+    kv_quant_rows_kernel<KQ_U, 1><<<grid, threads, 0, st>>>(x, r, tok_off, scales, pool, pool_layer_stride,
+                                                            page_size, head_dim, err);
   return check_launch("kv_quant_rows");
 }
 

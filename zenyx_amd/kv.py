@@ -29,18 +29,26 @@ def _err_word(device) -> torch.Tensor:
     return torch.zeros(1, dtype=torch.int32, device=device)
 
 
+def kernel_error_text(e: int) -> str:
+    """The ZX_KERR_* bits of a device error word, in words."""
+    parts = []
+    if e & N.ZX_KERR_PAGE_RANGE:
+        parts.append("block table entry outside [0, n_pages)")
+    if e & N.ZX_KERR_POS_RANGE:
+        parts.append("token position beyond max_blocks * page_size (attention: or a query row beyond "
+                     "max_q_per_seq)")
+    if e & N.ZX_KERR_SPIN:
+        parts.append("bounded wait ran out")
+    if e & N.ZX_KERR_OVERFLOW:
+        parts.append("a token exceeds 464 x its static FP8 scale (stored as the NaN code, or as +-448 when "
+                     "saturating)")
+    return "; ".join(parts)
+
+
 def _raise_kernel_error(err: torch.Tensor, what: str) -> None:
     e = int(err.item())
     if e:
-        parts = []
-        if e & N.ZX_KERR_PAGE_RANGE:
-            parts.append("block table entry outside [0, n_pages)")
-        if e & N.ZX_KERR_POS_RANGE:
-            parts.append("token position beyond max_blocks * page_size (attention: or a query row beyond "
-                         "max_q_per_seq)")
-        if e & N.ZX_KERR_SPIN:
-            parts.append("bounded wait ran out")
-        raise ValueError(f"{what}: " + "; ".join(parts))
+        raise ValueError(f"{what}: " + kernel_error_text(e))
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
@@ -125,9 +133,10 @@ def int8_legacy_dequant_slabs(q: torch.Tensor, scales: torch.Tensor) -> torch.Te
 
 # ------------------------------------------------------------------ FP8 per head
 
-def fp8_quant_heads(x: torch.Tensor):
+def fp8_quant_heads(x: torch.Tensor, two_pass: bool = False, check: bool = False):
     """x: bf16 ``[n_outer, n_batch, n_heads, run]`` -> (codes uint8 same shape, scales
-    fp32 ``[n_outer, n_heads]``), one scale per (outer, head)."""
+    fp32 ``[n_outer, n_heads]``), one scale per (outer, head).  The single-pass kernel reads
+    x once; ``two_pass`` forces the amax pass + encode pass (same results)."""
     N.ensure_gpu()
     if x.dtype != torch.bfloat16 or x.dim() != 4:
         raise ValueError("fp8_quant_heads: x must be bf16 [n_outer, n_batch, n_heads, run]")
@@ -135,8 +144,14 @@ def fp8_quant_heads(x: torch.Tensor):
     O, B, H, R = x.shape
     codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
     scales = torch.empty((O, H), dtype=torch.float32, device=x.device)
-    N.check(N.load().zx_fp8_quant_heads(N.ptr(x), O, B, H, R, N.ptr(codes), N.ptr(scales),
-                                        N.stream_ptr(x.device)), "fp8_quant_heads")
+    lib = N.load()
+    ws = None if two_pass else _workspace(lib.zx_fp8_quant_heads_workspace_bytes(O, B, H, R), x.device)
+    err = _err_word(x.device)
+    N.check(lib.zx_fp8_quant_heads(N.ptr(x), O, B, H, R, N.ptr(codes), N.ptr(scales),
+                                   N.ZX_HEADS_TWO_PASS if two_pass else 0, N.ptr(err), N.ptr(ws),
+                                   0 if ws is None else ws.numel(), N.stream_ptr(x.device)), "fp8_quant_heads")
+    if check:
+        _raise_kernel_error(err, "fp8_quant_heads")
     return codes, scales
 
 
@@ -195,13 +210,17 @@ def kv_scales(x: torch.Tensor) -> torch.Tensor:
 def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: torch.Tensor,
                     pool: torch.Tensor, scales: torch.Tensor | None = None,
                     start_pos: torch.Tensor | None = None, static_scales: bool = False,
-                    check: bool = False, two_pass: bool = False) -> torch.Tensor:
+                    check: bool = False, two_pass: bool = False, saturate: bool = False,
+                    err: torch.Tensor | None = None) -> torch.Tensor:
     """Paged append with fused FP8 quantisation.
 
     x ``[L, n_tok, 2, H, D]`` bf16; cu_seqlens int32 ``[B+1]``; block_tables int32
     ``[B, max_blocks]``; pool uint8 ``[L, n_pages, 2, H, P, D]`` (written in place).
     Without ``static_scales`` the scales are computed from this batch and written into
-    ``scales`` (allocated if None); returns the scales ``[L, 2, H]``.
+    ``scales`` (allocated if None); returns the scales ``[L, 2, H]``.  With static scales a
+    token beyond 464 x its scale is stored as the NaN code and flags an overflow, or as
+    +-448 with ``saturate``.  ``err`` (device int32 ``[1]``) collects the kernels' error
+    bits across calls (a fresh word by default); ``check`` reads it and raises.
     """
     N.ensure_gpu()
     x = _layers(x)
@@ -229,10 +248,16 @@ def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: tor
     for name, t in (("x", x), ("cu_seqlens", cu_seqlens), ("block_tables", block_tables), ("pool", pool),
                     ("scales", scales)) + ((("start_pos", start_pos),) if start_pos is not None else ()):
         N.require_device(t, name)
+    if saturate and not static_scales:
+        raise ValueError("saturate applies to static scales (dynamic scales never overflow)")
     lib = N.load()
     ws = _workspace(lib.zx_kv_quant_append_workspace_bytes(L, T, H, D), x.device)
-    err = _err_word(x.device)
-    flags = (N.ZX_APPEND_STATIC_SCALES if static_scales else 0) | (N.ZX_APPEND_TWO_PASS if two_pass else 0)
+    if err is None:
+        err = _err_word(x.device)
+    elif err.dtype != torch.int32 or err.numel() < 1 or err.device != x.device:
+        raise ValueError("err must be an int32 tensor on x's device")
+    flags = (N.ZX_APPEND_STATIC_SCALES if static_scales else 0) | (N.ZX_APPEND_TWO_PASS if two_pass else 0) | \
+        (N.ZX_APPEND_SATURATE if saturate else 0)
     N.check(lib.zx_kv_quant_append(N.ptr(x), T * 2 * H * D, L, T, H, D, N.ptr(cu_seqlens), N.ptr(start_pos),
                                    block_tables.shape[0], N.ptr(block_tables), block_tables.shape[1], P,
                                    N.ptr(pool), pool[0].numel(), n_pages, N.ptr(scales), flags, N.ptr(err),

@@ -59,9 +59,46 @@ def _copy(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) -> No
                                        ctypes.c_void_p(stream.cuda_stream), None), "tier copy")
 
 
+class _HostKeepAlive:
+    """Host tensors read by copies still queued on a stream.
+
+    A copy issued through hipMemcpyAsync is invisible to torch's pinned-memory caching
+    allocator, which would hand a freed pinned block to the next pin_memory() request
+    (another tier move, a DataLoader) while the DMA still reads it.  Each source is held
+    here with an event recorded after its copy and dropped once the event has completed;
+    completed entries are released whenever a new one is added or ``release_done`` runs.
+    """
+
+    _pending: list = []  # (event, tensor), in the order the copies were queued
+
+    @classmethod
+    def hold(cls, tensor: torch.Tensor, stream: torch.cuda.Stream) -> None:
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        cls.release_done()
+        cls._pending.append((ev, tensor))
+
+    @classmethod
+    def release_done(cls) -> None:
+        cls._pending = [(ev, t) for ev, t in cls._pending if not ev.query()]
+
+    @classmethod
+    def release_all(cls) -> None:
+        for ev, _ in cls._pending:
+            ev.synchronize()
+        cls._pending = []
+
+
+def keep_host_alive(tensor: torch.Tensor, stream: torch.cuda.Stream) -> None:
+    """Keep ``tensor`` (the host side of a copy just queued on ``stream``) referenced until
+    that copy has run."""
+    _HostKeepAlive.hold(tensor, stream)
+
+
 def to_device(cpu_tensor: torch.Tensor, device: torch.device) -> torch.Tensor:
     """Host tensor -> new device tensor, copied on the side stream, ordered before any later
-    work on the caller's current stream."""
+    work on the caller's current stream.  The host tensor stays referenced until the copy
+    has run, so the caller may drop it at once."""
     N.ensure_gpu()
     src = cpu_tensor.contiguous()
     cur = torch.cuda.current_stream(device)
@@ -69,6 +106,7 @@ def to_device(cpu_tensor: torch.Tensor, device: torch.device) -> torch.Tensor:
     out = torch.empty(src.shape, dtype=src.dtype, device=device)
     side.wait_stream(cur)
     _copy(out, src, side)
+    keep_host_alive(src, side)
     out.record_stream(side)
     cur.wait_stream(side)
     return out
@@ -138,9 +176,11 @@ class KVTierManager:
         reads them."""
         if device is not None:
             _SideStream.get(torch.device(device)).synchronize()
+            _HostKeepAlive.release_done()
             return
         for s in list(_SideStream._streams.values()):
             s.synchronize()
+        _HostKeepAlive.release_done()
 
     def _evict_t0_if_needed(self) -> None:  # :57-61, least recently used first
         while len(self.t0) > self.t0_capacity:
@@ -161,4 +201,4 @@ def build_ring_timeline(num_blocks: int) -> dict[str, list[int]]:
     return {"forward": forward, "backward": backward}
 
 
-__all__ = ["KVTierManager", "KVBlockRef", "build_ring_timeline"]
+__all__ = ["KVTierManager", "KVBlockRef", "build_ring_timeline", "keep_host_alive"]

@@ -26,6 +26,7 @@ import torch
 
 from .. import _native as N
 from .. import kv
+from .kv_tiering import keep_host_alive
 
 
 @dataclass
@@ -113,6 +114,7 @@ class LayerWeightStreamer:
         self._side.wait_stream(cur)  # `out` may reuse memory the current stream just freed
         if nbytes:
             kv.tier_copy_runs(out, host, [0], [0], nbytes, stream=self._side)
+            keep_host_alive(host, self._side)  # a temporary pinned copy must outlive the DMA
         out.record_stream(self._side)
         done.record(self._side)
         return out, done

@@ -42,15 +42,16 @@ class RingAttentionAccessSequence:
     def __len__(self) -> int:
         return 2 * self.num_layers * self.ring_degree * self.ring_degree * self.pages_per_shard
 
-    def trace(self, device: torch.device | str = "cpu") -> torch.Tensor:
-        """int32 page ids, forward then backward."""
+    def trace(self, device: torch.device | str | None = None) -> torch.Tensor:
+        """int32 page ids, forward then backward: layer l's page of shard k, index i is
+        (l R + k) S + i.  Built on the GPU by zx_ring_curriculum_trace as one step of
+        constant degree R over R S pages per layer (shard k of that step is exactly pages
+        [k S, (k + 1) S)); ``device="cpu"`` returns a host copy."""
         L, R, S = self.num_layers, self.ring_degree, self.pages_per_shard
-        step = torch.arange(R, device=device).view(R, 1)
-        dev = torch.arange(R, device=device).view(1, R)
-        shard = (dev - step) % R  # [step, device]
-        base = (torch.arange(L, device=device).view(L, 1, 1, 1) * R + shard.view(1, R, R, 1)) * S
-        fwd = (base + torch.arange(S, device=device).view(1, 1, 1, S)).reshape(-1).to(torch.int32)
-        return torch.cat([fwd, fwd.flip(0)])
+        dev = torch.device(device) if device is not None else N.ensure_gpu()
+        gdev = dev if dev.type == "cuda" else N.ensure_gpu()
+        t = kv.ring_curriculum_trace([R], [R * S], L, R * S, device=gdev)
+        return t if dev.type == "cuda" else t.cpu()
 
 
 class BeladyKVCacheTieringManager:
@@ -123,17 +124,22 @@ class BeladyKVCacheTieringManager:
 
     def replay_transfers(self, t_begin: int, t_end: int, compute=None, max_pool_pages: int | None = None) -> dict:
         """Execute the window's tier moves with real page buffers: a device pool and a pinned
-        host pool, page p in device slot p % slots and host slot rank(p).  Copies run on a
-        side stream; ``compute`` (a callable launching kernels on the current stream) runs
-        concurrently.  Returns bytes moved and times."""
+        host pool with one slot per page the window moves (page p in slot rank(p) on both
+        sides).  All D2H copies are queued, then all H2D copies, on a side stream; ``compute``
+        (a callable launching kernels on the current stream) runs concurrently.  Returns
+        bytes moved and times.  ``max_pool_pages`` below the window's page count is refused:
+        pages would share slots and overwrite each other (ThreeTierReplay schedules slots
+        access by access for windows larger than the pool)."""
         dev = self.device or N.ensure_gpu()
         d2h, h2d = self.transfers(t_begin, t_end)
         # batch the window's moves in page order: adjacent pages have adjacent slots on both
         # sides, so zx_tier_copy_runs merges them into few large copies
         d2h, h2d = np.sort(d2h), np.sort(h2d)
         pages = np.unique(np.concatenate([d2h, h2d]))
-        slots = len(pages) if max_pool_pages is None else min(len(pages), max_pool_pages)
-        slots = max(slots, 1)
+        if max_pool_pages is not None and max_pool_pages < len(pages):
+            raise ValueError(f"the window moves {len(pages)} distinct pages, more than max_pool_pages="
+                             f"{max_pool_pages} device slots")
+        slots = max(len(pages), 1)
         host_rank = {int(p): i for i, p in enumerate(pages)}
         pb = self.page_bytes
         dev_pool = torch.empty(slots * pb, dtype=torch.uint8, device=dev)
@@ -144,7 +150,7 @@ class BeladyKVCacheTieringManager:
         def offs(ids, on_host):
             if on_host:
                 return (ctypes.c_int64 * len(ids))(*[host_rank[int(p)] * pb for p in ids])
-            return (ctypes.c_int64 * len(ids))(*[(host_rank[int(p)] % slots) * pb for p in ids])
+            return (ctypes.c_int64 * len(ids))(*[host_rank[int(p)] * pb for p in ids])
 
         cur = torch.cuda.current_stream(dev)
         side.wait_stream(cur)

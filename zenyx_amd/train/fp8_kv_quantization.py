@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import torch
 
+from .. import _native as N
 from .. import kv
 from .._native import ensure_gpu
 
@@ -49,56 +50,109 @@ class FP8KVQuantizer:
 
 
 class PagedFP8KVCache:
-    """Paged FP8 KV cache with fused quantize+append and gather+dequant."""
+    """Paged FP8 KV cache with fused quantize+append and gather+dequant.
+
+    The first append computes the per-(layer, kv, head) scales from its tokens (prefill);
+    later appends reuse them (decode), so pages written earlier keep decoding with the
+    scale they were encoded with.  A later token beyond 464 x its slab's scale does not fit
+    e4m3: with ``overflow="raise"`` (default) it is stored as the NaN code, as the torch
+    cast would, and the next checked call raises; with ``overflow="saturate"`` it is
+    stored as +-448 and counted in ``saturated_appends``.  Kernel error bits (bad page ids,
+    positions, overflow, a timed-out wait) accumulate in one device word, read without an
+    extra synchronisation by the calls that synchronise anyway (``check_errors``, the
+    attention calls, ``append(check=True)``)."""
 
     def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, num_pages: int,
-                 page_size: int = 16, device: torch.device | None = None):
+                 page_size: int = 16, device: torch.device | None = None, overflow: str = "raise"):
+        if overflow not in ("raise", "saturate"):
+            raise ValueError('overflow must be "raise" or "saturate"')
         self.device = device or ensure_gpu()
         self.L, self.H, self.D, self.P = num_layers, num_kv_heads, head_dim, page_size
         self.num_pages = num_pages
+        self.overflow = overflow
         self.pool = torch.zeros((num_layers, num_pages, 2, num_kv_heads, page_size, head_dim),
                                 dtype=torch.uint8, device=self.device)
         self.scales = torch.ones((num_layers, 2, num_kv_heads), dtype=torch.float32, device=self.device)
         self.has_scales = False
+        self.err = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.saturated_appends = 0
         self._free = list(range(num_pages - 1, -1, -1))
         self.pages: dict = {}    # seq id -> list of page ids
         self.lengths: dict = {}  # seq id -> tokens stored
 
-    def _reserve(self, seq_id, new_len: int) -> None:
+    def _reserve(self, seq_id, new_len: int, taken: list) -> None:
         pages = self.pages.setdefault(seq_id, [])
         need = -(-new_len // self.P)
         while len(pages) < need:
             if not self._free:
                 raise MemoryError("PagedFP8KVCache: out of pages")
-            pages.append(self._free.pop())
+            p = self._free.pop()
+            pages.append(p)
+            taken.append((seq_id, p))
+
+    def _release(self, taken: list) -> None:
+        for seq_id, p in reversed(taken):
+            self.pages[seq_id].remove(p)
+            if not self.pages[seq_id]:
+                del self.pages[seq_id]
+            self._free.append(p)
 
     def _tables(self, seq_ids) -> torch.Tensor:
         width = max(1, max(len(self.pages.get(s, [])) for s in seq_ids))
         rows = [self.pages.get(s, []) + [-1] * (width - len(self.pages.get(s, []))) for s in seq_ids]
         return torch.tensor(rows, dtype=torch.int32).to(self.device)
 
-    def append(self, x: torch.Tensor, seq_ids: list, lengths: list[int], dynamic_scales: bool | None = None):
+    def append(self, x: torch.Tensor, seq_ids: list, lengths: list[int], dynamic_scales: bool | None = None,
+               check: bool = False):
         """Append new tokens of several sequences.  x: ``[L, n_tok, 2, H, D]`` bf16, tokens of
         sequence ``seq_ids[i]`` packed in order with ``lengths[i]`` tokens each.  Scales are
-        computed from this batch on the first append (or when ``dynamic_scales``) and reused
-        otherwise, so earlier pages keep decoding correctly."""
+        computed from this batch on the first append and reused afterwards (static); asking
+        for dynamic scales once pages hold tokens is refused, since it would change the
+        scale of pages already written.  ``check`` synchronises and raises on any kernel
+        error bit (see ``check_errors``)."""
         if sum(lengths) != x.shape[1]:
             raise ValueError("sum(lengths) must equal x.shape[1]")
-        start = [self.lengths.get(s, 0) for s in seq_ids]
-        for s, st, n in zip(seq_ids, start, lengths):
-            self._reserve(s, st + n)
-        cu = [0]
-        for n in lengths:
-            cu.append(cu[-1] + n)
+        stored = any(n > 0 for n in self.lengths.values())
         dyn = (not self.has_scales) if dynamic_scales is None else dynamic_scales
-        kv.kv_quant_append(x.to(self.device), torch.tensor(cu, dtype=torch.int32).to(self.device),
-                           self._tables(seq_ids), self.pool, scales=self.scales,
-                           start_pos=torch.tensor(start, dtype=torch.int32).to(self.device),
-                           static_scales=not dyn)
+        if dyn and stored:
+            raise ValueError("dynamic scales on a cache that already holds tokens would re-scale pages written "
+                             "with the old scales; free the sequences first")
+        start = [self.lengths.get(s, 0) for s in seq_ids]
+        taken: list = []
+        try:
+            for s, st, n in zip(seq_ids, start, lengths):
+                self._reserve(s, st + n, taken)
+            cu = [0]
+            for n in lengths:
+                cu.append(cu[-1] + n)
+            kv.kv_quant_append(x.to(self.device), torch.tensor(cu, dtype=torch.int32).to(self.device),
+                               self._tables(seq_ids), self.pool, scales=self.scales,
+                               start_pos=torch.tensor(start, dtype=torch.int32).to(self.device),
+                               static_scales=not dyn, saturate=(not dyn) and self.overflow == "saturate",
+                               err=self.err)
+        except BaseException:
+            self._release(taken)
+            raise
         self.has_scales = True
         for s, st, n in zip(seq_ids, start, lengths):
             self.lengths[s] = st + n
+        if check:
+            self.check_errors()
         return self.scales
+
+    def check_errors(self) -> None:
+        """Read (and clear) the cache's device error word; raise ValueError for any bit, except
+        an overflow in ``overflow="saturate"`` mode, which only counts ``saturated_appends``.
+        Synchronises with the cache's device."""
+        e = int(self.err.item())
+        if not e:
+            return
+        self.err.zero_()
+        if self.overflow == "saturate" and e & N.ZX_KERR_OVERFLOW:
+            self.saturated_appends += 1
+            e &= ~N.ZX_KERR_OVERFLOW
+        if e:
+            raise ValueError("PagedFP8KVCache: " + kv.kernel_error_text(e))
 
     def gather(self, layer: int, seq_ids: list, out_len: int | None = None):
         """bf16 ``(k, v)``, each ``[B, H, out_len, D]``, of one layer for decode; positions past a
@@ -148,18 +202,22 @@ class QuantizedRingAttention:
         for n in q_lens:
             cu.append(cu[-1] + n)
         dev = c.device
-        return kv.ring_attention_fp8(
+        out = kv.ring_attention_fp8(
             q.to(dev).contiguous(), torch.tensor(cu, dtype=torch.int32).to(dev),
             torch.tensor([m - n for n, m in zip(q_lens, lens)], dtype=torch.int32).to(dev), c.pool[layer],
             c.scales[layer].contiguous(), c._tables(seq_ids), torch.tensor(lens, dtype=torch.int32).to(dev),
             ring_degree=self.ring_degree, causal=self.causal, sm_scale=self.sm_scale, check=True)
+        c.check_errors()  # the appends behind these pages (the check above has synchronised)
+        return out
 
     def decode(self, q: torch.Tensor, layer: int, seq_ids: list) -> torch.Tensor:
         """q ``[B, Hq, D]`` bf16, one query token per sequence over all its cached tokens."""
         c = self.cache
         lens = torch.tensor([c.lengths.get(s, 0) for s in seq_ids], dtype=torch.int32).to(c.device)
-        return kv.paged_attention_decode(q.to(c.device).contiguous(), c.pool[layer], c.scales[layer].contiguous(),
-                                         c._tables(seq_ids), lens, sm_scale=self.sm_scale, check=True)
+        out = kv.paged_attention_decode(q.to(c.device).contiguous(), c.pool[layer], c.scales[layer].contiguous(),
+                                        c._tables(seq_ids), lens, sm_scale=self.sm_scale, check=True)
+        c.check_errors()
+        return out
 
 
 __all__ = ["FP8KVQuantizer", "PagedFP8KVCache", "QuantizedRingAttention"]
