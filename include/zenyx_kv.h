@@ -169,6 +169,25 @@ int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_laye
                        int32_t flags, int32_t *err, void *workspace, size_t workspace_bytes,
                        zx_stream_t stream);
 
+/* zx_kv_quant_append without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, semantics and results
+ * as zx_kv_quant_append; its scratch is a fixed array of
+ * ZX_KV_APPEND_NOALLOC_SCRATCH_BYTES in the library's code object, one per GPU, held
+ * until the process ends (its address is looked up once per device, on the first call).
+ * A call whose zx_kv_quant_append_workspace_bytes() exceeds it fails with
+ * ZX_ERR_WORKSPACE before launching anything (at 8 heads, D = 128 and 32 layers: up to
+ * about 980,000 tokens).  Calls no allocating routine.  Every call on one GPU uses the
+ * same scratch: calls that overlap on one GPU (different streams, or host threads) race;
+ * calls in one stream are ordered. */
+#define ZX_KV_APPEND_NOALLOC_SCRATCH_BYTES (8u << 20)
+int zx_kv_quant_append_noalloc(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
+                               int64_t n_tok, int32_t n_heads, int32_t head_dim,
+                               const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
+                               const int32_t *block_tables, int32_t max_blocks, int32_t page_size,
+                               uint8_t *pool, int64_t pool_layer_stride, int64_t n_pages, float *scales,
+                               int32_t flags, int32_t *err, zx_stream_t stream);
+
 /* Paged gather + dequant for decode of one layer.
  * scales: the layer's [2][H] fp32.  Output k_out, v_out: [n_seqs][H][out_len][D] bf16;
  * positions t >= seq_lens[b] are written as zeros, as are rows whose page id is out of

@@ -50,6 +50,8 @@ SIGNATURES = {
     "zx_kv_quant_append_workspace_bytes": (_SZ, [_I32, _I64, _I32, _I32]),
     "zx_kv_quant_append": (_INT, [_P, _I64, _I32, _I64, _I32, _I32, _P, _P, _I32, _P, _I32, _I32,
                                   _P, _I64, _I64, _P, _I32, _P, _P, _SZ, _P]),
+    "zx_kv_quant_append_noalloc": (_INT, [_P, _I64, _I32, _I64, _I32, _I32, _P, _P, _I32, _P, _I32, _I32,
+                                          _P, _I64, _I64, _P, _I32, _P, _P]),
     "zx_kv_gather_dequant": (_INT, [_P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _P,
                                     _P, _P, _P]),
     "zx_belady_argmax_workspace_bytes": (_SZ, [_I64]),

@@ -4,6 +4,8 @@
 //   * per-(layer, kv, head) scales and the paged append with fused quant
 // Every kernel streams 16-byte vectors; all are HBM-bound (no MFMA: nothing here is a
 // contraction).
+#include <mutex>
+
 #include "zx_internal.h"
 
 namespace zx {
@@ -747,14 +749,17 @@ extern "C" size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n
          append_fused_workspace_bytes(n_layers, n_heads);
 }
 
-extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
-                                  int64_t n_tok, int32_t n_heads, int32_t head_dim,
-                                  const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
-                                  const int32_t *block_tables, int32_t max_blocks, int32_t page_size,
-                                  uint8_t *pool, int64_t pool_layer_stride, int64_t n_pages,
-                                  float *scales, int32_t flags, int32_t *err, void *workspace,
-                                  size_t workspace_bytes, zx_stream_t stream) {
-  clear_error();
+namespace {
+// The body of zx_kv_quant_append and zx_kv_quant_append_noalloc: argument checks, token
+// offsets, then the single-pass kernel or the two passes.  Launches kernels only (no
+// allocation); everything the workspace must hold at the start is written by kernels on
+// `st` (token offsets, the single pass's slots and abort flag), so a workspace's old
+// contents never matter.
+int kv_quant_append_impl(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, int64_t n_tok, int32_t n_heads,
+                         int32_t head_dim, const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
+                         const int32_t *block_tables, int32_t max_blocks, int32_t page_size, uint8_t *pool,
+                         int64_t pool_layer_stride, int64_t n_pages, float *scales, int32_t flags, int32_t *err,
+                         void *workspace, size_t workspace_bytes, hipStream_t st) {
   ZX_REQUIRE(scales && cu_seqlens && block_tables && pool, "kv_quant_append: null pointer");
   ZX_REQUIRE(x || n_tok == 0, "kv_quant_append: null x");
   ZX_REQUIRE(n_layers > 0 && n_layers <= 65535, "kv_quant_append: n_layers out of range");
@@ -774,7 +779,6 @@ extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int
     return fail(ZX_ERR_WORKSPACE, "kv_quant_append: workspace %zu < %zu bytes", workspace_bytes, need);
   ZX_REQUIRE(!(flags & ~(ZX_APPEND_STATIC_SCALES | ZX_APPEND_TWO_PASS | ZX_APPEND_SATURATE)),
              "kv_quant_append: unknown flag bits 0x%x", (unsigned)flags);
-  hipStream_t st = as_stream(stream);
   const bool dynamic = !(flags & ZX_APPEND_STATIC_SCALES);
   if (n_tok == 0) return dynamic ? kv_scales_impl(x, g, n_layers, scales, st) : ZX_OK;
   int64_t *tok_off = reinterpret_cast<int64_t *>(workspace);
@@ -805,6 +809,63 @@ extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int
     kv_quant_rows_kernel<KQ_U, 1><<<grid, threads, 0, st>>>(x, r, tok_off, scales, pool, pool_layer_stride,
                                                             page_size, head_dim, err);
   return check_launch("kv_quant_rows");
+}
+
+// Scratch of zx_kv_quant_append_noalloc: one copy per GPU, in the code object (no
+// allocation call).  Its host-side name is not a device address: kernels get the address
+// hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) uint8_t scratch[ZX_KV_APPEND_NOALLOC_SCRATCH_BYTES];
+
+int noalloc_scratch(void **out) {
+  static std::mutex mu;
+  static void *ptr[64] = {nullptr};
+  int dev = 0;
+  ZX_TRY_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(ZX_ERR_UNSUPPORTED, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void *p = nullptr;
+    ZX_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(ZX_ERR_HIP, "hipGetSymbolAddress returned no address for the append scratch");
+    ptr[dev] = p;
+  }
+  *out = ptr[dev];
+  return ZX_OK;
+}
+}  // namespace
+
+extern "C" int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
+                                  int64_t n_tok, int32_t n_heads, int32_t head_dim,
+                                  const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
+                                  const int32_t *block_tables, int32_t max_blocks, int32_t page_size,
+                                  uint8_t *pool, int64_t pool_layer_stride, int64_t n_pages,
+                                  float *scales, int32_t flags, int32_t *err, void *workspace,
+                                  size_t workspace_bytes, zx_stream_t stream) {
+  clear_error();
+  return kv_quant_append_impl(x, x_layer_stride, n_layers, n_tok, n_heads, head_dim, cu_seqlens, start_pos, n_seqs,
+                              block_tables, max_blocks, page_size, pool, pool_layer_stride, n_pages, scales, flags,
+                              err, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int zx_kv_quant_append_noalloc(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
+                                          int64_t n_tok, int32_t n_heads, int32_t head_dim,
+                                          const int32_t *cu_seqlens, const int32_t *start_pos, int32_t n_seqs,
+                                          const int32_t *block_tables, int32_t max_blocks, int32_t page_size,
+                                          uint8_t *pool, int64_t pool_layer_stride, int64_t n_pages, float *scales,
+                                          int32_t flags, int32_t *err, zx_stream_t stream) {
+  clear_error();
+  const size_t need = zx_kv_quant_append_workspace_bytes(n_layers, n_tok, n_heads, head_dim);
+  if (n_tok < 0 || need > (size_t)ZX_KV_APPEND_NOALLOC_SCRATCH_BYTES)
+    return fail(ZX_ERR_WORKSPACE,
+                "kv_quant_append_noalloc: this call needs %zu bytes of scratch, more than the %u bytes it has "
+                "(use zx_kv_quant_append with a workspace)",
+                need, (unsigned)ZX_KV_APPEND_NOALLOC_SCRATCH_BYTES);
+  void *ws = nullptr;
+  int rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  return kv_quant_append_impl(x, x_layer_stride, n_layers, n_tok, n_heads, head_dim, cu_seqlens, start_pos, n_seqs,
+                              block_tables, max_blocks, page_size, pool, pool_layer_stride, n_pages, scales, flags,
+                              err, ws, ZX_KV_APPEND_NOALLOC_SCRATCH_BYTES, as_stream(stream));
 }
 
 namespace zx {
