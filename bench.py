@@ -230,8 +230,24 @@ def belady_leg(torch, dev, skip_cpu):
            "evictions": ev, "misses": stats["misses"], "hits": stats["hits"],
            "simulate_ms": round(sim_s * 1e3, 3), "next_use_ms": round(nu_s * 1e3, 3),
            "evictions_per_s": round(ev / sim_s, 1)}
+    # the next-use tables alone (zx_belady_next_use: radix sort of the trace by page, then
+    # neighbours), HIP events on the compute stream, median of 5 after a warm-up
+    from zenyx_amd import kv
+    trace_d = m.sim.trace
+    kv.next_use(trace_d, m.n_pages)
+    nu_ms = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        kv.next_use(trace_d, m.n_pages)
+        e1.record()
+        torch.cuda.synchronize(dev)
+        nu_ms.append(e0.elapsed_time(e1))
+    out["next_use_kernels_ms"] = round(sorted(nu_ms)[2], 3)
+    out["next_use_note"] = ("next_use_ms times the whole BeladyTraceSim set-up (tables, state, eviction lists) on the "
+                            "host clock; next_use_kernels_ms the radix sort and neighbour kernels alone")
     log(f"belady: {ev} evictions in {sim_s * 1e3:.1f} ms -> {ev / sim_s / 1e6:.2f} M evictions/s "
-        f"(next-use tables {nu_s * 1e3:.1f} ms)")
+        f"(set-up with next-use tables {nu_s * 1e3:.1f} ms; next-use kernels {out['next_use_kernels_ms']} ms)")
     # tier moves of one backward layer while a dequant-gather runs on the compute stream
     n = len(m.sequence)
     per_layer = n // 2 // 80
@@ -240,21 +256,24 @@ def belady_leg(torch, dev, skip_cpu):
     bt = torch.randperm(8192, device=dev)[:64 * 128].to(torch.int32).view(64, 128)
     sl = torch.full((64,), 2048, dtype=torch.int32, device=dev)
     sc = torch.full((2, 8), 0.01, dtype=torch.float32, device=dev)
-    from zenyx_amd import kv
 
     def compute():
         for _ in range(20):
             kv.kv_gather_dequant(pool, sc, bt, sl, 2048)
 
+    # two windows: the backward of layer 39 brings spilled pages back (H2D); the forward of
+    # layer 50 evicts pages that the backward will use again (D2H)
+    windows = {"backward_layer39": t_a, "forward_layer50": 50 * per_layer}
     m.replay_transfers(t_a, t_a + per_layer)  # warm-up: pinned pools, copy engines
-    r = m.replay_transfers(t_a, t_a + per_layer, compute=compute)
-    out["tier_moves"] = {"window": f"backward of layer 39: trace positions [{t_a}, {t_a + per_layer})",
-                         "d2h_pages": r["d2h_pages"], "h2d_pages": r["h2d_pages"],
-                         "d2h_GBps": round(r["d2h_GBps"], 2), "h2d_GBps": round(r["h2d_GBps"], 2),
-                         "overlapped_with": "20 paged gather+dequant kernels on the compute stream",
-                         "wall_ms": round(r["wall_ms"], 3)}
-    log(f"tier moves: {r['d2h_pages']} D2H pages at {r['d2h_GBps']:.1f} GB/s, {r['h2d_pages']} H2D pages at "
-        f"{r['h2d_GBps']:.1f} GB/s")
+    out["tier_moves"] = {}
+    for name, a in windows.items():
+        r = m.replay_transfers(a, a + per_layer, compute=compute)
+        out["tier_moves"][name] = {
+            "window": f"trace positions [{a}, {a + per_layer})", "d2h_pages": r["d2h_pages"],
+            "h2d_pages": r["h2d_pages"], "d2h_GBps": round(r["d2h_GBps"], 2), "h2d_GBps": round(r["h2d_GBps"], 2),
+            "overlapped_with": "20 paged gather+dequant kernels on the compute stream", "wall_ms": round(r["wall_ms"], 3)}
+        log(f"tier moves, {name}: {r['d2h_pages']} D2H pages at {r['d2h_GBps']:.1f} GB/s, {r['h2d_pages']} H2D pages "
+            f"at {r['h2d_GBps']:.1f} GB/s")
     out["dropin_cache"] = dropin_belady_leg(torch, dev, m.capacity, len(m.sequence))
     out["curriculum"] = curriculum_leg(torch, dev, skip_cpu)
     if not skip_cpu:

@@ -106,13 +106,27 @@ def test_belady_argmax_matches_oracle(dev):
 
 
 def test_next_use_matches_oracle(dev):
+    """The hand-written radix sort behind next_use: 1 to 4 passes of 7-bit digits, lengths
+    that end mid-tile, one page accessed everywhere (one digit holds every element), and
+    skewed traces."""
     rng = np.random.default_rng(9)
-    for n, n_pages in ((1, 1), (50, 3), (100_000, 777), (300_000, 1 << 17)):
+    cases = [(1, 1), (50, 3), (4097, 2), (100_000, 777), (300_000, 1 << 17), (12_345, 1 << 14),
+             (70_001, 1 << 21), (5_000, 1 << 25)]
+    for n, n_pages in cases:
         trace = rng.integers(0, n_pages, n).astype(np.int32)
         nu, pu = kv.next_use(torch.from_numpy(trace).to(dev), n_pages, check=True)
         wnu, wpu = O.next_use(trace, n_pages)
         np.testing.assert_array_equal(nu.cpu().numpy(), wnu)
         np.testing.assert_array_equal(pu.cpu().numpy(), wpu)
+    for trace, n_pages in ((np.full(50_000, 7, np.int32), 9),
+                           ((rng.zipf(1.3, 200_000) % 5000).astype(np.int32), 5000)):
+        nu, pu = kv.next_use(torch.from_numpy(trace).to(dev), n_pages, check=True)
+        wnu, wpu = O.next_use(trace, n_pages)
+        np.testing.assert_array_equal(nu.cpu().numpy(), wnu)
+        np.testing.assert_array_equal(pu.cpu().numpy(), wpu)
+    bad = torch.tensor([0, 3, -1, 2, 3], dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError, match="block table entry outside"):
+        kv.next_use(bad, 4, check=True)
     ring = O.ring_trace(2, 8, 16)
     nu, pu = kv.next_use(torch.from_numpy(ring).to(dev), 2 * 8 * 16)
     wnu, wpu = O.next_use(ring, 2 * 8 * 16)

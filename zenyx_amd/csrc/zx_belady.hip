@@ -1,7 +1,5 @@
 // zx_belady.hip -- Belady victim selection (zenyx/streaming/belady.py:39-51) and the
 // next-use tables it needs.  The trace-level simulator lives in zx_belady_sim.hip.
-#include <hipcub/hipcub.hpp>
-
 #include "zx_internal.h"
 
 namespace zx {
@@ -105,13 +103,196 @@ static int argmax_blocks(int64_t n) {
 
 // ------------------------------------------------------------------ next use
 
-__global__ void iota_check_kernel(const int32_t *trace, int64_t n, int32_t n_pages, int32_t *pos,
-                                  int32_t *err) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  pos[i] = (int32_t)i;
-  int32_t p = trace[i];
-  if ((p < 0 || p >= n_pages) && err) atomicOr(err, ZX_KERR_PAGE_RANGE);
+// next_use / prev_use come from the trace sorted by page, stably (positions of one page
+// stay in trace order): neighbours with the same page are consecutive uses.  The sort is an
+// LSD radix sort of (page, position) pairs with 7-bit digits, ceil(bits(n_pages) / 7)
+// passes, each:
+//   1. rs_hist_kernel: per tile of RS_TILE elements, the count of every digit, stored
+//      digit-major (hist[d * n_tiles + tile]);
+//   2. an exclusive scan of that table (rs_scan_*): the output position where digit d's
+//      elements of each tile start;
+//   3. rs_scatter_kernel: each tile ranks its elements stably within their digit and
+//      writes (page, position) to the scanned start plus the rank.
+// Ranking in a tile runs in RS_ITEMS rounds of 256 consecutive elements (one per thread,
+// loads coalesced).  In a round, the lanes of a wave holding the same digit find each other
+// with 7 ballots (their rank in the wave = the peers below them); each wave's count per
+// digit goes to LDS, and an element's rank in the tile = (count of its digit in earlier
+// rounds) + (count in earlier waves of this round) + (rank in its wave).
+constexpr int RS_BITS = 7;
+constexpr int RS_RADIX = 1 << RS_BITS;
+constexpr int RS_THREADS = 256;
+constexpr int RS_WAVES = RS_THREADS / 64;
+constexpr int RS_ITEMS = 16;
+constexpr int RS_TILE = RS_THREADS * RS_ITEMS;
+constexpr int RS_SCAN_CHUNK = 4096;  // entries of the digit table per scan block
+
+__global__ void __launch_bounds__(RS_THREADS)
+rs_hist_kernel(const int32_t *keys, int64_t n, int shift, int32_t n_pages, uint32_t *hist, int64_t n_tiles,
+               int32_t *err) {
+  __shared__ uint32_t cnt[RS_RADIX];
+  if (threadIdx.x < RS_RADIX) cnt[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * RS_TILE;
+  bool bad = false;
+#pragma unroll 4
+  for (int r = 0; r < RS_ITEMS; ++r) {
+    const int64_t e = base + r * RS_THREADS + threadIdx.x;
+    if (e < n) {
+      const int32_t k = keys[e];
+      bad |= k < 0 || k >= n_pages;
+      atomicAdd(&cnt[((uint32_t)k >> shift) & (RS_RADIX - 1)], 1u);
+    }
+  }
+  if (err && shift == 0 && __ballot(bad) && (threadIdx.x & 63) == 0) atomicOr(err, ZX_KERR_PAGE_RANGE);
+  __syncthreads();
+  if (threadIdx.x < RS_RADIX) hist[(int64_t)threadIdx.x * n_tiles + blockIdx.x] = cnt[threadIdx.x];
+}
+
+// Exclusive scan of m entries: block sums of RS_SCAN_CHUNK-entry chunks, a one-block scan of
+// those, then each chunk rescanned from its base (in place).
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t &total) {
+  __shared__ uint32_t wsum[RS_WAVES];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  uint32_t x = v;  // inclusive scan inside the wave
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) wsum[wid] = x;
+  __syncthreads();
+  uint32_t before = 0;
+  total = 0;
+  for (int w = 0; w < RS_WAVES; ++w) {
+    before += w < wid ? wsum[w] : 0u;
+    total += wsum[w];
+  }
+  __syncthreads();
+  return before + x - v;
+}
+
+__global__ void __launch_bounds__(RS_THREADS) rs_scan_sums_kernel(const uint32_t *a, int64_t m, uint32_t *sums) {
+  const int64_t c0 = (int64_t)blockIdx.x * RS_SCAN_CHUNK;
+  uint32_t s = 0;
+  for (int i = threadIdx.x; i < RS_SCAN_CHUNK; i += RS_THREADS)
+    if (c0 + i < m) s += a[c0 + i];
+  uint32_t total;
+  block_excl_scan(s, total);
+  if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+__global__ void __launch_bounds__(RS_THREADS) rs_scan_top_kernel(uint32_t *sums, int64_t n_chunks) {
+  uint32_t carry = 0;  // one block walks the chunk sums RS_THREADS at a time
+  for (int64_t i0 = 0; i0 < n_chunks; i0 += RS_THREADS) {
+    const int64_t i = i0 + threadIdx.x;
+    const uint32_t v = i < n_chunks ? sums[i] : 0u;
+    uint32_t total;
+    const uint32_t ex = block_excl_scan(v, total);
+    if (i < n_chunks) sums[i] = carry + ex;
+    carry += total;
+  }
+}
+
+__global__ void __launch_bounds__(RS_THREADS)
+rs_scan_chunks_kernel(uint32_t *a, int64_t m, const uint32_t *sums) {
+  const int64_t c0 = (int64_t)blockIdx.x * RS_SCAN_CHUNK;
+  constexpr int PER = RS_SCAN_CHUNK / RS_THREADS;  // consecutive entries per thread
+  uint32_t v[PER], s = 0;
+  const int64_t i0 = c0 + (int64_t)threadIdx.x * PER;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    v[k] = i0 + k < m ? a[i0 + k] : 0u;
+    s += v[k];
+  }
+  uint32_t total;
+  uint32_t run = sums[blockIdx.x] + block_excl_scan(s, total);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    if (i0 + k < m) a[i0 + k] = run;
+    run += v[k];
+  }
+}
+
+// vals_in == nullptr: the values are the element indices (the first pass).  The tile is
+// ranked, staged in LDS in digit order, then written out: the elements of one digit go to
+// consecutive output positions, so neighbouring threads write neighbouring words.
+__global__ void __launch_bounds__(RS_THREADS)
+rs_scatter_kernel(const int32_t *keys_in, const int32_t *vals_in, int64_t n, int shift, const uint32_t *offs,
+                  int64_t n_tiles, int32_t *keys_out, int32_t *vals_out) {
+  __shared__ uint32_t gstart[RS_RADIX];              // output position of the tile's first element of digit d
+  __shared__ uint32_t lstart[RS_RADIX];              // its position in the tile's digit order
+  __shared__ uint32_t run[RS_RADIX];                 // elements of digit d ranked so far (earlier rounds)
+  __shared__ uint32_t wcnt[2][RS_WAVES][RS_RADIX];   // per round (parity), per wave, per digit
+  __shared__ int32_t lk[RS_TILE], lv[RS_TILE];       // the tile in digit order
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t base = (int64_t)blockIdx.x * RS_TILE;
+  const int tile_n = (int)min((int64_t)RS_TILE, n - base);
+  uint32_t cnt = 0;
+  if (threadIdx.x < RS_RADIX) {
+    // digit-major exclusive scan: the next entry is this tile's start plus its count
+    const int64_t i = (int64_t)threadIdx.x * n_tiles + blockIdx.x;
+    const uint32_t st = offs[i];
+    const uint32_t nx = i + 1 < n_tiles * RS_RADIX ? offs[i + 1] : (uint32_t)n;
+    gstart[threadIdx.x] = st;
+    cnt = nx - st;
+    run[threadIdx.x] = 0;
+  }
+  for (int i = threadIdx.x; i < 2 * RS_WAVES * RS_RADIX; i += RS_THREADS) (&wcnt[0][0][0])[i] = 0;
+  uint32_t total;
+  const uint32_t ex = block_excl_scan(threadIdx.x < RS_RADIX ? cnt : 0u, total);  // synchronises
+  if (threadIdx.x < RS_RADIX) lstart[threadIdx.x] = ex;
+  __syncthreads();
+  const uint64_t below = (1ull << lane) - 1;
+  int led[2] = {-1, -1};  // digit this lane led two rounds ago, per parity (its entry to clear)
+  for (int r = 0; r < RS_ITEMS; ++r) {
+    const int par = r & 1;
+    const int e = r * RS_THREADS + threadIdx.x;  // element of the tile
+    const bool valid = e < tile_n;
+    const int32_t k = valid ? keys_in[base + e] : 0;
+    const int32_t v = valid ? (vals_in ? vals_in[base + e] : (int32_t)(base + e)) : 0;
+    const uint32_t d = ((uint32_t)k >> shift) & (RS_RADIX - 1);
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < RS_BITS; ++b) {
+      const uint64_t ones = __ballot((d >> b) & 1u);
+      peers &= ((d >> b) & 1u) ? ones : ~ones;
+    }
+    const uint32_t rank_w = (uint32_t)__popcll(peers & below);
+    // clear what this lane wrote two rounds ago (every wave has read it since), then
+    // publish this round's count of the digit for the wave
+    if (led[par] >= 0) wcnt[par][wid][led[par]] = 0;
+    led[par] = -1;
+    if (valid && rank_w == 0) {
+      wcnt[par][wid][d] = (uint32_t)__popcll(peers);
+      led[par] = (int)d;
+    }
+    __syncthreads();
+    if (valid) {
+      uint32_t pos = lstart[d] + run[d] + rank_w;
+      for (int w = 0; w < wid; ++w) pos += wcnt[par][w][d];
+      lk[pos] = k;
+      lv[pos] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < RS_RADIX) {  // the round's elements of digit d follow earlier rounds'
+      uint32_t c = 0;
+      for (int w = 0; w < RS_WAVES; ++w) c += wcnt[par][w][threadIdx.x];
+      run[threadIdx.x] += c;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < tile_n; i += RS_THREADS) {
+    const int32_t k = lk[i];
+    const uint32_t d = ((uint32_t)k >> shift) & (RS_RADIX - 1);
+    const uint32_t pos = gstart[d] + (uint32_t)i - lstart[d];
+    keys_out[pos] = k;
+    vals_out[pos] = lv[i];
+  }
+}
+
+static int key_bits(int32_t n_pages) {
+  int b = 1;
+  while (b < 31 && (1LL << b) < (int64_t)n_pages) ++b;
+  return b;
 }
 
 __global__ void next_use_kernel(const int32_t *skey, const int32_t *spos, int64_t n, int32_t *next_use,
@@ -123,20 +304,29 @@ __global__ void next_use_kernel(const int32_t *skey, const int32_t *spos, int64_
   prev_use[pos] = (k > 0 && skey[k - 1] == p) ? spos[k - 1] : -1;
 }
 
-static int key_bits(int32_t n_pages) {
-  int b = 1;
-  while (b < 31 && (1LL << b) < (int64_t)n_pages) ++b;
-  return b;
-}
+// Workspace: keys and positions twice (ping-pong), the digit table, the scan's chunk sums.
+struct NextUseWs {
+  int32_t *k[2], *v[2];
+  uint32_t *hist, *sums;
+  int64_t n_tiles, m, n_chunks;
+  size_t bytes;
+};
 
-
-
-static size_t sort_temp_bytes(int64_t n, int32_t n_pages) {
-  size_t temp = 0;
-  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp, (const int32_t *)nullptr, (int32_t *)nullptr,
-                                     (const int32_t *)nullptr, (int32_t *)nullptr, (int)n, 0,
-                                     key_bits(n_pages));
-  return temp;
+static NextUseWs next_use_ws(void *base, int64_t n) {
+  NextUseWs w;
+  w.n_tiles = ceil_div(n, RS_TILE);
+  w.m = w.n_tiles * RS_RADIX;
+  w.n_chunks = ceil_div(w.m, RS_SCAN_CHUNK);
+  char *p = static_cast<char *>(base);
+  const size_t a = align256((size_t)n * 4);
+  for (int i = 0; i < 2; ++i) {
+    w.k[i] = reinterpret_cast<int32_t *>(p + (2 * i) * a);
+    w.v[i] = reinterpret_cast<int32_t *>(p + (2 * i + 1) * a);
+  }
+  w.hist = reinterpret_cast<uint32_t *>(p + 4 * a);
+  w.sums = reinterpret_cast<uint32_t *>(p + 4 * a + align256((size_t)w.m * 4));
+  w.bytes = 4 * a + align256((size_t)w.m * 4) + align256((size_t)w.n_chunks * 4);
+  return w;
 }
 
 }  // namespace zx
@@ -177,8 +367,9 @@ extern "C" int zx_belady_update_slots(int64_t *keys, uint8_t *resident, int64_t 
 }
 
 extern "C" size_t zx_belady_next_use_workspace_bytes(int64_t n, int32_t n_pages) {
+  (void)n_pages;
   if (n <= 0) return 256;
-  return 3 * align256((size_t)n * 4) + align256(sort_temp_bytes(n, n_pages > 0 ? n_pages : 1));
+  return next_use_ws(nullptr, n).bytes;
 }
 
 extern "C" int zx_belady_next_use(const int32_t *trace, int64_t n, int32_t n_pages, int32_t *next_use,
@@ -193,18 +384,26 @@ extern "C" int zx_belady_next_use(const int32_t *trace, int64_t n, int32_t n_pag
   if (!workspace || workspace_bytes < need)
     return fail(ZX_ERR_WORKSPACE, "belady_next_use: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t st = as_stream(stream);
-  char *ws = reinterpret_cast<char *>(workspace);
-  const size_t a = align256((size_t)n * 4);
-  int32_t *pos_in = reinterpret_cast<int32_t *>(ws);
-  int32_t *key_out = reinterpret_cast<int32_t *>(ws + a);
-  int32_t *pos_out = reinterpret_cast<int32_t *>(ws + 2 * a);
-  void *temp = ws + 3 * a;
-  size_t temp_bytes = need - 3 * a;
-  iota_check_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(trace, n, n_pages, pos_in, err);
-  int rc = check_launch("belady_iota");
-  if (rc) return rc;
-  ZX_TRY_HIP(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, trace, key_out, pos_in, pos_out, (int)n, 0,
-                                                key_bits(n_pages), st));
-  next_use_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(key_out, pos_out, n, next_use, prev_use);
+  const NextUseWs w = next_use_ws(workspace, n);
+  const int bits = key_bits(n_pages), passes = (bits + RS_BITS - 1) / RS_BITS;
+  const unsigned tiles = (unsigned)w.n_tiles;
+  int rc;
+  for (int p = 0; p < passes; ++p) {
+    const int shift = p * RS_BITS;
+    const int32_t *kin = p == 0 ? trace : w.k[(p + 1) & 1];
+    const int32_t *vin = p == 0 ? nullptr : w.v[(p + 1) & 1];
+    rs_hist_kernel<<<tiles, RS_THREADS, 0, st>>>(kin, n, shift, n_pages, w.hist, w.n_tiles, err);
+    if ((rc = check_launch("radix_hist"))) return rc;
+    rs_scan_sums_kernel<<<(unsigned)w.n_chunks, RS_THREADS, 0, st>>>(w.hist, w.m, w.sums);
+    if ((rc = check_launch("radix_scan_sums"))) return rc;
+    rs_scan_top_kernel<<<1, RS_THREADS, 0, st>>>(w.sums, w.n_chunks);
+    if ((rc = check_launch("radix_scan_top"))) return rc;
+    rs_scan_chunks_kernel<<<(unsigned)w.n_chunks, RS_THREADS, 0, st>>>(w.hist, w.m, w.sums);
+    if ((rc = check_launch("radix_scan_chunks"))) return rc;
+    rs_scatter_kernel<<<tiles, RS_THREADS, 0, st>>>(kin, vin, n, shift, w.hist, w.n_tiles, w.k[p & 1], w.v[p & 1]);
+    if ((rc = check_launch("radix_scatter"))) return rc;
+  }
+  const int last = (passes - 1) & 1;
+  next_use_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(w.k[last], w.v[last], n, next_use, prev_use);
   return check_launch("belady_next_use");
 }
