@@ -691,14 +691,16 @@ def ring_attention_leg(torch, dev, steps, warmup, skip_cpu):
            "useful_flop_per_step": flops,
            "note": "P.V runs twice on the matrix cores (P split into bf16 hi + lo), so the matrix cores execute "
                    "1.5x the useful flops"}
-    for ring in (1, 8):
-        fn = lambda: kv.ring_attention_fp8(q, cu, qp, pool, sc, bt, kl, ring_degree=ring, causal=True)  # noqa: E731
+    for key, ring, single in (("ring1", 1, True), ("ring8", 8, True), ("ring8_steps", 8, False)):
+        fn = lambda: kv.ring_attention_fp8(q, cu, qp, pool, sc, bt, kl, ring_degree=ring, causal=True,  # noqa: E731
+                                           single_launch=single)
         ms, _, _ = time_steps(torch, fn, steps, warmup)
         tf = flops / (ms * 1e-3) / 1e12
-        log(f"ring attention degree {ring}: {ms:.3f} ms/step, {tf:.1f} TFLOP/s "
+        how = "one launch walking the shards" if single else "one launch per shard, merged through HBM"
+        log(f"ring attention degree {ring} ({how}): {ms:.3f} ms/step, {tf:.1f} TFLOP/s "
             f"({100 * tf / MFMA_BF16_PEAK_TFLOPS:.1f}% of the bf16 MFMA peak)")
-        res[f"ring{ring}"] = {"ms_per_step": round(ms, 4), "TFLOPs": round(tf, 1),
-                              "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        res[key] = {"ms_per_step": round(ms, 4), "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "launches": "1" if single else str(ring)}
     if not skip_cpu:
         # the C oracle (double precision, one thread) on the last 16 query rows of sequence 0
         # (about 20 s on one host core)

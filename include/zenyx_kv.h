@@ -342,6 +342,13 @@ int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, i
  * attention over the union of the steps' key ranges.  Needs head_dim 128 and a page size
  * that is a multiple of 16. */
 enum { ZX_PREFILL_MERGE = 1, ZX_PREFILL_INIT = 2, ZX_PREFILL_BF16 = 4 };
+/* All R steps of a ring on one GPU in one launch: the same computation as R calls of
+ * zx_paged_attention_prefill over key ranges kv_begin[r * n_seqs + b], kv_end[r * n_seqs + b]
+ * (r < n_ranges, device int32), except that each block walks the ranges in order with the
+ * running row maxima, output and row sums in registers, so nothing is merged through
+ * memory between ranges; flags as above (MERGE then merges the union of the ranges into
+ * o_acc / lse2 once).  The ranges of a sequence should not overlap (a key in two ranges
+ * counts twice).  Within the same tolerance as the per-step composition. */
 int zx_paged_attention_prefill(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int32_t *q_pos0,
                                int32_t n_q_heads, const uint8_t *pool, int64_t n_pages, int32_t n_kv_heads,
                                int32_t head_dim, int32_t page_size, const float *scales,
@@ -349,6 +356,12 @@ int zx_paged_attention_prefill(const uint16_t *q, int64_t n_q, const int32_t *cu
                                const int32_t *kv_end, int32_t n_seqs, int32_t max_q_per_seq, int32_t causal,
                                float sm_scale, int32_t flags, float *o_acc, float *lse2, uint16_t *out,
                                int32_t *err, zx_stream_t stream);
+int zx_paged_attention_ring(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int32_t *q_pos0,
+                            int32_t n_q_heads, const uint8_t *pool, int64_t n_pages, int32_t n_kv_heads,
+                            int32_t head_dim, int32_t page_size, const float *scales, const int32_t *block_tables,
+                            int32_t max_blocks, const int32_t *kv_begin, const int32_t *kv_end, int32_t n_ranges,
+                            int32_t n_seqs, int32_t max_q_per_seq, int32_t causal, float sm_scale, int32_t flags,
+                            float *o_acc, float *lse2, uint16_t *out, int32_t *err, zx_stream_t stream);
 
 #ifdef __cplusplus
 }

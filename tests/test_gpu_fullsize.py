@@ -132,6 +132,9 @@ def test_ring_attention_bench_shape(dev):
     for ring in (1, 8):
         outs[ring] = kv.ring_attention_fp8(R["q"], R["cu"], R["q_pos0"], R["pool"], R["scales"], R["bt"],
                                            R["kv_len"], ring_degree=ring, causal=True, check=True)
+    # ring 8 as eight launches merged through the fp32 running output (the multi-GPU unit)
+    outs["8s"] = kv.ring_attention_fp8(R["q"], R["cu"], R["q_pos0"], R["pool"], R["scales"], R["bt"], R["kv_len"],
+                                       ring_degree=8, causal=True, check=True, single_launch=False)
     torch.cuda.synchronize()
     codes, bt, sc = R["codes"].numpy(), R["bt_host"].numpy(), R["scales_host"].numpy()
     dec = np.abs(O.e4m3_decode(np.arange(256, dtype=np.uint8)).astype(np.float64))
@@ -152,18 +155,20 @@ def test_ring_attention_bench_shape(dev):
                                                  np.zeros(1, np.int32), np.full(1, T, np.int32), True, sm)
         assert err == 0
         vm = np.repeat(vmax[b, :, row], grp, axis=0)[None]  # [1, Hq, D]
-        for ring in (1, 8):
+        for ring in (1, 8, "8s"):
             assert_within_one_ulp(bits16(outs[ring][i:i + 1]), want, vm)
-    print("ring 1 and 8: 6 rows x 32 heads within tolerance of the oracle", flush=True)
-    for b in range(R["B"]):  # one sequence at a time (float32 is exact for bf16 values and their differences)
-        a = outs[1][b * T:(b + 1) * T].float().cpu().numpy()
-        c = outs[8][b * T:(b + 1) * T].float().cpu().numpy()
-        vm_b = np.repeat(vmax[b], grp, axis=0).transpose(1, 0, 2).astype(np.float32)  # [T, Hq, D]
-        mag = np.maximum(np.maximum(np.abs(a), np.abs(c)), np.float32(2.0 ** -100))
-        tol = 2 * np.exp2(np.floor(np.log2(mag)) - 7) + np.float32(2.0 ** -16) * vm_b
-        bad = np.abs(a - c) > tol
-        assert not bad.any(), f"sequence {b}: {bad.sum()} elements of ring 8 differ from ring 1 beyond tolerance"
-    print("ring 8 == ring 1 within tolerance on all 33.5 M outputs", flush=True)
+    print("ring 1, ring 8 (one launch) and ring 8 (eight launches): 6 rows x 32 heads within tolerance of the "
+          "oracle", flush=True)
+    for other in (8, "8s"):
+        for b in range(R["B"]):  # one sequence at a time (float32 is exact for bf16 values and their differences)
+            a = outs[1][b * T:(b + 1) * T].float().cpu().numpy()
+            c = outs[other][b * T:(b + 1) * T].float().cpu().numpy()
+            vm_b = np.repeat(vmax[b], grp, axis=0).transpose(1, 0, 2).astype(np.float32)  # [T, Hq, D]
+            mag = np.maximum(np.maximum(np.abs(a), np.abs(c)), np.float32(2.0 ** -100))
+            tol = 2 * np.exp2(np.floor(np.log2(mag)) - 7) + np.float32(2.0 ** -16) * vm_b
+            bad = np.abs(a - c) > tol
+            assert not bad.any(), f"sequence {b}: {bad.sum()} elements of ring {other} differ from ring 1"
+        print(f"ring {other} == ring 1 within tolerance on all 33.5 M outputs", flush=True)
 
 
 def test_configs3_full_belady_schedule(dev):

@@ -111,15 +111,45 @@ def _ring_case():
     return _RING_CASE
 
 
+@pytest.mark.parametrize("single_launch", [True, False])
 @pytest.mark.parametrize("ring", [1, 3, 8])
-def test_ring_attention_equals_full_attention(ring):
+def test_ring_attention_equals_full_attention(ring, single_launch):
     c = _ring_case()
-    print(f"ring {ring}", flush=True)
+    print(f"ring {ring} single_launch={single_launch}", flush=True)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
     out = kv.ring_attention_fp8(c["q"].to(DEV), t(c["cu"]), t(c["qp"]), t(c["pool"]), t(c["scales"]), t(c["bt"]),
-                                t(c["lens"]), ring_degree=ring, causal=True, check=True)
+                                t(c["lens"]), ring_degree=ring, causal=True, check=True, single_launch=single_launch)
     torch.cuda.synchronize()
     assert_within_one_ulp(bits16(out), c["want"], c["vmax"])
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_ring_ranges_in_device_order(causal):
+    """zx_paged_attention_ring with the shards in the order one device of a ring of 5 sees
+    them (its own shard first, then (g - r) mod 5), uneven shards, an empty shard and a
+    range that starts mid-page: equal to attention over the union."""
+    c = _ring_case()
+    lens = c["lens"]
+    R, g = 5, 3
+    cuts = np.stack([np.array([0, 1, 2, 2, 4, 5]) * L // 5 for L in lens], axis=1)  # shard 2 empty
+    cuts[1] = np.minimum(cuts[1] + 7, cuts[2])  # uneven: shard 0 longer, starting mid-page for shard 1
+    order = [(g - r) % R for r in range(R)]
+    kb = np.stack([cuts[s] for s in order]).astype(np.int32)
+    ke = np.stack([cuts[s + 1] for s in order]).astype(np.int32)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    out = kv.paged_attention_ring(c["q"].to(DEV), t(c["cu"]), t(c["qp"]), t(c["pool"]), t(c["scales"]), t(c["bt"]),
+                                  t(kb), t(ke), causal=causal, check=True)
+    torch.cuda.synchronize()
+    if causal:
+        want, vmax = c["want"], c["vmax"]
+    else:
+        zeros = np.zeros(len(lens), np.int32)
+        sm = float(np.float32(1.0 / np.sqrt(128)))
+        want, _, err = O.paged_attention_prefill(bits16(c["q"]), c["cu"], c["qp"], c["pool"], c["scales"], c["bt"],
+                                                 zeros, lens, False, sm)
+        assert err == 0
+        vmax = c["vmax"]
+    assert_within_one_ulp(bits16(out), want, vmax)
 
 
 def test_prefill_flags_bad_pages():
@@ -200,11 +230,12 @@ def test_ring_degree_above_sequence_lengths():
     q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, lens, [0, 0, 0], lens, seed=17)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
     kl = np.asarray(lens, np.int32)
-    out = kv.ring_attention_fp8(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kl), ring_degree=8,
-                                causal=True, check=True)
-    torch.cuda.synchronize()
     sm = float(np.float32(1.0 / np.sqrt(128)))
     zeros = np.zeros(3, np.int32)
     want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, zeros, kl, True, sm)
     assert err == 0
-    assert_within_one_ulp(bits16(out), want, vmax_rows(pool, scales, bt, cu, zeros, kl, Hq))
+    for single in (True, False):
+        out = kv.ring_attention_fp8(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kl), ring_degree=8,
+                                    causal=True, check=True, single_launch=single)
+        torch.cuda.synchronize()
+        assert_within_one_ulp(bits16(out), want, vmax_rows(pool, scales, bt, cu, zeros, kl, Hq))

@@ -72,6 +72,8 @@ SIGNATURES = {
     "zx_ring_curriculum_trace": (_INT, [_P, _P, _I32, _I32, _I32, _P, _I64, _P]),
     "zx_paged_attention_prefill": (_INT, [_P, _I64, _P, _P, _I32, _P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P,
                                           _P, _I32, _I32, _I32, ctypes.c_float, _I32, _P, _P, _P, _P, _P]),
+    "zx_paged_attention_ring": (_INT, [_P, _I64, _P, _P, _I32, _P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P,
+                                       _P, _I32, _I32, _I32, _I32, ctypes.c_float, _I32, _P, _P, _P, _P, _P]),
 }
 
 _lib = None

@@ -42,13 +42,13 @@ struct PrefillArgs {
   const int32_t *cu_q, *q_pos0;
   const uint8_t *pool;
   const float *scales;  // [2][Hkv]
-  const int32_t *bt, *kv_begin, *kv_end;
+  const int32_t *bt, *kv_begin, *kv_end;  // [n_ranges][n_seqs] key ranges, walked in order
   float *o_acc;   // [n_q][Hq][128] fp32, normalised
   float *lse2;    // [n_q][Hq]
   uint16_t *out;  // [n_q][Hq][128] bf16 (PF_WRITE_BF16)
   int32_t *err;
   int64_t n_pages;
-  int32_t n_q_heads, n_kv_heads, page_size, max_blocks, mode, causal;
+  int32_t n_q_heads, n_kv_heads, page_size, max_blocks, mode, causal, n_ranges, n_seqs;
   uint32_t p_magic;
   int32_t p_shift;
   float sm_log2e;  // sm_scale * log2 e
@@ -93,19 +93,40 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   int32_t e = 0;
   // rows past gridDim.x * QT (max_q_per_seq too small) are not computed: flag it
   if (blockIdx.x == 0 && (int64_t)gridDim.x * QT < n_qb) e |= ZX_KERR_POS_RANGE;
-  const int kb = a.kv_begin[b] > 0 ? a.kv_begin[b] : 0;
-  int ke = a.kv_end[b];
   const int kmax = a.max_blocks * a.page_size;  // < 2^31 (checked by the host)
-  if (ke > kmax) {
-    e |= ZX_KERR_POS_RANGE;
-    ke = kmax;
-  }
   // keys past the block's last query position never count when causal
   const int last_row = min(row0_blk + QT, n_qb) - 1;
-  const int ke_blk = a.causal ? (int)max((int64_t)-1, min((int64_t)ke, qp0 + last_row + 1)) : ke;
-  const int s_first = (kb / 16) * 16;
-  if (ke_blk <= s_first && !(a.mode & (PF_INIT | PF_WRITE_BF16))) {
-    // no key of this step reaches the block's rows: merging would leave o_acc and lse2 as
+  // Range r of this sequence: keys [kb, ke) (ke clipped to the block table), walked in
+  // 64-key steps from s_first (kb rounded down to a 16-key tile) while below ke_blk (ke,
+  // or the block's last causal key + 1).  All block-uniform.
+  struct Range {
+    int kb, ke, s_first, ke_blk;
+  };
+  auto range = [&](int r) -> Range {
+    Range g;
+    const int64_t i = (int64_t)r * a.n_seqs + b;
+    g.kb = a.kv_begin[i] > 0 ? a.kv_begin[i] : 0;
+    g.ke = a.kv_end[i];
+    if (g.ke > kmax) {
+      e |= ZX_KERR_POS_RANGE;
+      g.ke = kmax;
+    }
+    g.ke_blk = a.causal ? (int)max((int64_t)-1, min((int64_t)g.ke, qp0 + last_row + 1)) : g.ke;
+    g.s_first = (g.kb / 16) * 16;
+    return g;
+  };
+  // the first range with a step at or after r (a.n_ranges if none)
+  auto next_range = [&](int r, Range &g) -> int {
+    for (; r < a.n_ranges; ++r) {
+      g = range(r);
+      if (g.s_first < g.ke_blk) return r;
+    }
+    return a.n_ranges;
+  };
+  Range cur;
+  int rc = next_range(0, cur);
+  if (rc == a.n_ranges && !(a.mode & (PF_INIT | PF_WRITE_BF16))) {
+    // no key of any range reaches the block's rows: merging would leave o_acc and lse2 as
     // they are (block-uniform exit)
     if (e && a.err && threadIdx.x == 0) atomicOr(a.err, e);
     return;
@@ -116,16 +137,17 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 
   // every page the block may load inside the pool? (then the steps skip the per-tile
   // block-table checks; otherwise tiles on bad pages count as masked)
-  bool all_ok = true;
-  if (s_first < ke) {
-    const int p_lo = (int)pf_page_of(a, (uint32_t)s_first), p_hi = (int)pf_page_of(a, (uint32_t)(ke - 1));
-    bool bad = false;
+  bool bad = false;
+  for (int r = 0; r < a.n_ranges; ++r) {
+    const Range g = range(r);
+    if (g.s_first >= g.ke) continue;
+    const int p_lo = (int)pf_page_of(a, (uint32_t)g.s_first), p_hi = (int)pf_page_of(a, (uint32_t)(g.ke - 1));
     for (int pi = p_lo + (int)threadIdx.x; pi <= p_hi; pi += PF_THREADS) {
       const int64_t pg = bt[pi];
       bad |= pg < 0 || pg >= a.n_pages;
     }
-    all_ok = !__syncthreads_or(bad);
   }
+  const bool all_ok = !__syncthreads_or(bad);
 
   // Q rows as the B operand of S^T = K . Q^T: lane (n, kg) of row tile rt holds row
   // wrow0 + 16 rt + n, channels 32 kg + 8 c ..+8 for MFMA c (the K operand's channel order)
@@ -166,13 +188,13 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   // tiles past the range or on a bad page load through zero-length resources
   const int kp2 = threadIdx.x >> 3, g8 = threadIdx.x & 7;
   const int kk0 = 2 * kp2;
-  auto tile_ok = [&](int tp) -> bool {  // uniform
+  auto tile_ok = [&](int tp, int ke) -> bool {  // uniform
     if (tp >= ke) return false;
     if (all_ok) return true;
     const int64_t page = bt[pf_page_of(a, (uint32_t)tp)];
     return page >= 0 && page < a.n_pages;
   };
-  auto load_step = [&](int s0, att_u32x4 (&kc)[2], att_u32x4 (&vc)[2]) {
+  auto load_step = [&](int s0, int ke, att_u32x4 (&kc)[2], att_u32x4 (&vc)[2]) {
     const int tp = s0 + 16 * wave;  // this wave's 16-key tile (scalar: the buffer resources stay in SGPRs)
     const int live = max(0, min(16, ke - tp));
     const int tc = tp < ke ? tp : (ke > 0 ? ke - 1 : 0);
@@ -217,10 +239,10 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 
   // one step: S^T, softmax, then the next step's K/V stored into the other LDS buffer
   // (free since the last barrier) ahead of the PV products so the two can overlap
-  auto compute_step = [&](int buf, int s0, const att_u32x4 (&kc)[2], const att_u32x4 (&vc)[2]) {
+  auto compute_step = [&](int buf, int s0, int kb, int ke, const att_u32x4 (&kc)[2], const att_u32x4 (&vc)[2]) {
     bool tok[4];
 #pragma unroll
-    for (int KT = 0; KT < 4; ++KT) tok[KT] = tile_ok(s0 + 16 * KT);
+    for (int KT = 0; KT < 4; ++KT) tok[KT] = tile_ok(s0 + 16 * KT, ke);
     // S^T tiles: sc[rt][KT] lane (n, kg) holds keys 16 KT + 4 kg + i of row 16 rt + n
     att_f32x4 sc[2][4];
 #pragma unroll
@@ -341,23 +363,32 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   };
 
   // steps: data of step s + 1 loaded into registers while step s computes; one barrier
-  // per step (the LDS buffers alternate).  The last step also loads and stores the step
-  // after it (zero-length loads past kv_end; that buffer is never read).
+  // per step (the LDS buffers alternate).  The steps of the ranges follow each other (the
+  // step after a range's last one is the next non-empty range's first), with the running
+  // row maxima, O and row sums carried in registers from range to range.  The last step
+  // also loads and stores a step after it (zero-length loads; that buffer is never read).
   att_u32x4 kc[2], vc[2];
-  int s0 = s_first;
-  if (s0 < ke_blk) {
-    load_step(s0, kc, vc);
+  int s0 = cur.s_first;
+  if (rc < a.n_ranges) {
+    load_step(s0, cur.ke, kc, vc);
     store_step(0, kc, vc);
   }
   __syncthreads();
   int buf = 0;
-  while (s0 < ke_blk) {
-    const int s1 = s0 + PF_KEYS;
-    load_step(s1, kc, vc);
-    compute_step(buf, s0, kc, vc);
+  while (rc < a.n_ranges) {
+    Range nxt = cur;
+    int rn = rc, s1 = s0 + PF_KEYS;
+    if (s1 >= cur.ke_blk) {
+      rn = next_range(rc + 1, nxt);
+      s1 = rn < a.n_ranges ? nxt.s_first : 0;
+    }
+    load_step(s1, rn < a.n_ranges ? nxt.ke : 0, kc, vc);
+    compute_step(buf, s0, cur.kb, cur.ke, kc, vc);
     __syncthreads();
     buf ^= 1;
     s0 = s1;
+    rc = rn;
+    cur = nxt;
   }
 
   // rows: normalise; merge; store channels 16 jt + 4 kg ..+4
@@ -411,16 +442,16 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 
 using namespace zx;
 
-extern "C" int zx_paged_attention_prefill(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int32_t *q_pos0,
-                                          int32_t n_q_heads, const uint8_t *pool, int64_t n_pages, int32_t n_kv_heads,
-                                          int32_t head_dim, int32_t page_size, const float *scales,
-                                          const int32_t *block_tables, int32_t max_blocks, const int32_t *kv_begin,
-                                          const int32_t *kv_end, int32_t n_seqs, int32_t max_q_per_seq,
-                                          int32_t causal, float sm_scale, int32_t flags, float *o_acc, float *lse2,
-                                          uint16_t *out, int32_t *err, zx_stream_t stream) {
-  clear_error();
+namespace {
+int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int32_t *q_pos0, int32_t n_q_heads,
+                 const uint8_t *pool, int64_t n_pages, int32_t n_kv_heads, int32_t head_dim, int32_t page_size,
+                 const float *scales, const int32_t *block_tables, int32_t max_blocks, const int32_t *kv_begin,
+                 const int32_t *kv_end, int32_t n_ranges, int32_t n_seqs, int32_t max_q_per_seq, int32_t causal,
+                 float sm_scale, int32_t flags, float *o_acc, float *lse2, uint16_t *out, int32_t *err,
+                 zx_stream_t stream) {
   ZX_REQUIRE(q && cu_q && q_pos0 && pool && scales && block_tables && kv_begin && kv_end,
              "paged_attention_prefill: null pointer");
+  ZX_REQUIRE(n_ranges >= 1, "paged_attention: n_ranges must be positive");
   ZX_REQUIRE(n_q >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_pages > 0 && page_size > 0 && max_blocks > 0 &&
                  n_seqs > 0 && max_q_per_seq >= 0,
              "paged_attention_prefill: sizes must be positive");
@@ -447,6 +478,8 @@ extern "C" int zx_paged_attention_prefill(const uint16_t *q, int64_t n_q, const 
   a.bt = block_tables;
   a.kv_begin = kv_begin;
   a.kv_end = kv_end;
+  a.n_ranges = n_ranges;
+  a.n_seqs = n_seqs;
   a.o_acc = o_acc;
   a.lse2 = lse2;
   a.out = out;
@@ -476,4 +509,31 @@ extern "C" int zx_paged_attention_prefill(const uint16_t *q, int64_t n_q, const 
     default: paged_prefill_mfma_kernel<1><<<grid, PF_THREADS, 0, st>>>(a); break;
   }
   return check_launch("paged_prefill_mfma");
+}
+}  // namespace
+
+extern "C" int zx_paged_attention_prefill(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int32_t *q_pos0,
+                                          int32_t n_q_heads, const uint8_t *pool, int64_t n_pages, int32_t n_kv_heads,
+                                          int32_t head_dim, int32_t page_size, const float *scales,
+                                          const int32_t *block_tables, int32_t max_blocks, const int32_t *kv_begin,
+                                          const int32_t *kv_end, int32_t n_seqs, int32_t max_q_per_seq,
+                                          int32_t causal, float sm_scale, int32_t flags, float *o_acc, float *lse2,
+                                          uint16_t *out, int32_t *err, zx_stream_t stream) {
+  clear_error();
+  return prefill_impl(q, n_q, cu_q, q_pos0, n_q_heads, pool, n_pages, n_kv_heads, head_dim, page_size, scales,
+                      block_tables, max_blocks, kv_begin, kv_end, 1, n_seqs, max_q_per_seq, causal, sm_scale, flags,
+                      o_acc, lse2, out, err, stream);
+}
+
+extern "C" int zx_paged_attention_ring(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int32_t *q_pos0,
+                                       int32_t n_q_heads, const uint8_t *pool, int64_t n_pages, int32_t n_kv_heads,
+                                       int32_t head_dim, int32_t page_size, const float *scales,
+                                       const int32_t *block_tables, int32_t max_blocks, const int32_t *kv_begin,
+                                       const int32_t *kv_end, int32_t n_ranges, int32_t n_seqs, int32_t max_q_per_seq,
+                                       int32_t causal, float sm_scale, int32_t flags, float *o_acc, float *lse2,
+                                       uint16_t *out, int32_t *err, zx_stream_t stream) {
+  clear_error();
+  return prefill_impl(q, n_q, cu_q, q_pos0, n_q_heads, pool, n_pages, n_kv_heads, head_dim, page_size, scales,
+                      block_tables, max_blocks, kv_begin, kv_end, n_ranges, n_seqs, max_q_per_seq, causal, sm_scale,
+                      flags, o_acc, lse2, out, err, stream);
 }

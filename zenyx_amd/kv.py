@@ -426,21 +426,69 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
     return out if write_bf16 else None
 
 
+def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor, pool_layer: torch.Tensor,
+                         scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_begin: torch.Tensor,
+                         kv_end: torch.Tensor, causal: bool = True, sm_scale: float | None = None,
+                         max_q_per_seq: int | None = None, check: bool = False,
+                         err: torch.Tensor | None = None) -> torch.Tensor:
+    """All steps of a ring in one launch (zx_paged_attention_ring): ``kv_begin`` /
+    ``kv_end`` int32 ``[R, B]`` hold step r's key range of every sequence; each block
+    walks the R ranges with its running softmax state in registers and writes the bf16
+    rows once.  Same arguments and result as R paged_attention_prefill steps merged."""
+    N.require_device(q, "q")
+    if q.dtype != torch.bfloat16 or q.dim() != 3:
+        raise ValueError("q must be [n_q, n_q_heads, head_dim] bfloat16")
+    N.require_device(pool_layer, "pool_layer")
+    if pool_layer.dim() != 5 or pool_layer.dtype != torch.uint8 or pool_layer.shape[1] != 2:
+        raise ValueError("pool_layer must be uint8 [n_pages, 2, n_kv_heads, page_size, head_dim]")
+    n_pages, _, Hkv, P, D = pool_layer.shape
+    n_q, Hq, Dq = q.shape
+    if Dq != D:
+        raise ValueError("q and pool_layer disagree on head_dim")
+    N.require_device(scales_layer, "scales_layer")
+    if scales_layer.shape != (2, Hkv) or scales_layer.dtype != torch.float32:
+        raise ValueError(f"scales_layer must be float32 [2, {Hkv}]")
+    B = cu_q.numel() - 1
+    for t, name in ((cu_q, "cu_q"), (q_pos0, "q_pos0"), (block_tables, "block_tables"), (kv_begin, "kv_begin"),
+                    (kv_end, "kv_end")):
+        N.require_device(t, name)
+        if t.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32")
+    if kv_begin.dim() != 2 or kv_begin.shape != kv_end.shape or kv_begin.shape[1] != B:
+        raise ValueError("kv_begin and kv_end must be int32 [n_ranges, n_seqs]")
+    if q_pos0.numel() != B or block_tables.dim() != 2 or block_tables.shape[0] != B:
+        raise ValueError("cu_q, q_pos0 and block_tables disagree on the number of sequences")
+    if max_q_per_seq is None:
+        max_q_per_seq = int((cu_q[1:] - cu_q[:-1]).max().item()) if B else 0
+    out = torch.empty_like(q)
+    sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
+    if err is None:
+        err = _err_word(q.device)
+    N.check(N.load().zx_paged_attention_ring(
+        N.ptr(q), n_q, N.ptr(cu_q), N.ptr(q_pos0), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer),
+        N.ptr(block_tables), block_tables.shape[1], N.ptr(kv_begin), N.ptr(kv_end), kv_begin.shape[0], B,
+        int(max_q_per_seq), int(bool(causal)), sm, N.ZX_PREFILL_BF16, None, None, N.ptr(out), N.ptr(err),
+        N.stream_ptr(q.device)), "paged_attention_ring")
+    if check:
+        _raise_kernel_error(err, "paged_attention_ring")
+    return out
+
+
 def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor, pool_layer: torch.Tensor,
                        scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_len: torch.Tensor,
                        ring_degree: int, causal: bool = True, sm_scale: float | None = None,
-                       check: bool = False) -> torch.Tensor:
+                       check: bool = False, single_launch: bool = True) -> torch.Tensor:
     """Ring attention over the FP8 pages on one GPU: the keys [0, kv_len[b]) of every
     sequence are split into ``ring_degree`` shards (the KV blocks a ring would pass
-    around), each shard is one ring step (paged_attention_prefill) merged into a running
-    fp32 output and log-sum-exp, and the last step writes bf16.  Equals attention over all
-    keys (the exchange between devices is what one GPU leaves out)."""
+    around), shard r being ring step r.  With ``single_launch`` one launch walks the R
+    shards with the running softmax state in registers (zx_paged_attention_ring);
+    otherwise each step is its own launch (paged_attention_prefill, the unit a ring over R
+    GPUs runs) merged into a running fp32 output and log-sum-exp, the last one writing
+    bf16.  Either equals attention over all keys (the exchange between devices is what
+    one GPU leaves out)."""
     if ring_degree < 1:
         raise ValueError("ring_degree must be >= 1")
     n_q, Hq, D = q.shape
-    o_acc = torch.empty((n_q, Hq, D), dtype=torch.float32, device=q.device)
-    lse2 = torch.empty((n_q, Hq), dtype=torch.float32, device=q.device)
-    out = torch.empty_like(q)
     mq = int((cu_q[1:] - cu_q[:-1]).max().item()) if cu_q.numel() > 1 else 0
     # Shard r covers keys [kv_len * r // R, kv_len * (r + 1) // R): all bounds in one go,
     # so the loop below only launches the ring steps (rows padded to 16 bytes, the
@@ -450,6 +498,16 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     bounds = torch.empty((ring_degree + 1, (B + 3) // 4 * 4), dtype=torch.int32, device=kv_len.device)
     bounds[:, :B] = kv_len.to(torch.int64)[None, :] * steps[:, None] // ring_degree
     err = _err_word(q.device)
+    if single_launch:
+        out = paged_attention_ring(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables,
+                                   bounds[:-1, :B].contiguous(), bounds[1:, :B].contiguous(), causal=causal,
+                                   sm_scale=sm_scale, max_q_per_seq=mq, err=err)
+        if check:
+            _raise_kernel_error(err, "ring_attention_fp8")
+        return out
+    o_acc = torch.empty((n_q, Hq, D), dtype=torch.float32, device=q.device)
+    lse2 = torch.empty((n_q, Hq), dtype=torch.float32, device=q.device)
+    out = torch.empty_like(q)
     for r in range(ring_degree):
         paged_attention_prefill(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables, bounds[r, :B],
                                 bounds[r + 1, :B],
