@@ -691,16 +691,20 @@ def ring_attention_leg(torch, dev, steps, warmup, skip_cpu):
            "useful_flop_per_step": flops,
            "note": "P.V runs twice on the matrix cores (P split into bf16 hi + lo), so the matrix cores execute "
                    "1.5x the useful flops"}
-    for key, ring, single in (("ring1", 1, True), ("ring8", 8, True), ("ring8_steps", 8, False)):
+    for key, ring, single, fast in (("ring1", 1, True, False), ("ring8", 8, True, False),
+                                    ("ring8_steps", 8, False, False), ("ring1_fast_p", 1, True, True),
+                                    ("ring8_fast_p", 8, True, True)):
         fn = lambda: kv.ring_attention_fp8(q, cu, qp, pool, sc, bt, kl, ring_degree=ring, causal=True,  # noqa: E731
-                                           single_launch=single)
+                                           single_launch=single, fast_p=fast)
         ms, _, _ = time_steps(torch, fn, steps, warmup)
         tf = flops / (ms * 1e-3) / 1e12
         how = "one launch walking the shards" if single else "one launch per shard, merged through HBM"
+        how += ", P rounded once to bf16 (error <= 1 ulp + 2^-8 max|V|)" if fast else ""
         log(f"ring attention degree {ring} ({how}): {ms:.3f} ms/step, {tf:.1f} TFLOP/s "
             f"({100 * tf / MFMA_BF16_PEAK_TFLOPS:.1f}% of the bf16 MFMA peak)")
         res[key] = {"ms_per_step": round(ms, 4), "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                    "launches": "1" if single else str(ring)}
+                    "launches": "1" if single else str(ring),
+                    "p_in_pv": "bf16 (one product)" if fast else "bf16 hi + lo (two products)"}
     if not skip_cpu:
         # the C oracle (double precision, one thread) on the last 16 query rows of sequence 0
         # (about 20 s on one host core)

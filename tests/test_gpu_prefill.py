@@ -123,6 +123,33 @@ def test_ring_attention_equals_full_attention(ring, single_launch):
     assert_within_one_ulp(bits16(out), c["want"], c["vmax"])
 
 
+def assert_within_fast_p_bound(got_bits, want_bits, vmax):
+    """ZX_PREFILL_FAST_P's bound: |got - exact| <= one bf16 ulp of the exact value + 2^-8 max|V|
+    (the oracle value, rounded to bf16, stands for the exact one: one more ulp)."""
+    got = torch.from_numpy(got_bits.view(np.int16)).view(torch.bfloat16).double().numpy()
+    want = torch.from_numpy(want_bits.view(np.int16)).view(torch.bfloat16).double().numpy()
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
+    tol = 2 * ulp + 2.0 ** -8 * vmax
+    bad = np.abs(got - want) > tol
+    assert not bad.any(), f"{bad.sum()} outputs beyond one ulp + 2^-8 max|V|"
+    return float(np.max(np.abs(got - want) / np.maximum(vmax, 1e-30)))
+
+
+@pytest.mark.parametrize("ring,single", [(1, True), (8, True), (3, False)])
+def test_ring_attention_fast_p(ring, single):
+    """P rounded once to bf16 for P.V (ZX_PREFILL_FAST_P): within its stated bound of the
+    oracle, and strictly looser than the exact mode (the hi + lo mode stays within
+    2^-17 max|V|)."""
+    c = _ring_case()
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    out = kv.ring_attention_fp8(c["q"].to(DEV), t(c["cu"]), t(c["qp"]), t(c["pool"]), t(c["scales"]), t(c["bt"]),
+                                t(c["lens"]), ring_degree=ring, causal=True, check=True, single_launch=single,
+                                fast_p=True)
+    torch.cuda.synchronize()
+    worst = assert_within_fast_p_bound(bits16(out), c["want"], c["vmax"])
+    print(f"ring {ring} fast P: worst |err| / max|V| = {worst:.3g}", flush=True)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_ring_ranges_in_device_order(causal):
     """zx_paged_attention_ring with the shards in the order one device of a ring of 5 sees

@@ -25,7 +25,7 @@ ZX_KERR_PAGE_RANGE, ZX_KERR_POS_RANGE, ZX_KERR_SPIN, ZX_KERR_OVERFLOW = 1, 2, 4,
 ZX_APPEND_STATIC_SCALES = 1
 ZX_APPEND_TWO_PASS = 2
 ZX_APPEND_SATURATE = 4
-ZX_PREFILL_MERGE, ZX_PREFILL_INIT, ZX_PREFILL_BF16 = 1, 2, 4
+ZX_PREFILL_MERGE, ZX_PREFILL_INIT, ZX_PREFILL_BF16, ZX_PREFILL_FAST_P = 1, 2, 4, 8
 ZX_HEADS_TWO_PASS = 1
 ZX_NEVER = 0x7FFFFFFF
 ABI_VERSION = 2

@@ -67,7 +67,10 @@ __device__ __forceinline__ int pf_vslot_byte(int c, int key) {
   return c * PF_VROW + ((((kb << 2) + kg) ^ (c >> 4)) << 4) + 2 * (4 * KT + i);
 }
 
-template <int G>
+// EXACT: P enters P.V (and the row sums) as bf16 hi + lo, two MFMAs per tile, so P is
+// carried to ~2^-17 relative; otherwise P is rounded once to bf16 (one MFMA per tile), the
+// usual flash-attention numerics.
+template <int G, bool EXACT>
 __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(PrefillArgs a) {
   constexpr int D = 128;
   constexpr int QT = 32 * 4 / G;  // query rows per block
@@ -319,8 +322,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
           const float p0 = __builtin_amdgcn_exp2f(xe[KT][2 * j]), p1 = __builtin_amdgcn_exp2f(xe[KT][2 * j + 1]);
           const uint32_t hw = pack_bf16(p0, p1);
           ph[rt][KT >> 1][2 * (KT & 1) + j] = hw;
-          pl[rt][KT >> 1][2 * (KT & 1) + j] =
-              pack_bf16(p0 - __uint_as_float(hw << 16), p1 - __uint_as_float(hw & 0xFFFF0000u));
+          if constexpr (EXACT)
+            pl[rt][KT >> 1][2 * (KT & 1) + j] =
+                pack_bf16(p0 - __uint_as_float(hw << 16), p1 - __uint_as_float(hw & 0xFFFF0000u));
         }
     }
     // rescale O only when some row's maximum was raised
@@ -346,8 +350,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
         for (int rt = 0; rt < 2; ++rt) {
           o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, ph[rt][kbk]),
                                                               o[rt][jt], 0, 0, 0);
-          o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, pl[rt][kbk]),
-                                                              o[rt][jt], 0, 0, 0);
+          if constexpr (EXACT)
+            o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, pl[rt][kbk]),
+                                                                o[rt][jt], 0, 0, 0);
         }
       }
     }
@@ -357,8 +362,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
       for (int rt = 0; rt < 2; ++rt) {
         ol[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(att_bf16x8, ph[rt][kbk]), ol[rt], 0,
                                                          0, 0);
-        ol[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(att_bf16x8, pl[rt][kbk]), ol[rt], 0,
-                                                         0, 0);
+        if constexpr (EXACT)
+          ol[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(att_bf16x8, pl[rt][kbk]), ol[rt],
+                                                           0, 0, 0);
       }
   };
 
@@ -456,7 +462,7 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
                  n_seqs > 0 && max_q_per_seq >= 0,
              "paged_attention_prefill: sizes must be positive");
   ZX_REQUIRE(n_q_heads % n_kv_heads == 0, "paged_attention_prefill: n_q_heads must be a multiple of n_kv_heads");
-  ZX_REQUIRE((flags & ~(ZX_PREFILL_MERGE | ZX_PREFILL_INIT | ZX_PREFILL_BF16)) == 0,
+  ZX_REQUIRE((flags & ~(ZX_PREFILL_MERGE | ZX_PREFILL_INIT | ZX_PREFILL_BF16 | ZX_PREFILL_FAST_P)) == 0,
              "paged_attention_prefill: unknown flags");
   ZX_REQUIRE(!(flags & ZX_PREFILL_MERGE) || (o_acc && lse2), "paged_attention_prefill: merging needs o_acc and lse2");
   ZX_REQUIRE(!(flags & ZX_PREFILL_BF16) || out, "paged_attention_prefill: bf16 output requested without out");
@@ -503,10 +509,14 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
   const dim3 grid((unsigned)ceil_div(max_q_per_seq, QT), (unsigned)(n_q_heads / G), (unsigned)n_seqs);
   ZX_REQUIRE(grid.x < (1u << 31) && n_seqs <= 65535, "paged_attention_prefill: too many query tiles or sequences");
   hipStream_t st = as_stream(stream);
-  switch (G) {
-    case 4: paged_prefill_mfma_kernel<4><<<grid, PF_THREADS, 0, st>>>(a); break;
-    case 2: paged_prefill_mfma_kernel<2><<<grid, PF_THREADS, 0, st>>>(a); break;
-    default: paged_prefill_mfma_kernel<1><<<grid, PF_THREADS, 0, st>>>(a); break;
+  const bool exact = !(flags & ZX_PREFILL_FAST_P);
+  switch (G * 2 + exact) {
+    case 9: paged_prefill_mfma_kernel<4, true><<<grid, PF_THREADS, 0, st>>>(a); break;
+    case 8: paged_prefill_mfma_kernel<4, false><<<grid, PF_THREADS, 0, st>>>(a); break;
+    case 5: paged_prefill_mfma_kernel<2, true><<<grid, PF_THREADS, 0, st>>>(a); break;
+    case 4: paged_prefill_mfma_kernel<2, false><<<grid, PF_THREADS, 0, st>>>(a); break;
+    case 3: paged_prefill_mfma_kernel<1, true><<<grid, PF_THREADS, 0, st>>>(a); break;
+    default: paged_prefill_mfma_kernel<1, false><<<grid, PF_THREADS, 0, st>>>(a); break;
   }
   return check_launch("paged_prefill_mfma");
 }

@@ -360,7 +360,7 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
                             o_acc: torch.Tensor | None = None, lse2: torch.Tensor | None = None,
                             first: bool = True, out: torch.Tensor | None = None, write_bf16: bool = True,
                             max_q_per_seq: int | None = None, check: bool = False,
-                            err: torch.Tensor | None = None):
+                            err: torch.Tensor | None = None, fast_p: bool = False):
     """One ring step of attention over the FP8 pages (zx_paged_attention_prefill).
 
     ``q`` [n_q, Hq, 128] bf16 rows of all sequences (``cu_q`` [B+1] int32 offsets,
@@ -409,7 +409,8 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
     if max_q_per_seq is None:
         max_q_per_seq = int((cu_q[1:] - cu_q[:-1]).max().item()) if B else 0
     flags = (N.ZX_PREFILL_MERGE if o_acc is not None else 0) | (N.ZX_PREFILL_INIT if o_acc is not None and first
-                                                                else 0) | (N.ZX_PREFILL_BF16 if write_bf16 else 0)
+                                                                else 0) | (N.ZX_PREFILL_BF16 if write_bf16 else 0) | \
+        (N.ZX_PREFILL_FAST_P if fast_p else 0)
     sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
     dev = q.device
     if err is None:
@@ -430,11 +431,14 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
                          scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_begin: torch.Tensor,
                          kv_end: torch.Tensor, causal: bool = True, sm_scale: float | None = None,
                          max_q_per_seq: int | None = None, check: bool = False,
-                         err: torch.Tensor | None = None) -> torch.Tensor:
+                         err: torch.Tensor | None = None, fast_p: bool = False) -> torch.Tensor:
     """All steps of a ring in one launch (zx_paged_attention_ring): ``kv_begin`` /
     ``kv_end`` int32 ``[R, B]`` hold step r's key range of every sequence; each block
     walks the R ranges with its running softmax state in registers and writes the bf16
-    rows once.  Same arguments and result as R paged_attention_prefill steps merged."""
+    rows once.  Same arguments and result as R paged_attention_prefill steps merged.
+    ``fast_p`` rounds the softmax weights once to bf16 for P.V (ZX_PREFILL_FAST_P: one
+    matrix product per tile instead of two, error bound one ulp + 2^-8 max|V| instead of
+    one ulp + 2^-17 max|V|)."""
     N.require_device(q, "q")
     if q.dtype != torch.bfloat16 or q.dim() != 3:
         raise ValueError("q must be [n_q, n_q_heads, head_dim] bfloat16")
@@ -467,7 +471,8 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
     N.check(N.load().zx_paged_attention_ring(
         N.ptr(q), n_q, N.ptr(cu_q), N.ptr(q_pos0), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer),
         N.ptr(block_tables), block_tables.shape[1], N.ptr(kv_begin), N.ptr(kv_end), kv_begin.shape[0], B,
-        int(max_q_per_seq), int(bool(causal)), sm, N.ZX_PREFILL_BF16, None, None, N.ptr(out), N.ptr(err),
+        int(max_q_per_seq), int(bool(causal)), sm, N.ZX_PREFILL_BF16 | (N.ZX_PREFILL_FAST_P if fast_p else 0), None,
+        None, N.ptr(out), N.ptr(err),
         N.stream_ptr(q.device)), "paged_attention_ring")
     if check:
         _raise_kernel_error(err, "paged_attention_ring")
@@ -477,7 +482,7 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
 def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor, pool_layer: torch.Tensor,
                        scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_len: torch.Tensor,
                        ring_degree: int, causal: bool = True, sm_scale: float | None = None,
-                       check: bool = False, single_launch: bool = True) -> torch.Tensor:
+                       check: bool = False, single_launch: bool = True, fast_p: bool = False) -> torch.Tensor:
     """Ring attention over the FP8 pages on one GPU: the keys [0, kv_len[b]) of every
     sequence are split into ``ring_degree`` shards (the KV blocks a ring would pass
     around), shard r being ring step r.  With ``single_launch`` one launch walks the R
@@ -485,7 +490,8 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     otherwise each step is its own launch (paged_attention_prefill, the unit a ring over R
     GPUs runs) merged into a running fp32 output and log-sum-exp, the last one writing
     bf16.  Either equals attention over all keys (the exchange between devices is what
-    one GPU leaves out)."""
+    one GPU leaves out).  ``fast_p``: softmax weights rounded once to bf16 for P.V (see
+    paged_attention_ring)."""
     if ring_degree < 1:
         raise ValueError("ring_degree must be >= 1")
     n_q, Hq, D = q.shape
@@ -501,7 +507,7 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     if single_launch:
         out = paged_attention_ring(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables,
                                    bounds[:-1, :B].contiguous(), bounds[1:, :B].contiguous(), causal=causal,
-                                   sm_scale=sm_scale, max_q_per_seq=mq, err=err)
+                                   sm_scale=sm_scale, max_q_per_seq=mq, err=err, fast_p=fast_p)
         if check:
             _raise_kernel_error(err, "ring_attention_fp8")
         return out
@@ -512,7 +518,7 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
         paged_attention_prefill(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables, bounds[r, :B],
                                 bounds[r + 1, :B],
                                 causal=causal, sm_scale=sm_scale, o_acc=o_acc, lse2=lse2, first=r == 0, out=out,
-                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, err=err)
+                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, err=err, fast_p=fast_p)
     if check:
         _raise_kernel_error(err, "ring_attention_fp8")
     return out

@@ -24,6 +24,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import _native as N
+from .._streams import all_copy_streams, copy_stream
 
 
 @dataclass
@@ -36,18 +37,11 @@ class KVBlockRef:
 
 
 class _SideStream:
-    """One side stream per device for tier copies."""
+    """The tier copies' side stream of a device (the library's shared h2d copy stream)."""
 
-    _streams: dict = {}
-
-    @classmethod
-    def get(cls, device: torch.device) -> torch.cuda.Stream:
-        idx = device.index if device.index is not None else torch.cuda.current_device()
-        s = cls._streams.get(idx)
-        if s is None:
-            s = torch.cuda.Stream(device=idx)  # default priority
-            cls._streams[idx] = s
-        return s
+    @staticmethod
+    def get(device: torch.device) -> torch.cuda.Stream:
+        return copy_stream(device, "h2d")
 
 
 def _copy(dst: torch.Tensor, src: torch.Tensor, stream: torch.cuda.Stream) -> None:
@@ -178,7 +172,7 @@ class KVTierManager:
             _SideStream.get(torch.device(device)).synchronize()
             _HostKeepAlive.release_done()
             return
-        for s in list(_SideStream._streams.values()):
+        for s in all_copy_streams():
             s.synchronize()
         _HostKeepAlive.release_done()
 

@@ -26,6 +26,7 @@ import torch
 
 from .. import _native as N
 from .. import kv
+from .._streams import copy_stream
 from .kv_tiering import keep_host_alive
 
 
@@ -68,7 +69,7 @@ class LayerWeightStreamer:
         self._side = None
         if self.device.type == "cuda":
             N.ensure_gpu()
-            self._side = torch.cuda.Stream(device=self.device)  # default priority
+            self._side = copy_stream(self.device, "h2d")
 
     def prefetch(self, layer_id: str) -> None:
         if layer_id in self._resident or layer_id in self._prefetch:

@@ -37,6 +37,7 @@ import torch
 
 from .. import _native as N
 from .. import kv
+from .._streams import copy_stream
 
 SRC_HIT, SRC_T1, SRC_T2, SRC_NEW = 0, 1, 2, 3
 
@@ -300,8 +301,8 @@ class ThreeTierReplay:
         if self.fd is None:
             self.fd = os.open(t2_path, flags, 0o600)
         self.pool = cf.ThreadPoolExecutor(max(1, io_threads))
-        self.s_out = torch.cuda.Stream(device=self.device)  # T0 -> host
-        self.s_in = torch.cuda.Stream(device=self.device)   # host -> T0
+        self.s_out = copy_stream(self.device, "d2h")  # T0 -> host
+        self.s_in = copy_stream(self.device, "h2d")   # host -> T0
         self._stage_in = torch.empty(0, dtype=torch.uint8, pin_memory=True)
         self._stage_out = torch.empty(0, dtype=torch.uint8, pin_memory=True)
         self._err = torch.zeros(1, dtype=torch.int32, device=self.device)

@@ -25,6 +25,7 @@ import torch
 
 from .. import _native as N
 from .. import kv
+from .._streams import copy_stream
 
 
 class RingAttentionAccessSequence:
@@ -145,7 +146,7 @@ class BeladyKVCacheTieringManager:
         dev_pool = torch.empty(slots * pb, dtype=torch.uint8, device=dev)
         host_pool = torch.empty(len(pages) * pb if len(pages) else pb, dtype=torch.uint8, pin_memory=True)
         lib = N.load()
-        side = torch.cuda.Stream(device=dev)
+        side = copy_stream(dev, "h2d")
 
         def offs(ids, on_host):
             if on_host:

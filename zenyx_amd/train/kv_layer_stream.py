@@ -8,12 +8,12 @@ order 0 .. L-1, a backward pass gathers them in order L-1 .. 0.  Only ``hbm_laye
 layer pools fit in HBM.  When layer l >= S needs a slot, the resident layer whose next use
 is farthest goes (Belady): in the backward sweep that is the lowest-numbered resident
 layer, i.e. layer l - S.  So the layers 0 .. L-S-1 are the spilled ones, known in advance:
-each is written back to pinned host memory on a side stream right after its own append
-(write-behind), and the append that reuses its slot waits only for that copy.  In the
-backward sweep, the slot a gather frees at once receives the H2D prefetch of the spilled
-layer S positions later in the sweep (layer l - S), again on the side stream, and that
-layer's gather waits for its copy.  Every wait is an event between the caller's stream
-and the side stream; the host never blocks.
+each is written back to pinned host memory on the library's d2h copy stream right after
+its own append (write-behind), and the append that reuses its slot waits only for that
+copy.  In the backward sweep, the slot a gather frees at once receives the H2D prefetch of
+the spilled layer S positions later in the sweep (layer l - S), on the h2d copy stream,
+and that layer's gather waits for its copy.  Every wait is an event between the caller's
+stream and a copy stream; the host never blocks.
 """
 from __future__ import annotations
 
@@ -21,6 +21,7 @@ import torch
 
 from .. import _native as N
 from .. import kv
+from .._streams import copy_stream
 
 
 class LayerStreamedKVCache:
@@ -47,7 +48,8 @@ class LayerStreamedKVCache:
                      if self.n_spill else None)
         self.scales = torch.empty((self.L, 2, num_kv_heads), dtype=torch.float32, device=self.device)
         self.err = torch.zeros(1, dtype=torch.int32, device=self.device)
-        self.side = torch.cuda.Stream(device=self.device)  # default priority
+        self.d2h = copy_stream(self.device, "d2h")  # write-behind of the spilled layers
+        self.h2d = copy_stream(self.device, "h2d")  # prefetch back into freed slots
         self.timing = timing
         self.reset()
 
@@ -63,11 +65,12 @@ class LayerStreamedKVCache:
         return torch.cuda.Event(enable_timing=self.timing)
 
     def _copy(self, dst: torch.Tensor, src: torch.Tensor, kind: str) -> torch.cuda.Event:
+        side = self.d2h if kind == "d2h" else self.h2d
         e0 = self._event()
-        e0.record(self.side)
-        kv.tier_copy_runs(dst, src, [0], [0], self.layer_bytes, stream=self.side)
+        e0.record(side)
+        kv.tier_copy_runs(dst, src, [0], [0], self.layer_bytes, stream=side)
         e1 = self._event()
-        e1.record(self.side)
+        e1.record(side)
         if self.timing:
             self.events[kind].append((e0, e1))
         return e1
@@ -94,7 +97,7 @@ class LayerStreamedKVCache:
         if self.timing:
             self.events["append"].append((e0, e1))
         if layer < self.n_spill:  # a future victim: write it back now
-            self.side.wait_event(e1)
+            self.d2h.wait_event(e1)
             self._d2h_done[layer] = self._copy(self.host[layer], self.slots[slot], "d2h")
         self._next_fwd += 1
 
@@ -118,7 +121,7 @@ class LayerStreamedKVCache:
             self.events["gather"].append((e0, e1))
         nxt = layer - self.S
         if 0 <= nxt < self.n_spill:  # prefetch that layer into the slot just freed
-            self.side.wait_event(e1)
+            self.h2d.wait_event(e1)
             self._h2d_done[nxt] = self._copy(self.slots[slot], self.host[nxt], "h2d")
             self.slot_of[nxt] = slot
         self._next_bwd -= 1
