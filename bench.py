@@ -37,6 +37,8 @@ METRIC = "KV quant+append & gather+dequant GB/s (% HBM peak); evictions/sec"
 # WRITE_SIZE and scaled by the same counters on a plain 4 GiB copy (profiles/*.md); keyed by
 # (workload, seed) because the append's size depends on the seed.
 MEASURED_TRAFFIC = {("append", 1): 14_804_340_633, ("gather", 2): 12_889_463_193}
+TRAFFIC_SOURCE = ("profile figure, not measured in this run: rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 "
+                  "per dispatch (profiles/kv_append_fused_configs1.md, profiles/gather_dequant_configs2.md)")
 
 
 def parse():
@@ -879,6 +881,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4),
                          "traffic": MEASURED_TRAFFIC.get(("append", args.seed)),
+                         "traffic_source": TRAFFIC_SOURCE if ("append", args.seed) in MEASURED_TRAFFIC else None,
                          "kernel": "kv_append_fused_kernel (HIP events around the whole zx_kv_quant_append "
                                    "call: token offsets + fills + the fused kernel)"},
         })
@@ -902,7 +905,7 @@ def main():
         gb_g = G["alg_bytes"] / (ms_g * 1e-3) / 1e9
         log(f"gather: {ms_g:.3f} ms/step, {gb_g:.1f} GB/s ({100 * gb_g / HBM_PEAK_GBPS:.1f}% of peak)")
         gather = {"GBps": round(gb_g, 2), "ms_per_step": round(ms_g, 4), "frac": round(gb_g / HBM_PEAK_GBPS, 4),
-                  "traffic": MEASURED_TRAFFIC.get(("gather", 2)),
+                  "traffic": MEASURED_TRAFFIC.get(("gather", 2)), "traffic_source": TRAFFIC_SOURCE,
                   "workload": "configs[2]: paged gather + dequant, 64 seqs x 32768, 300k-page pool, one layer K+V",
                   "algorithmic_bytes_per_step": G["alg_bytes"]}
         if not args.skip_cpu:
