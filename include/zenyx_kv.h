@@ -95,15 +95,16 @@ int zx_int8_legacy_dequant_slabs(const int8_t *q, const void *scales, int scale_
  * [L][2][B][H][T][D]: n_outer = 2L, run = T*D).  scales: [n_outer][n_heads] fp32,
  * written by quant, read by dequant.  run must be a multiple of 16.
  */
-#define ZX_HEADS_TWO_PASS 1 /* flag: amax pass + encode pass instead of the single pass */
+#define ZX_HEADS_TWO_PASS 1    /* flag: amax pass + encode pass instead of the single pass */
+#define ZX_HEADS_SINGLE_PASS 2 /* flag: the single pass below 256 MiB too (where it is slower) */
 size_t zx_fp8_quant_heads_workspace_bytes(int64_t n_outer, int64_t n_batch, int64_t n_heads, int64_t run);
 /* The slab (outer, head) is read once: each of its n_batch runs is cut into shares held in
  * registers by one workgroup each, the workgroups of a slab exchange their maxima through
  * the workspace, then encode what they hold (cooperative launch; every wait is bounded and
  * a timeout sets ZX_KERR_SPIN in *err, device int32, may be NULL).  A slab needing more
- * workgroups than the device holds (n_batch * ceil(run / 46080) > compute units), an
- * input below 256 MiB (whose second read the Infinity Cache serves, making two passes
- * faster), or ZX_HEADS_TWO_PASS take two passes (same results).
+ * workgroups than the device holds (n_batch * ceil(run / 46080) > compute units), an input
+ * below 256 MiB without ZX_HEADS_SINGLE_PASS (the Infinity Cache serves the second read
+ * there, making two passes faster), or ZX_HEADS_TWO_PASS take two passes (same results).
  * workspace: zx_fp8_quant_heads_workspace_bytes() device bytes (unused with two passes,
  * may then be NULL). */
 int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_heads,

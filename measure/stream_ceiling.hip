@@ -25,9 +25,16 @@
 //            default-policy (temporal) and nontemporal loads on the first read;
 //   chunked  the two-pass design that would rely on it: 1 Gi bf16 elements (2 GiB) as
 //            chunks of C MiB, each read twice (a max pass, then a pass that writes 1 byte
-//            per element), against the same passes over the whole buffer.
+//            per element), against the same passes over the whole buffer;
+//   heads    the bytes of one single-pass per-head quantisation of 1 Gi bf16 elements
+//            (2 GiB read, 1 GiB written) as a plain stream (one 16-byte vector per thread)
+//            and as the persistent structure of the single-pass quantiser with nothing
+//            else in it: one 1024-thread workgroup per CU, 15 waves holding K = 6 vectors
+//            of NB = 4 contiguous 64 KiB shares in registers, each share written (8 bytes
+//            per vector) and its buffer refilled in turn; the shares fixed per workgroup
+//            (as the quantiser has them) or dealt out at run time by an atomic counter.
 //
-// Usage: stream_ceiling [plain|pages|append|columns|cache|chunked|all] (default all).
+// Usage: stream_ceiling [plain|pages|append|columns|cache|chunked|heads|all] (default all).
 // Prints one line per measurement.  Every access is in bounds; nothing waits on another
 // workgroup.  Built by __graft_entry__.build() into measure/bin/stream_ceiling.
 #include <hip/hip_runtime.h>
@@ -243,6 +250,144 @@ __global__ void __launch_bounds__(256) read_write_half(const sc_v4u *__restrict_
   }
 }
 
+// ---------------------------------------------------------------- 7. persistent contiguous shares
+
+constexpr int HP_DATA = 960;  // 15 data waves
+constexpr int HP_K = 6, HP_NB = 4;
+constexpr long HP_SHARE = 4096;  // vectors per share (64 KiB)
+
+// Workgroup w takes shares w, w + G, w + 2G, ... of n vectors; steps past the end load and
+// store nothing.  The 16th wave idles, as the control wave of the quantiser mostly does.
+__global__ void __launch_bounds__(1024) heads_pattern(const sc_v4u *__restrict__ x, sc_v2u *__restrict__ out,
+                                                      long n) {
+  const int t = threadIdx.x;
+  if (t >= HP_DATA) return;
+  const long G = gridDim.x, n_sh = (n + HP_SHARE - 1) / HP_SHARE;
+  const long steps = (n_sh - blockIdx.x + G - 1) / G;
+  const long steps_pad = (steps + HP_NB - 1) / HP_NB * HP_NB;
+  auto idx = [&](long i, int k) -> long {  // vector of slot k at step i, or -1
+    const long sh = blockIdx.x + i * G;
+    const long v = (long)k * HP_DATA + t;
+    return (i < steps && v < HP_SHARE && sh * HP_SHARE + v < n) ? sh * HP_SHARE + v : -1;
+  };
+  sc_v4u buf[HP_NB][HP_K];
+#pragma unroll
+  for (int j = 0; j < HP_NB; ++j)
+#pragma unroll
+    for (int k = 0; k < HP_K; ++k) {
+      const long v = idx(j, k);
+      buf[j][k] = v >= 0 ? __builtin_nontemporal_load(x + v) : sc_v4u{0, 0, 0, 0};
+    }
+  for (long i0 = 0; i0 < steps_pad; i0 += HP_NB) {
+#pragma unroll
+    for (int j = 0; j < HP_NB; ++j) {
+      const long i = i0 + j;
+#pragma unroll
+      for (int k = 0; k < HP_K; ++k) {
+        const long v = idx(i, k);
+        if (v >= 0) __builtin_nontemporal_store(sc_v2u{buf[j][k].x ^ buf[j][k].y, buf[j][k].z ^ buf[j][k].w}, out + v);
+      }
+#pragma unroll
+      for (int k = 0; k < HP_K; ++k) {
+        const long v = idx(i + HP_NB, k);
+        buf[j][k] = v >= 0 ? __builtin_nontemporal_load(x + v) : sc_v4u{0, 0, 0, 0};
+      }
+    }
+  }
+}
+
+// The same with the shares dealt out at run time: the 16th wave claims share ids from a
+// global counter (zero at launch) into an LDS ring ahead of the data waves, so a workgroup
+// on a faster part of the chip takes more shares.  Claims only increase, so a data wave
+// stops at the first id past the end.
+// LAZY: the share of step c is claimed only once every data wave has stored step c - NB
+// (the buffer it goes into is free), as a kernel must that may not hold a claimed share it
+// has not loaded; otherwise up to HP_RING claims run ahead of the data waves.
+constexpr int HP_RING = 8;  // > HP_NB
+template <bool LAZY>
+__global__ void __launch_bounds__(1024) heads_pattern_dyn(const sc_v4u *__restrict__ x, sc_v2u *__restrict__ out,
+                                                          long n, unsigned *counter) {
+  __shared__ long sid[HP_RING];
+  __shared__ unsigned ready[HP_RING], used[HP_RING], fin[HP_RING];
+  const int t = threadIdx.x;
+  const long n_sh = (n + HP_SHARE - 1) / HP_SHARE;
+  if (t < HP_RING) {
+    ready[t] = 0;
+    used[t] = 0;
+    fin[t] = 0;
+  }
+  __syncthreads();
+  if (t >= HP_DATA) {  // claimer: lane 0 of the 16th wave
+    if (t != HP_DATA) return;
+    for (int c = 0;; ++c) {
+      const int r = c % HP_RING;
+      const unsigned need = (unsigned)(c / HP_RING) * (HP_DATA / 64);  // earlier rounds consumed
+      while (__hip_atomic_load(&used[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != need)
+        __builtin_amdgcn_s_sleep(1);
+      if (LAZY && c >= HP_NB) {  // step c - NB stored by every data wave
+        const int f = c - HP_NB;
+        const unsigned want = (unsigned)(f / HP_RING + 1) * (HP_DATA / 64);
+        while (__hip_atomic_load(&fin[f % HP_RING], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < want)
+          __builtin_amdgcn_s_sleep(1);
+      }
+      const long s = (long)atomicAdd(counter, 1u);
+      sid[r] = s;
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __hip_atomic_store(&ready[r], (unsigned)(c + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (s >= n_sh) return;
+    }
+  }
+  auto get = [&](int c) -> long {
+    const int r = c % HP_RING;
+    while (__hip_atomic_load(&ready[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (unsigned)(c + 1))
+      __builtin_amdgcn_s_sleep(1);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const long s = sid[r];
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if ((t & 63) == 0) __hip_atomic_fetch_add(&used[r], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return s;
+  };
+  auto vec = [&](long sh, int k) -> long {
+    const long v = (long)k * HP_DATA + t;
+    return (sh < n_sh && v < HP_SHARE && sh * HP_SHARE + v < n) ? sh * HP_SHARE + v : -1;
+  };
+  long cur[HP_NB];
+  sc_v4u buf[HP_NB][HP_K];
+  int c_next = 0;
+  bool done = false;
+#pragma unroll
+  for (int j = 0; j < HP_NB; ++j) {
+    cur[j] = done ? n_sh : get(c_next++);
+    done = done || cur[j] >= n_sh;
+#pragma unroll
+    for (int k = 0; k < HP_K; ++k) {
+      const long v = vec(cur[j], k);
+      buf[j][k] = v >= 0 ? __builtin_nontemporal_load(x + v) : sc_v4u{0, 0, 0, 0};
+    }
+  }
+  // a round refills the buffers in claim order: when the first refill is past the end, so
+  // are the others, and nothing is left
+  for (int i0 = 0; cur[0] < n_sh; i0 += HP_NB) {
+#pragma unroll
+    for (int j = 0; j < HP_NB; ++j) {
+#pragma unroll
+      for (int k = 0; k < HP_K; ++k) {
+        const long v = vec(cur[j], k);
+        if (v >= 0) __builtin_nontemporal_store(sc_v2u{buf[j][k].x ^ buf[j][k].y, buf[j][k].z ^ buf[j][k].w}, out + v);
+      }
+      if (LAZY && (t & 63) == 0)  // step i0 + j stored by this wave
+        __hip_atomic_fetch_add(&fin[(i0 + j) % HP_RING], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      cur[j] = done ? n_sh : get(c_next++);
+      done = done || cur[j] >= n_sh;
+#pragma unroll
+      for (int k = 0; k < HP_K; ++k) {
+        const long v = vec(cur[j], k);
+        buf[j][k] = v >= 0 ? __builtin_nontemporal_load(x + v) : sc_v4u{0, 0, 0, 0};
+      }
+    }
+  }
+}
+
 static unsigned grid_for(long n_vec) {
   const long g = (n_vec + 1023) / 1024;
   return (unsigned)(g < 1 ? 1 : (g > 16384 ? 16384 : g));
@@ -451,6 +596,34 @@ int main(int argc, char **argv) {
         fflush(stdout);
       }
     }
+  }
+  if (want(sel, "heads")) {
+    const long total = 2L << 30;  // 1 Gi bf16 elements read, 1 GiB of codes written
+    const long n = total / 16;
+    const sc_v4u *xv = reinterpret_cast<const sc_v4u *>(x);
+    sc_v2u *ov = reinterpret_cast<sc_v2u *>(out);
+    float ms = best_ms([&] { plain_stream<16, 8><<<(unsigned)((n + 255) / 256), 256>>>(x, out, n); }, 5);
+    printf("heads: plain stream 2:1 over 2 GiB (one vector per thread): %.4f ms, %.1f GB/s of 3 GiB\n", ms,
+           3.0 * (1L << 30) / ms / 1e6);
+    ms = best_ms([&] { heads_pattern<<<(unsigned)ncu, 1024>>>(xv, ov, n); }, 5);
+    printf("heads: persistent grid (%d x 1024), contiguous 64 KiB shares, K = %d, NB = %d: %.4f ms, %.1f GB/s of "
+           "3 GiB\n",
+           ncu, HP_K, HP_NB, ms, 3.0 * (1L << 30) / ms / 1e6);
+    for (int lazy = 0; lazy < 2; ++lazy) {
+      ms = best_ms(
+          [&] {
+            SC_CHECK(hipMemsetAsync(counter, 0, sizeof(unsigned)));
+            if (lazy)
+              heads_pattern_dyn<true><<<(unsigned)ncu, 1024>>>(xv, ov, n, counter);
+            else
+              heads_pattern_dyn<false><<<(unsigned)ncu, 1024>>>(xv, ov, n, counter);
+          },
+          5);
+      printf("heads: persistent grid, shares dealt by an atomic counter, %s (counter reset included): %.4f ms, "
+             "%.1f GB/s of 3 GiB\n",
+             lazy ? "claimed when a buffer frees" : "claimed up to 8 steps ahead", ms, 3.0 * (1L << 30) / ms / 1e6);
+    }
+    fflush(stdout);
   }
   SC_CHECK(hipFree(x));
   SC_CHECK(hipFree(out));

@@ -79,14 +79,17 @@ def test_fp8_quant_dequant_heads_bit_exact(dev, shape, seed):
     assert_bf16_equal(bits16(y), O.fp8_dequant_heads(wc, ws))
 
 
-@pytest.mark.parametrize("two_pass", [False, True])
+@pytest.mark.parametrize("mode", ["single", "two", "auto"])
 @pytest.mark.parametrize("shape", [(4, 1, 3, 16), (2, 3, 2, 30720 * 8 + 5 * 16), (3, 7, 3, 4000),
-                                   (1, 1, 2, 64), (2, 300, 1, 16), (5, 2, 5, 61440 * 8)])
-def test_fp8_heads_single_and_two_pass(dev, shape, two_pass):
-    """Both quantiser paths against the oracle: runs split into several shares with a
-    ragged last one, more batches than shares, spare groups (more groups than slabs), a slab
-    needing more workgroups than the device has (falls back to two passes), several steps per
-    group; special values in one slab of every shape."""
+                                   (1, 1, 2, 64), (2, 300, 1, 16), (5, 2, 5, 61440 * 8), (40, 2, 8, 5760 * 8 * 3 + 16)])
+def test_fp8_heads_single_and_two_pass(dev, shape, mode):
+    """Both quantiser paths against the oracle ("single" forces the single pass below the
+    256 MiB where "auto" picks two passes): runs split into several shares with a ragged
+    last one, more batches than shares, spare groups (more groups than slabs), a slab
+    needing more workgroups than the device has (falls back to two passes), 320 slabs of
+    runs whose last share is two vectors long (many steps per group); special values in
+    one slab of every shape."""
+    two_pass = mode == "two"
     n_outer, B, H, run = shape
     g = torch.Generator().manual_seed(run + B)
     x = (torch.randn((n_outer, B, H, run), generator=g) * torch.rand((n_outer, 1, H, 1), generator=g) * 9)
@@ -94,7 +97,7 @@ def test_fp8_heads_single_and_two_pass(dev, shape, two_pass):
     x[n_outer - 1, 0, 0, run - 1] = -3.0e4
     x = x.to(torch.bfloat16)
     err = torch.zeros(1, dtype=torch.int32)
-    codes, scales = kv.fp8_quant_heads(x.to(dev), two_pass=two_pass, check=True)
+    codes, scales = kv.fp8_quant_heads(x.to(dev), two_pass=two_pass, single_pass=mode == "single", check=True)
     wc, ws = O.fp8_quant_heads(bits16(x))
     np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint32), ws.view(np.uint32))
     np.testing.assert_array_equal(codes.cpu().numpy(), wc)

@@ -27,6 +27,7 @@ ZX_APPEND_TWO_PASS = 2
 ZX_APPEND_SATURATE = 4
 ZX_PREFILL_MERGE, ZX_PREFILL_INIT, ZX_PREFILL_BF16, ZX_PREFILL_FAST_P = 1, 2, 4, 8
 ZX_HEADS_TWO_PASS = 1
+ZX_HEADS_SINGLE_PASS = 2
 ZX_NEVER = 0x7FFFFFFF
 ABI_VERSION = 2
 

@@ -685,7 +685,10 @@ extern "C" int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_
                                   void *workspace, size_t workspace_bytes, zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(x && codes && scales, "fp8_quant_heads: null pointer");
-  ZX_REQUIRE(!(flags & ~ZX_HEADS_TWO_PASS), "fp8_quant_heads: unknown flag bits 0x%x", (unsigned)flags);
+  ZX_REQUIRE(!(flags & ~(ZX_HEADS_TWO_PASS | ZX_HEADS_SINGLE_PASS)), "fp8_quant_heads: unknown flag bits 0x%x",
+             (unsigned)flags);
+  ZX_REQUIRE((flags & (ZX_HEADS_TWO_PASS | ZX_HEADS_SINGLE_PASS)) != (ZX_HEADS_TWO_PASS | ZX_HEADS_SINGLE_PASS),
+             "fp8_quant_heads: ZX_HEADS_TWO_PASS and ZX_HEADS_SINGLE_PASS together");
   HeadsGeom g;
   int64_t nb;
   int rc = heads_geom(n_outer, n_batch, n_heads, run, g, nb);
@@ -695,7 +698,7 @@ extern "C" int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_
   // passes are faster (MI355X: 0.069 vs 0.091 ms at configs[0]'s 151 MB); above it the
   // single pass saves the second HBM read (1 Gi elements: 0.66 vs 1.02 ms).
   const bool large = (double)n_outer * n_batch * n_heads * run * 2 >= (double)(256 << 20);
-  if (!(flags & ZX_HEADS_TWO_PASS) && large) {
+  if (!(flags & ZX_HEADS_TWO_PASS) && (large || (flags & ZX_HEADS_SINGLE_PASS))) {
     const size_t need = heads_fused_workspace_bytes(n_outer, n_batch, n_heads, run);
     if (!workspace || workspace_bytes < need)
       return fail(ZX_ERR_WORKSPACE, "fp8_quant_heads: workspace %zu < %zu bytes", workspace_bytes, need);

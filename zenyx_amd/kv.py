@@ -133,10 +133,12 @@ def int8_legacy_dequant_slabs(q: torch.Tensor, scales: torch.Tensor) -> torch.Te
 
 # ------------------------------------------------------------------ FP8 per head
 
-def fp8_quant_heads(x: torch.Tensor, two_pass: bool = False, check: bool = False):
+def fp8_quant_heads(x: torch.Tensor, two_pass: bool = False, check: bool = False, single_pass: bool = False):
     """x: bf16 ``[n_outer, n_batch, n_heads, run]`` -> (codes uint8 same shape, scales
-    fp32 ``[n_outer, n_heads]``), one scale per (outer, head).  The single-pass kernel reads
-    x once; ``two_pass`` forces the amax pass + encode pass (same results)."""
+    fp32 ``[n_outer, n_heads]``), one scale per (outer, head).  Inputs of 256 MiB and more
+    are read once (the single-pass kernel), smaller ones in two passes (the second read
+    comes from the Infinity Cache); ``two_pass`` / ``single_pass`` force either path (same
+    results)."""
     N.ensure_gpu()
     if x.dtype != torch.bfloat16 or x.dim() != 4:
         raise ValueError("fp8_quant_heads: x must be bf16 [n_outer, n_batch, n_heads, run]")
@@ -145,10 +147,13 @@ def fp8_quant_heads(x: torch.Tensor, two_pass: bool = False, check: bool = False
     codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
     scales = torch.empty((O, H), dtype=torch.float32, device=x.device)
     lib = N.load()
+    if two_pass and single_pass:
+        raise ValueError("fp8_quant_heads: two_pass and single_pass are exclusive")
     ws = None if two_pass else _workspace(lib.zx_fp8_quant_heads_workspace_bytes(O, B, H, R), x.device)
     err = _err_word(x.device)
+    flags = N.ZX_HEADS_TWO_PASS if two_pass else (N.ZX_HEADS_SINGLE_PASS if single_pass else 0)
     N.check(lib.zx_fp8_quant_heads(N.ptr(x), O, B, H, R, N.ptr(codes), N.ptr(scales),
-                                   N.ZX_HEADS_TWO_PASS if two_pass else 0, N.ptr(err), N.ptr(ws),
+                                   flags, N.ptr(err), N.ptr(ws),
                                    0 if ws is None else ws.numel(), N.stream_ptr(x.device)), "fp8_quant_heads")
     if check:
         _raise_kernel_error(err, "fp8_quant_heads")
