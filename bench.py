@@ -691,22 +691,23 @@ def ring_attention_leg(torch, dev, steps, warmup, skip_cpu):
     res = {"workload": "ring attention from FP8 pages: 4 seqs x 8192 tokens causal, 32 query heads over 8 KV "
                        "heads, D=128, page 16 (Llama-3-8B attention shape); kernel paged_prefill_mfma",
            "useful_flop_per_step": flops,
-           "note": "P.V runs twice on the matrix cores (P split into bf16 hi + lo), so the matrix cores execute "
-                   "1.5x the useful flops"}
-    for key, ring, single, fast in (("ring1", 1, True, False), ("ring8", 8, True, False),
-                                    ("ring8_steps", 8, False, False), ("ring1_fast_p", 1, True, True),
-                                    ("ring8_fast_p", 8, True, True)):
+           "note": "peak: the 2.5 PFLOP/s dense bf16/fp16 MFMA figure; with precision 'exact' P.V runs twice "
+                   "(P as bf16 hi + lo), so the matrix cores execute 1.5x the useful flops"}
+    p_desc = {"f16": "P x 2^7 rounded once to fp16, V fp16 (error <= 1 ulp + 2^-10 max|V|)",
+              "bf16": "P rounded once to bf16 (error <= 1 ulp + 2^-7 max|V|)",
+              "exact": "P as bf16 hi + lo, two products (error <= 1 ulp + 2^-15 max|V|; measured within 2^-17)"}
+    for key, ring, single, prec in (("ring1", 1, True, "f16"), ("ring8", 8, True, "f16"),
+                                    ("ring8_steps", 8, False, "f16"), ("ring1_exact", 1, True, "exact"),
+                                    ("ring8_exact", 8, True, "exact"), ("ring1_bf16p", 1, True, "bf16")):
         fn = lambda: kv.ring_attention_fp8(q, cu, qp, pool, sc, bt, kl, ring_degree=ring, causal=True,  # noqa: E731
-                                           single_launch=single, fast_p=fast)
+                                           single_launch=single, precision=prec)
         ms, _, _ = time_steps(torch, fn, steps, warmup)
         tf = flops / (ms * 1e-3) / 1e12
         how = "one launch walking the shards" if single else "one launch per shard, merged through HBM"
-        how += ", P rounded once to bf16 (error <= 1 ulp + 2^-8 max|V|)" if fast else ""
-        log(f"ring attention degree {ring} ({how}): {ms:.3f} ms/step, {tf:.1f} TFLOP/s "
+        log(f"ring attention degree {ring} ({how}; {p_desc[prec]}): {ms:.3f} ms/step, {tf:.1f} TFLOP/s "
             f"({100 * tf / MFMA_BF16_PEAK_TFLOPS:.1f}% of the bf16 MFMA peak)")
         res[key] = {"ms_per_step": round(ms, 4), "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                    "launches": "1" if single else str(ring),
-                    "p_in_pv": "bf16 (one product)" if fast else "bf16 hi + lo (two products)"}
+                    "launches": "1" if single else str(ring), "precision": prec, "p_in_pv": p_desc[prec]}
     if not skip_cpu:
         # the C oracle (double precision, one thread) on the last 16 query rows of sequence 0
         # (about 20 s on one host core)

@@ -58,7 +58,7 @@ enum zx_kernel_error {
 
 /* Message describing the last failing call on this thread ("" if none). */
 const char *zx_last_error(void);
-/* ABI version of the library (bumped on any signature change). */
+/* ABI version of the library (bumped on any change of a signature or of a default). */
 int zx_abi_version(void);
 
 /* ---------------------------------------------------------------------------
@@ -342,13 +342,25 @@ int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, i
  * Running every step of a ring with MERGE (INIT on the first) and BF16 on the last gives
  * attention over the union of the steps' key ranges.  Needs head_dim 128 and a page size
  * that is a multiple of 16. */
-enum { ZX_PREFILL_MERGE = 1, ZX_PREFILL_INIT = 2, ZX_PREFILL_BF16 = 4, ZX_PREFILL_FAST_P = 8 };
-/* ZX_PREFILL_FAST_P: the softmax weights P enter P.V rounded once to bf16 (one matrix
- * product per tile instead of the hi + lo pair that carries P to ~2^-17), as flash
- * attention usually does.  The row sums use the same rounded P, so a row is an average of
- * V under weights perturbed by at most 2^-9 relative, which moves it by at most
- * 2^-9 max|V - out| <= 2^-8 max|V|: |got - exact| <= one bf16 ulp + 2^-8 max|V| (instead of
- * one ulp + 2^-17 max|V|). */
+enum {
+  ZX_PREFILL_MERGE = 1,
+  ZX_PREFILL_INIT = 2,
+  ZX_PREFILL_BF16 = 4,
+  ZX_PREFILL_FAST_P = 8,
+  ZX_PREFILL_EXACT_P = 16
+};
+/* Precision of P.V.  The row sums use the same rounded softmax weights P as P.V, so a row
+ * is an average of V under weights perturbed by at most e relative, which moves it by at
+ * most e max|V - out| <= 2 e max|V| (and lse2 by at most log2(1 + e)); steps merged
+ * through lse2 stay such an average:
+ *   default            P (times 2^7, which keeps it in range) rounded once to fp16, V in
+ *                      fp16, one matrix product per tile: e = 2^-11, so |got - exact| <=
+ *                      one bf16 ulp + 2^-10 max|V|;
+ *   ZX_PREFILL_FAST_P  P rounded once to bf16 (as flash attention usually does), same
+ *                      speed: e = 2^-8, one ulp + 2^-7 max|V|;
+ *   ZX_PREFILL_EXACT_P P as bf16 hi + lo, two matrix products per tile (~1.3x the time):
+ *                      e = 2^-16, one ulp + 2^-15 max|V| at worst (measured within one ulp
+ *                      + 2^-17 max|V|). */
 /* All R steps of a ring on one GPU in one launch: the same computation as R calls of
  * zx_paged_attention_prefill over key ranges kv_begin[r * n_seqs + b], kv_end[r * n_seqs + b]
  * (r < n_ranges, device int32), except that each block walks the ranges in order with the

@@ -45,15 +45,22 @@ def v_colmax(pool, scales, bt, lens, Hq):
     return out
 
 
-def assert_within_one_ulp(got_bits: np.ndarray, want_bits: np.ndarray, vmax: np.ndarray):
+def assert_within_bound(got_bits: np.ndarray, want_bits: np.ndarray, vmax: np.ndarray, e: float, ulps: int = 1):
+    """|got - want| <= ``ulps`` bf16 ulps of want + e * max|V| elementwise (NaN as a class)."""
     g, w = bf16_to_f32(got_bits), bf16_to_f32(want_bits)
     g_nan, w_nan = np.isnan(g), np.isnan(w)
     np.testing.assert_array_equal(g_nan, w_nan)
     g, w, vm = g[~g_nan].astype(np.float64), w[~w_nan].astype(np.float64), vmax[~w_nan]
     mag = np.maximum(np.abs(w), 2.0 ** -100)
-    tol = np.exp2(np.floor(np.log2(mag)) - 7) + 2.0 ** -17 * vm
+    tol = ulps * np.exp2(np.floor(np.log2(mag)) - 7) + e * vm
     bad = np.abs(g - w) > tol
     assert not bad.any(), f"{bad.sum()} of {bad.size} beyond tolerance, e.g. got {g[bad][:4]} want {w[bad][:4]}"
+    return float(np.max(np.abs(g - w) / np.maximum(vm, 1e-30))) if g.size else 0.0
+
+
+def assert_within_one_ulp(got_bits: np.ndarray, want_bits: np.ndarray, vmax: np.ndarray):
+    """The exact kernels' bound: one bf16 ulp + 2^-17 max|V|."""
+    return assert_within_bound(got_bits, want_bits, vmax, 2.0 ** -17)
 
 
 def make_case(Hq, Hkv, D, P, lens, seed, n_pages=None, nan_codes=False):

@@ -16,9 +16,9 @@
 //     column of every MFMA tile: S^T = K . Q^T on v_mfma_f32_16x16x32_bf16 (K rows as A,
 //     Q rows as B), key range / causal mask only on the steps that cross a boundary,
 //     online softmax in the exp2 domain with row maxima over the 4 lane rows by
-//     v_permlane32/16_swap, P^T kept in registers as the B operand split into bf16
-//     hi + lo, O^T += V^T . P^T on the same MFMA, and the row sums of P as a ninth tile
-//     against ones (the rescale of O skipped unless a row maximum was raised).
+//     v_permlane32/16_swap, P^T kept in registers as the B operand (fp16 by default,
+//     see PM below), O^T += V^T . P^T on the matrix cores, and the row sums of P as a
+//     ninth tile against ones (the rescale of O skipped unless a row maximum was raised).
 // At the end each row is normalised; with MERGE the step's (O, lse2) is combined with
 // the running one in o_acc / lse2 (each (row, head) belongs to one block, so no races);
 // with the bf16 flag the merged row is also written as bf16.
@@ -67,11 +67,47 @@ __device__ __forceinline__ int pf_vslot_byte(int c, int key) {
   return c * PF_VROW + ((((kb << 2) + kg) ^ (c >> 4)) << 4) + 2 * (4 * KT + i);
 }
 
-// EXACT: P enters P.V (and the row sums) as bf16 hi + lo, two MFMAs per tile, so P is
-// carried to ~2^-17 relative; otherwise P is rounded once to bf16 (one MFMA per tile), the
-// usual flash-attention numerics.
-template <int G, bool EXACT>
+// How P enters P.V (and the row sums, which use the same P):
+//   PF_P_F16   P * 2^7 rounded once to fp16 (11 significant bits, relative error <= 2^-11;
+//              the 2^7 keeps P's range (<= 2^PF_LAZY) inside fp16 and pushes its
+//              subnormal range 7 octaves down), V^T in LDS as fp16 (e4m3 values are exact
+//              in fp16), one fp16 MFMA per tile;
+//   PF_P_BF16  P rounded once to bf16 (relative error <= 2^-9), one bf16 MFMA per tile,
+//              the usual flash-attention numerics;
+//   PF_P_EXACT P as bf16 hi + lo, two bf16 MFMAs per tile: P carried to ~2^-17.
+constexpr int PF_P_F16 = 0, PF_P_BF16 = 1, PF_P_EXACT = 2;
+constexpr float PF_F16_SHIFT = 7.0f;  // log2 of the factor P carries in PF_P_F16
+typedef _Float16 att_f16x8 __attribute__((ext_vector_type(8)));
+
+// O^T (or the row sums) += A . B on 16x16x32 tiles, A and B given as the bits of 8 values
+__device__ __forceinline__ att_f32x4 pf_mfma_bf16(att_u32x4 a, att_u32x4 b, att_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(att_bf16x8, a), __builtin_bit_cast(att_bf16x8, b),
+                                                 c, 0, 0, 0);
+}
+__device__ __forceinline__ att_f32x4 pf_mfma_f16(att_u32x4 a, att_u32x4 b, att_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(att_f16x8, a), __builtin_bit_cast(att_f16x8, b), c,
+                                                0, 0, 0);
+}
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  f16x2_t v;
+  v[0] = (_Float16)lo;
+  v[1] = (_Float16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+// 16 e4m3 codes -> 8 fp16 pairs (exact: every e4m3 value is an fp16 value).
+__device__ __forceinline__ void decode16_f16(uint4 c, uint32_t (&b)[8]) {
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    b[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w[i], 1.0f, false));
+    b[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)w[i], 1.0f, true));
+  }
+}
+
+template <int G, int PM>
 __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(PrefillArgs a) {
+  constexpr bool EXACT = PM == PF_P_EXACT, F16 = PM == PF_P_F16;
   constexpr int D = 128;
   constexpr int QT = 32 * 4 / G;  // query rows per block
   const int b = blockIdx.z;
@@ -174,7 +210,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 
   // O^T tiles: o[rt][jt] holds channels 16 jt + 4 kg ..+4 of row 16 rt + n; m per row.
   // The softmax denominator l is a ninth tile on the matrix cores: V^T rows of ones, so
-  // every element of ol[rt] is the row's sum of the same bf16 hi + lo P that O uses.
+  // every element of ol[rt] is the row's sum of the same P that O uses.
   att_f32x4 o[2][8], ol[2];
   float m[2];
 #pragma unroll
@@ -184,7 +220,10 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     ol[rt] = att_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     m[rt] = -INFINITY;
   }
-  const att_bf16x8 ones = __builtin_bit_cast(att_bf16x8, att_u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  const uint32_t one2 = F16 ? 0x3C003C00u : 0x3F803F80u;  // two ones (fp16 / bf16)
+  const att_u32x4 ones = {one2, one2, one2, one2};
+  // the factor 2^PF_F16_SHIFT that P carries in PF_P_F16 (it cancels in O / l)
+  const float p_shift = F16 ? PF_F16_SHIFT : 0.0f;
 
   // block-cooperative load of one step: thread t moves 16 bytes of K and of V of keys
   // 2 (t / 8) and 2 (t / 8) + 1 (so wave w loads 16-key tile w), channels 16 (t % 8) ..+16;
@@ -229,8 +268,13 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     }
     // V^T: channel c = 16 g8 + 2 p (+1) gets keys kk0, kk0 + 1 (adjacent k slots) as one word
     uint32_t v0[8], v1[8];
-    decode16_bf16(make_uint4(vc[0].x, vc[0].y, vc[0].z, vc[0].w), v0);
-    decode16_bf16(make_uint4(vc[1].x, vc[1].y, vc[1].z, vc[1].w), v1);
+    if constexpr (F16) {
+      decode16_f16(make_uint4(vc[0].x, vc[0].y, vc[0].z, vc[0].w), v0);
+      decode16_f16(make_uint4(vc[1].x, vc[1].y, vc[1].z, vc[1].w), v1);
+    } else {
+      decode16_bf16(make_uint4(vc[0].x, vc[0].y, vc[0].z, vc[0].w), v0);
+      decode16_bf16(make_uint4(vc[1].x, vc[1].y, vc[1].z, vc[1].w), v1);
+    }
     const int slot0 = pf_vslot_byte(16 * g8, kk0);  // channel 16 g8; the others add c * PF_VROW
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
@@ -270,7 +314,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
                       (!a.causal || (int64_t)s0 + PF_KEYS - 1 <= qp0 + wrow0);
     float alpha[2];
     bool grow_any = false;
-    att_u32x4 ph[2][2], pl[2][2];  // [rt][k-block] P^T hi / lo as bf16 pairs: word 2 KT + i / 2
+    att_u32x4 ph[2][2], pl[2][2];  // [rt][k-block] P^T (hi) / lo as 16-bit pairs: word 2 KT + i / 2
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int r = wrow0 + 16 * rt + n;
@@ -308,7 +352,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 #pragma unroll
       for (int KT = 0; KT < 4; ++KT)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xe[KT][i] = __builtin_fmaf(sc[rt][KT][i], qs, -ms);
+        for (int i = 0; i < 4; ++i) xe[KT][i] = __builtin_fmaf(sc[rt][KT][i], qs, p_shift - ms);
       if (!full) {
 #pragma unroll
         for (int KT = 0; KT < 4; ++KT)
@@ -320,7 +364,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const float p0 = __builtin_amdgcn_exp2f(xe[KT][2 * j]), p1 = __builtin_amdgcn_exp2f(xe[KT][2 * j + 1]);
-          const uint32_t hw = pack_bf16(p0, p1);
+          const uint32_t hw = F16 ? pack_f16(p0, p1) : pack_bf16(p0, p1);
           ph[rt][KT >> 1][2 * (KT & 1) + j] = hw;
           if constexpr (EXACT)
             pl[rt][KT >> 1][2 * (KT & 1) + j] =
@@ -343,16 +387,16 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
       const int ch = 16 * jt + n;
 #pragma unroll
       for (int kbk = 0; kbk < 2; ++kbk) {
-        const att_u32x4 w =
+        const att_u32x4 av =
             *reinterpret_cast<const att_u32x4 *>(&vtl[buf][ch * PF_VROW + ((((kbk << 2) + kg) ^ jt) << 4)]);
-        const att_bf16x8 av = __builtin_bit_cast(att_bf16x8, w);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-          o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, ph[rt][kbk]),
-                                                              o[rt][jt], 0, 0, 0);
-          if constexpr (EXACT)
-            o[rt][jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(att_bf16x8, pl[rt][kbk]),
-                                                                o[rt][jt], 0, 0, 0);
+          if constexpr (F16) {
+            o[rt][jt] = pf_mfma_f16(av, ph[rt][kbk], o[rt][jt]);
+          } else {
+            o[rt][jt] = pf_mfma_bf16(av, ph[rt][kbk], o[rt][jt]);
+            if constexpr (EXACT) o[rt][jt] = pf_mfma_bf16(av, pl[rt][kbk], o[rt][jt]);
+          }
         }
       }
     }
@@ -360,11 +404,12 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     for (int kbk = 0; kbk < 2; ++kbk)
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        ol[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(att_bf16x8, ph[rt][kbk]), ol[rt], 0,
-                                                         0, 0);
-        if constexpr (EXACT)
-          ol[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, __builtin_bit_cast(att_bf16x8, pl[rt][kbk]), ol[rt],
-                                                           0, 0, 0);
+        if constexpr (F16) {
+          ol[rt] = pf_mfma_f16(ones, ph[rt][kbk], ol[rt]);
+        } else {
+          ol[rt] = pf_mfma_bf16(ones, ph[rt][kbk], ol[rt]);
+          if constexpr (EXACT) ol[rt] = pf_mfma_bf16(ones, pl[rt][kbk], ol[rt]);
+        }
       }
   };
 
@@ -403,7 +448,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     const int r = wrow0 + 16 * rt + n;
     const float lt = ol[rt][0];
     if (r >= n_qb) continue;
-    const float lse_new = lt > 0.0f ? m[rt] + __builtin_amdgcn_logf(lt) : -INFINITY;
+    const float lse_new = lt > 0.0f ? m[rt] + (__builtin_amdgcn_logf(lt) - p_shift) : -INFINITY;
     const float inv = lt > 0.0f ? vscale / lt : 0.0f;  // V's dequant scale applied once, here
     const int64_t row = (q_lo + r) * a.n_q_heads + hq;
     float wa = 0.0f, wb = 1.0f, lse = lse_new;
@@ -462,8 +507,11 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
                  n_seqs > 0 && max_q_per_seq >= 0,
              "paged_attention_prefill: sizes must be positive");
   ZX_REQUIRE(n_q_heads % n_kv_heads == 0, "paged_attention_prefill: n_q_heads must be a multiple of n_kv_heads");
-  ZX_REQUIRE((flags & ~(ZX_PREFILL_MERGE | ZX_PREFILL_INIT | ZX_PREFILL_BF16 | ZX_PREFILL_FAST_P)) == 0,
+  ZX_REQUIRE((flags & ~(ZX_PREFILL_MERGE | ZX_PREFILL_INIT | ZX_PREFILL_BF16 | ZX_PREFILL_FAST_P | ZX_PREFILL_EXACT_P)) ==
+                 0,
              "paged_attention_prefill: unknown flags");
+  ZX_REQUIRE(!((flags & ZX_PREFILL_FAST_P) && (flags & ZX_PREFILL_EXACT_P)),
+             "paged_attention_prefill: ZX_PREFILL_FAST_P and ZX_PREFILL_EXACT_P together");
   ZX_REQUIRE(!(flags & ZX_PREFILL_MERGE) || (o_acc && lse2), "paged_attention_prefill: merging needs o_acc and lse2");
   ZX_REQUIRE(!(flags & ZX_PREFILL_BF16) || out, "paged_attention_prefill: bf16 output requested without out");
   ZX_REQUIRE(flags & (ZX_PREFILL_MERGE | ZX_PREFILL_BF16), "paged_attention_prefill: nothing to write");
@@ -509,14 +557,21 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
   const dim3 grid((unsigned)ceil_div(max_q_per_seq, QT), (unsigned)(n_q_heads / G), (unsigned)n_seqs);
   ZX_REQUIRE(grid.x < (1u << 31) && n_seqs <= 65535, "paged_attention_prefill: too many query tiles or sequences");
   hipStream_t st = as_stream(stream);
-  const bool exact = !(flags & ZX_PREFILL_FAST_P);
-  switch (G * 2 + exact) {
-    case 9: paged_prefill_mfma_kernel<4, true><<<grid, PF_THREADS, 0, st>>>(a); break;
-    case 8: paged_prefill_mfma_kernel<4, false><<<grid, PF_THREADS, 0, st>>>(a); break;
-    case 5: paged_prefill_mfma_kernel<2, true><<<grid, PF_THREADS, 0, st>>>(a); break;
-    case 4: paged_prefill_mfma_kernel<2, false><<<grid, PF_THREADS, 0, st>>>(a); break;
-    case 3: paged_prefill_mfma_kernel<1, true><<<grid, PF_THREADS, 0, st>>>(a); break;
-    default: paged_prefill_mfma_kernel<1, false><<<grid, PF_THREADS, 0, st>>>(a); break;
+  const int pm = (flags & ZX_PREFILL_EXACT_P) ? PF_P_EXACT : ((flags & ZX_PREFILL_FAST_P) ? PF_P_BF16 : PF_P_F16);
+  switch (G * 4 + pm) {
+#define ZX_PF_CASE(g, m) \
+  case g * 4 + m: paged_prefill_mfma_kernel<g, m><<<grid, PF_THREADS, 0, st>>>(a); break;
+    ZX_PF_CASE(4, PF_P_F16)
+    ZX_PF_CASE(4, PF_P_BF16)
+    ZX_PF_CASE(4, PF_P_EXACT)
+    ZX_PF_CASE(2, PF_P_F16)
+    ZX_PF_CASE(2, PF_P_BF16)
+    ZX_PF_CASE(2, PF_P_EXACT)
+    ZX_PF_CASE(1, PF_P_F16)
+    ZX_PF_CASE(1, PF_P_BF16)
+    ZX_PF_CASE(1, PF_P_EXACT)
+#undef ZX_PF_CASE
+    default: return fail(ZX_ERR_INVALID, "paged_attention_prefill: internal dispatch");
   }
   return check_launch("paged_prefill_mfma");
 }

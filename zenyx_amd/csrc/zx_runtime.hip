@@ -45,4 +45,4 @@ int num_cus() {
 
 extern "C" const char *zx_last_error(void) { return zx::g_msg; }
 
-extern "C" int zx_abi_version(void) { return 2; }
+extern "C" int zx_abi_version(void) { return 3; }

@@ -359,13 +359,32 @@ def paged_attention_decode(q: torch.Tensor, pool_layer: torch.Tensor, scales_lay
 
 # ------------------------------------------------------------------ Belady
 
+# How the softmax weights P enter P.V (the row sums use the same P); bound on |got - exact|
+# per output channel, beside one bf16 ulp of the exact value:
+#   "f16"   (default) P * 2^7 rounded once to fp16, V in fp16: 2^-10 max|V|;
+#   "bf16"  P rounded once to bf16 (ZX_PREFILL_FAST_P), the same speed: 2^-7 max|V|;
+#   "exact" P as bf16 hi + lo (ZX_PREFILL_EXACT_P), ~1.3x the time: 2^-15 max|V| at worst
+#           (measured within 2^-17 max|V|).
+PRECISIONS = ("f16", "bf16", "exact")
+
+
+def _precision_flag(precision: str) -> int:
+    if precision == "f16":
+        return 0
+    if precision == "bf16":
+        return N.ZX_PREFILL_FAST_P
+    if precision == "exact":
+        return N.ZX_PREFILL_EXACT_P
+    raise ValueError(f"precision must be one of {PRECISIONS}, got {precision!r}")
+
+
 def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor, pool_layer: torch.Tensor,
                             scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_begin: torch.Tensor,
                             kv_end: torch.Tensor, causal: bool = True, sm_scale: float | None = None,
                             o_acc: torch.Tensor | None = None, lse2: torch.Tensor | None = None,
                             first: bool = True, out: torch.Tensor | None = None, write_bf16: bool = True,
                             max_q_per_seq: int | None = None, check: bool = False,
-                            err: torch.Tensor | None = None, fast_p: bool = False):
+                            err: torch.Tensor | None = None, precision: str = "f16"):
     """One ring step of attention over the FP8 pages (zx_paged_attention_prefill).
 
     ``q`` [n_q, Hq, 128] bf16 rows of all sequences (``cu_q`` [B+1] int32 offsets,
@@ -374,7 +393,9 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
     / ``lse2`` (fp32 [n_q, Hq, 128] / [n_q, Hq]) the step merges into them (``first``
     overwrites); with ``write_bf16`` the (merged) rows go to ``out`` as bf16.  ``err`` (int32
     [1], zeroed by the caller) collects the kernel's input-error bits across several calls;
-    by default each call uses a fresh one.  Returns ``out`` (or None)."""
+    by default each call uses a fresh one.  ``precision``: see PRECISIONS.  Returns ``out``
+    (or None)."""
+    p_flag = _precision_flag(precision)
     N.require_device(q, "q")
     if q.dtype != torch.bfloat16 or q.dim() != 3:
         raise ValueError("q must be [n_q, n_q_heads, head_dim] bfloat16")
@@ -415,7 +436,7 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
         max_q_per_seq = int((cu_q[1:] - cu_q[:-1]).max().item()) if B else 0
     flags = (N.ZX_PREFILL_MERGE if o_acc is not None else 0) | (N.ZX_PREFILL_INIT if o_acc is not None and first
                                                                 else 0) | (N.ZX_PREFILL_BF16 if write_bf16 else 0) | \
-        (N.ZX_PREFILL_FAST_P if fast_p else 0)
+        p_flag
     sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
     dev = q.device
     if err is None:
@@ -436,14 +457,13 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
                          scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_begin: torch.Tensor,
                          kv_end: torch.Tensor, causal: bool = True, sm_scale: float | None = None,
                          max_q_per_seq: int | None = None, check: bool = False,
-                         err: torch.Tensor | None = None, fast_p: bool = False) -> torch.Tensor:
+                         err: torch.Tensor | None = None, precision: str = "f16") -> torch.Tensor:
     """All steps of a ring in one launch (zx_paged_attention_ring): ``kv_begin`` /
     ``kv_end`` int32 ``[R, B]`` hold step r's key range of every sequence; each block
     walks the R ranges with its running softmax state in registers and writes the bf16
-    rows once.  Same arguments and result as R paged_attention_prefill steps merged.
-    ``fast_p`` rounds the softmax weights once to bf16 for P.V (ZX_PREFILL_FAST_P: one
-    matrix product per tile instead of two, error bound one ulp + 2^-8 max|V| instead of
-    one ulp + 2^-17 max|V|)."""
+    rows once.  Same arguments and result as R paged_attention_prefill steps merged;
+    ``precision``: see PRECISIONS."""
+    p_flag = _precision_flag(precision)
     N.require_device(q, "q")
     if q.dtype != torch.bfloat16 or q.dim() != 3:
         raise ValueError("q must be [n_q, n_q_heads, head_dim] bfloat16")
@@ -476,7 +496,7 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
     N.check(N.load().zx_paged_attention_ring(
         N.ptr(q), n_q, N.ptr(cu_q), N.ptr(q_pos0), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer),
         N.ptr(block_tables), block_tables.shape[1], N.ptr(kv_begin), N.ptr(kv_end), kv_begin.shape[0], B,
-        int(max_q_per_seq), int(bool(causal)), sm, N.ZX_PREFILL_BF16 | (N.ZX_PREFILL_FAST_P if fast_p else 0), None,
+        int(max_q_per_seq), int(bool(causal)), sm, N.ZX_PREFILL_BF16 | p_flag, None,
         None, N.ptr(out), N.ptr(err),
         N.stream_ptr(q.device)), "paged_attention_ring")
     if check:
@@ -487,7 +507,7 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
 def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor, pool_layer: torch.Tensor,
                        scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_len: torch.Tensor,
                        ring_degree: int, causal: bool = True, sm_scale: float | None = None,
-                       check: bool = False, single_launch: bool = True, fast_p: bool = False) -> torch.Tensor:
+                       check: bool = False, single_launch: bool = True, precision: str = "f16") -> torch.Tensor:
     """Ring attention over the FP8 pages on one GPU: the keys [0, kv_len[b]) of every
     sequence are split into ``ring_degree`` shards (the KV blocks a ring would pass
     around), shard r being ring step r.  With ``single_launch`` one launch walks the R
@@ -495,8 +515,8 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     otherwise each step is its own launch (paged_attention_prefill, the unit a ring over R
     GPUs runs) merged into a running fp32 output and log-sum-exp, the last one writing
     bf16.  Either equals attention over all keys (the exchange between devices is what
-    one GPU leaves out).  ``fast_p``: softmax weights rounded once to bf16 for P.V (see
-    paged_attention_ring)."""
+    one GPU leaves out).  ``precision``: how P enters P.V (see PRECISIONS)."""
+    _precision_flag(precision)
     if ring_degree < 1:
         raise ValueError("ring_degree must be >= 1")
     n_q, Hq, D = q.shape
@@ -512,7 +532,7 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     if single_launch:
         out = paged_attention_ring(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables,
                                    bounds[:-1, :B].contiguous(), bounds[1:, :B].contiguous(), causal=causal,
-                                   sm_scale=sm_scale, max_q_per_seq=mq, err=err, fast_p=fast_p)
+                                   sm_scale=sm_scale, max_q_per_seq=mq, err=err, precision=precision)
         if check:
             _raise_kernel_error(err, "ring_attention_fp8")
         return out
@@ -523,7 +543,7 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
         paged_attention_prefill(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables, bounds[r, :B],
                                 bounds[r + 1, :B],
                                 causal=causal, sm_scale=sm_scale, o_acc=o_acc, lse2=lse2, first=r == 0, out=out,
-                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, err=err, fast_p=fast_p)
+                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, err=err, precision=precision)
     if check:
         _raise_kernel_error(err, "ring_attention_fp8")
     return out

@@ -180,14 +180,16 @@ class QuantizedRingAttention:
     in sequence.  ``decode`` is the one-token case (split-K decode kernel)."""
 
     def __init__(self, cache: PagedFP8KVCache, ring_degree: int = 8, causal: bool = True,
-                 sm_scale: float | None = None, fast_p: bool = False):
+                 sm_scale: float | None = None, precision: str = "f16"):
         if ring_degree < 1:
             raise ValueError("ring_degree must be >= 1")
         self.cache = cache
         self.ring_degree = ring_degree
         self.causal = causal
         self.sm_scale = sm_scale
-        self.fast_p = fast_p  # softmax weights rounded once to bf16 for P.V (ZX_PREFILL_FAST_P)
+        if precision not in kv.PRECISIONS:
+            raise ValueError(f"precision must be one of {kv.PRECISIONS}")
+        self.precision = precision  # how the softmax weights enter P.V (kv.PRECISIONS)
 
     def __call__(self, q: torch.Tensor, layer: int, seq_ids: list, q_lens: list[int]) -> torch.Tensor:
         """q ``[n_q, Hq, D]`` bf16: the queries of ``seq_ids[i]`` packed in order, ``q_lens[i]``
@@ -207,7 +209,8 @@ class QuantizedRingAttention:
             q.to(dev).contiguous(), torch.tensor(cu, dtype=torch.int32).to(dev),
             torch.tensor([m - n for n, m in zip(q_lens, lens)], dtype=torch.int32).to(dev), c.pool[layer],
             c.scales[layer].contiguous(), c._tables(seq_ids), torch.tensor(lens, dtype=torch.int32).to(dev),
-            ring_degree=self.ring_degree, causal=self.causal, sm_scale=self.sm_scale, check=True, fast_p=self.fast_p)
+            ring_degree=self.ring_degree, causal=self.causal, sm_scale=self.sm_scale, check=True,
+            precision=self.precision)
         c.check_errors()  # the appends behind these pages (the check above has synchronised)
         return out
 
