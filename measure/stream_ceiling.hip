@@ -605,6 +605,12 @@ int main(int argc, char **argv) {
     float ms = best_ms([&] { plain_stream<16, 8><<<(unsigned)((n + 255) / 256), 256>>>(x, out, n); }, 5);
     printf("heads: plain stream 2:1 over 2 GiB (one vector per thread): %.4f ms, %.1f GB/s of 3 GiB\n", ms,
            3.0 * (1L << 30) / ms / 1e6);
+    ms = best_ms([&] { read_fold<1><<<grid_for(n), 256>>>(xv, n, counter); }, 5);
+    printf("heads: read-only stream over 2 GiB (4 vectors in flight per thread, nontemporal): %.4f ms, %.1f GB/s\n",
+           ms, 2.0 * (1L << 30) / ms / 1e6);
+    ms = best_ms([&] { read_fold<0><<<grid_for(n), 256>>>(xv, n, counter); }, 5);
+    printf("heads: read-only stream over 2 GiB (default loads): %.4f ms, %.1f GB/s\n", ms,
+           2.0 * (1L << 30) / ms / 1e6);
     ms = best_ms([&] { heads_pattern<<<(unsigned)ncu, 1024>>>(xv, ov, n); }, 5);
     printf("heads: persistent grid (%d x 1024), contiguous 64 KiB shares, K = %d, NB = %d: %.4f ms, %.1f GB/s of "
            "3 GiB\n",

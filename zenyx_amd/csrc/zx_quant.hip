@@ -547,7 +547,7 @@ static int kv_scales_impl(const uint16_t *x, const RowGeom &g, int32_t n_layers,
   if (g.n_tok > 0) {
     const RowGeom8 r = row_geom8(g);
     const int64_t tiles = ceil_div(g.n_tok, (int64_t)KA_U * r.rpb);
-    const int64_t want = ceil_div((int64_t)num_cus() * 8, n_layers);
+    const int64_t want = ceil_div((int64_t)num_cus() * 4, n_layers);  // 4 blocks per CU: 1% faster than 8
     const unsigned gx = (unsigned)(tiles < want ? tiles : (want < 1 ? 1 : want));
     kv_amax_rows_kernel<KA_U><<<dim3(gx, n_layers), r.vpr8 * r.rpb, 0, st>>>(
         x, r, reinterpret_cast<uint32_t *>(scales));
