@@ -96,3 +96,56 @@ def test_build_ring_timeline_matches_reference():
 
     for n in (1, 2, 7):
         assert build_ring_timeline(n) == O.ref_ring_timeline(n)
+
+
+def header_constants():
+    """NAME -> value of every ZX_* constant the header defines (enum members and #defines)."""
+    text = open(os.path.join(ROOT, "include", "zenyx_kv.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    consts = {}
+    for name, val in re.findall(r"\b(ZX_[A-Z0-9_]+)\s*=\s*(-?\d+)", text):
+        consts[name] = int(val)
+    for name, val, sh in re.findall(r"#define\s+(ZX_[A-Z0-9_]+)\s+\(?(\d+)u?\s*(?:<<\s*(\d+))?", text):
+        consts[name] = int(val) << int(sh or 0)
+    return consts
+
+
+def test_header_constants_match_the_python_binding():
+    from zenyx_amd import _native as N
+
+    consts = header_constants()
+    for name in ("ZX_PREFILL_MERGE", "ZX_PREFILL_INIT", "ZX_PREFILL_BF16", "ZX_PREFILL_FAST_P", "ZX_PREFILL_EXACT_P",
+                 "ZX_HEADS_TWO_PASS", "ZX_HEADS_SINGLE_PASS", "ZX_APPEND_STATIC_SCALES", "ZX_APPEND_SATURATE",
+                 "ZX_APPEND_TWO_PASS", "ZX_KERR_PAGE_RANGE", "ZX_KERR_POS_RANGE", "ZX_KERR_SPIN", "ZX_KERR_OVERFLOW",
+                 "ZX_ERR_INVALID", "ZX_ERR_UNSUPPORTED", "ZX_ERR_WORKSPACE"):
+        assert name in consts, f"{name} not found in the header"
+        assert getattr(N, name) == consts[name], f"{name}: header {consts[name]}, binding {getattr(N, name)}"
+
+
+def test_exclusive_flags_are_refused_before_any_device_call():
+    from zenyx_amd import _native as N
+
+    lib = N.load()
+    p = ctypes.c_void_p(16)
+    rc = lib.zx_fp8_quant_heads(p, 1, 1, 1, 16, p, p, N.ZX_HEADS_TWO_PASS | N.ZX_HEADS_SINGLE_PASS, None, None, 0,
+                                None)
+    assert rc == N.ZX_ERR_INVALID and b"together" in lib.zx_last_error()
+    rc = lib.zx_fp8_quant_heads(p, 1, 1, 1, 16, p, p, 64, None, None, 0, None)
+    assert rc == N.ZX_ERR_INVALID and b"unknown flag" in lib.zx_last_error()
+    for fn, extra in ((lib.zx_paged_attention_prefill, ()), (lib.zx_paged_attention_ring, (1,))):
+        args = [p, 16, p, p, 8, p, 10, 2, 128, 16, p, p, 4] + [p, p] + list(extra) + [1, 16, 1, 0.1]
+        rc = fn(*args, N.ZX_PREFILL_BF16 | N.ZX_PREFILL_FAST_P | N.ZX_PREFILL_EXACT_P, None, None, p, None, None)
+        assert rc == N.ZX_ERR_INVALID and b"together" in lib.zx_last_error()
+
+
+def test_attention_precision_names():
+    import torch
+
+    from zenyx_amd import kv
+
+    assert kv.PRECISIONS == ("f16", "bf16", "exact")
+    t = torch.zeros(1)
+    with pytest.raises(ValueError, match="precision"):
+        kv.ring_attention_fp8(t, t, t, t, t, t, t, ring_degree=1, precision="fp8")
+    with pytest.raises(ValueError, match="precision"):
+        kv.paged_attention_prefill(t, t, t, t, t, t, t, t, precision="half")
