@@ -632,6 +632,7 @@ def configs0_leg(torch, dev, steps, warmup):
     del q8
     c8, sc8 = kv.fp8_quant_heads(big)
     ms_hq, _, _ = time_steps(torch, lambda: kv.fp8_quant_heads(big), steps, warmup)
+    ms_hq2, _, _ = time_steps(torch, lambda: kv.fp8_quant_heads(big, two_pass=True), steps, warmup)
     ms_hd, _, _ = time_steps(torch, lambda: kv.fp8_dequant_heads(c8, sc8), steps, warmup)
     del c8, big
     torch.cuda.empty_cache()
@@ -640,11 +641,16 @@ def configs0_leg(torch, dev, steps, warmup):
         "elements": nb, "dtype": "bf16",
         "int8_legacy_quant": {"ms": round(ms_lq, 4), "TBps_alg": tb(3, ms_lq), "TBps_moved": tb(5, ms_lq)},
         "int8_legacy_dequant": {"ms": round(ms_ld, 4), "TBps_alg": tb(3, ms_ld)},
-        "fp8_quant_heads": {"ms": round(ms_hq, 4), "TBps_alg": tb(3, ms_hq), "TBps_moved": tb(5, ms_hq)},
+        "fp8_quant_heads": {"ms": round(ms_hq, 4), "TBps_alg": tb(3, ms_hq),
+                            "frac": round(tb(3, ms_hq) * 1e3 / HBM_PEAK_GBPS, 4),
+                            "path": "single pass (heads_fused_kernel): 3 B/el moved"},
+        "fp8_quant_heads_two_pass": {"ms": round(ms_hq2, 4), "TBps_alg": tb(3, ms_hq2), "TBps_moved": tb(5, ms_hq2)},
         "fp8_dequant_heads": {"ms": round(ms_hd, 4), "TBps_alg": tb(3, ms_hd)},
-        "note": "quant = amax pass (2 B/el) + quant pass (2 B/el read, 1 written): 5 B/el moved, 3 B/el algorithmic"}
+        "note": "3 B/el algorithmic everywhere; the int8 legacy quant and the FP8 two-pass quant move 5 B/el "
+                "(amax pass 2 B/el + quant pass 2 B/el read, 1 written), the FP8 single pass 3 B/el; times are "
+                "whole calls (HIP events), kernel-only figures in profiles/fp8_heads_single_pass.md"}
     log(f"configs[0] functions at 1 Gi elements: int8 quant {ms_lq:.3f} ms, dequant {ms_ld:.3f} ms; fp8 heads quant "
-        f"{ms_hq:.3f} ms, dequant {ms_hd:.3f} ms")
+        f"{ms_hq:.3f} ms (two passes {ms_hq2:.3f} ms), dequant {ms_hd:.3f} ms")
     log(f"configs[0]: GPU fp8 {ms_f:.4f} ms, int8 per slab {ms_i:.4f} ms (loop {ms_il:.3f} ms); CPU {threads} threads fp8 "
         f"{cpu[threads][0]:.3f} s, 1 thread {cpu[1][0]:.3f} s; GPU == CPU: {same}, {same_i8}")
     return res
