@@ -10,9 +10,9 @@
 //     waits for slab s's scale, encodes slab s and refills that buffer with slab s+4, so
 //     loads stay in flight continuously and no block-wide barrier is ever taken;
 //   * a wave's max goes to an LDS slot (ds_max + arrival count); the control wave (the
-//     16th) stores the workgroup's max into its own device-coherent slot of slab s
-//     (slots start as a sentinel), reads all G slots of a slab with one wave-wide load
-//     until none is the sentinel, and broadcasts the finished scale through LDS.  It
+//     16th) stores the workgroup's max plus one into its own device-coherent slot of
+//     slab s (slots start at zero), reads all G slots of a slab with one wave-wide load
+//     until none is zero, and broadcasts the finished scale through LDS.  It
 //     publishes later slabs while still polling slab s, so their round trips overlap,
 //     and the data waves keep streaming throughout.
 // Loads and stores go through buffer resources, whose range check drops the lanes that
@@ -32,7 +32,8 @@ constexpr int FA_THREADS = 1024;
 constexpr int FA_DATA_WAVES = 15;
 constexpr int FA_DATA_THREADS = FA_DATA_WAVES * 64;
 constexpr int FA_SLOTS = 8;                 // LDS ring of per-slab reduction slots (>= NB + 1)
-constexpr uint32_t FA_EMPTY = 0xFFFFFFFFu;  // slot sentinel (a share max is at most 0x7FFF)
+// A slot holds a workgroup's share max (a bf16 magnitude, at most 0x7FFF) plus one, so the
+// zeroed workspace reads as "not published yet" (one fill clears flag and slots together).
 
 struct FusedArgs {
   const uint16_t *x;
@@ -44,7 +45,7 @@ struct FusedArgs {
   uint8_t *pool;
   int64_t pool_layer_stride;
   float *scales;
-  uint32_t *slots;  // [S][G] each workgroup's share max (bf16 magnitude), or FA_EMPTY
+  uint32_t *slots;  // [S][G] each workgroup's share max (bf16 magnitude) + 1, 0 until published
   uint32_t *abort_flag;
   int32_t *err;
   uint64_t spin_ticks;  // bound of one wait in s_memrealtime ticks (100 MHz)
@@ -220,7 +221,7 @@ __device__ __forceinline__ bool control_loop(const FusedArgs &a, FusedShared &sh
       ZX_COMPILER_FENCE();
       const uint32_t mx = ld_lds(&sh.max[slot]);
       if (lane == 0) {
-        __hip_atomic_store(&a.slots[(int64_t)next_pub * G + blockIdx.x], mx, __ATOMIC_RELAXED,
+        __hip_atomic_store(&a.slots[(int64_t)next_pub * G + blockIdx.x], mx + 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
         sh.max[slot] = 0;
         sh.cnt[slot] = 0;
@@ -234,11 +235,11 @@ __device__ __forceinline__ bool control_loop(const FusedArgs &a, FusedShared &sh
       bool full = true;
       for (uint32_t i = lane; i < G; i += 64) {
         const uint32_t v = __hip_atomic_load(&row[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        full = full && v != FA_EMPTY;
-        mx = max(mx, v == FA_EMPTY ? 0u : v);
+        full = full && v != 0u;
+        mx = max(mx, v);
       }
       if (__ballot(!full) == 0) {
-        mx = group_max(mx, 64);
+        mx = group_max(mx, 64) - 1u;
         const float sc = scale_from_amax_bits(mx << 16);
         const int slot = next_res & (FA_SLOTS - 1);
         if (lane == 0) {
@@ -434,10 +435,9 @@ int append_fused(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, in
   a.slots = reinterpret_cast<uint32_t *>(w + 256);
   a.err = err;
   a.spin_ticks = 200000000ull;  // 2 s without progress, at 100 MHz
-  // the abort flag starts at zero and every slot at the sentinel (fill kernels, not
-  // memsets, so the sequence stays valid inside a captured graph)
-  if ((rc = fill_u32(a.abort_flag, 1, 0, st))) return rc;
-  if ((rc = fill_u32(a.slots, S * G, FA_EMPTY, st))) return rc;
+  // the abort flag and every slot start at zero: one fill kernel (not a memset, so the
+  // sequence stays valid inside a captured graph) over the header and the slots
+  if ((rc = fill_u32(a.abort_flag, (256 + S * G * 4) / 4, 0, st))) return rc;
   void *args[] = {&a};
   const bool spill = ceil_div(n_tok, G) * (head_dim / 8) > (int64_t)FA_K * FA_DATA_THREADS;
   const bool wide = pool_layer_stride > FA_RANGE;  // pool offsets beyond 32-bit buffer offsets

@@ -10,9 +10,9 @@
 //     wave reduces step i + NB - 1 (loaded during step i - 1) and hands its max to the
 //     workgroup, waits for step i's scale, encodes step i and refills that buffer with step
 //     i + NB, so loads stay in flight and no block-wide barrier is taken;
-//   * the control wave (the 16th) publishes the workgroup's max into its own device-coherent
-//     slot of the slab (slots start as a sentinel), reads the g slots of the oldest
-//     published slab until none is the sentinel and broadcasts the scale through LDS.
+//   * the control wave (the 16th) publishes the workgroup's max (plus one) into its own
+//     device-coherent slot of the slab (slots start at zero), reads the g slots of the oldest
+//     published slab until none is zero and broadcasts the scale through LDS.
 // Each element is read from HBM once (2 B) and its code written once (1 B).  Loads and
 // stores go through buffer resources whose range ends at the member share, so lanes past
 // it need no branch.  Every wait is bounded in wall time; a timeout raises a global abort
@@ -34,7 +34,8 @@ constexpr int HF_K = HF_K_CHOICE;           // 16-byte vectors per data thread p
 constexpr int HF_NB = 4;                    // steps in flight (register buffers)
 constexpr int HF_SLOTS = 8;                 // LDS ring of per-step reduction slots (>= NB + 1)
 constexpr int64_t HF_SHARE_MAX = (int64_t)HF_K * HF_DATA_THREADS;  // vectors per member share
-constexpr uint32_t HF_EMPTY = 0xFFFFFFFFu;  // slot sentinel (a share max is at most 0x7FFF)
+// A slot holds a member's share max (a bf16 magnitude, at most 0x7FFF) plus one, so the
+// zeroed workspace reads as "not published yet" (one fill clears flag and slots together).
 
 struct HeadsFusedArgs {
   const uint16_t *x;
@@ -47,7 +48,7 @@ struct HeadsFusedArgs {
   int32_t g;       // members per slab = n_batch * m
   int32_t n_groups;
   int32_t n_slabs;  // n_outer * n_heads
-  uint32_t *slots;  // [n_slabs][g] each member's share max (bf16 magnitude), or HF_EMPTY
+  uint32_t *slots;  // [n_slabs][g] each member's share max (bf16 magnitude) + 1, 0 until published
   uint32_t *abort_flag;
   int32_t *err;
   uint64_t spin_ticks;  // bound of one wait in s_memrealtime ticks (100 MHz)
@@ -164,7 +165,7 @@ __device__ bool hf_control_loop(const HeadsFusedArgs &a, HeadsShared &sh, int gr
       const uint32_t mx = hf_ld_lds(&sh.max[slot]);
       if (lane == 0) {
         const int64_t s = group + (int64_t)next_pub * a.n_groups;
-        __hip_atomic_store(&a.slots[s * g + member], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&a.slots[s * g + member], mx + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         sh.max[slot] = 0;
         sh.cnt[slot] = 0;
       }
@@ -178,11 +179,11 @@ __device__ bool hf_control_loop(const HeadsFusedArgs &a, HeadsShared &sh, int gr
       bool full = true;
       for (uint32_t i = lane; i < g; i += 64) {
         const uint32_t v = __hip_atomic_load(&row[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        full = full && v != HF_EMPTY;
-        mx = max(mx, v == HF_EMPTY ? 0u : v);
+        full = full && v != 0u;
+        mx = max(mx, v);
       }
       if (__ballot(!full) == 0) {
-        mx = group_max(mx, 64);
+        mx = group_max(mx, 64) - 1u;
         const float sc = scale_from_amax_bits(mx << 16);
         const int slot = next_res & (HF_SLOTS - 1);
         if (lane == 0) {
@@ -340,8 +341,8 @@ int heads_fused(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_h
   a.slots = reinterpret_cast<uint32_t *>(w + 256);
   a.err = err;
   a.spin_ticks = 200000000ull;  // 2 s without progress, at 100 MHz
-  if ((rc = fill_u32(a.abort_flag, 1, 0, st))) return rc;
-  if ((rc = fill_u32(a.slots, (int64_t)a.n_slabs * p.g, HF_EMPTY, st))) return rc;
+  // the abort flag and every slot start at zero: one fill kernel over the header and slots
+  if ((rc = fill_u32(a.abort_flag, (256 + (int64_t)a.n_slabs * p.g * 4) / 4, 0, st))) return rc;
   void *args[] = {&a};
   ZX_TRY_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(heads_fused_kernel),
                                         dim3((unsigned)(p.n_groups * p.g)), dim3(HF_THREADS), args, 0, st));

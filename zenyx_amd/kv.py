@@ -29,6 +29,13 @@ def _err_word(device) -> torch.Tensor:
     return torch.zeros(1, dtype=torch.int32, device=device)
 
 
+def _err_word_if(check: bool, device) -> torch.Tensor | None:
+    """A fresh device error word when the call will read it (check=True), else None: the
+    kernels then skip their error reports (every one is guarded), and the call saves the
+    word's fill kernel."""
+    return _err_word(device) if check else None
+
+
 def kernel_error_text(e: int) -> str:
     """The ZX_KERR_* bits of a device error word, in words."""
     parts = []
@@ -150,7 +157,7 @@ def fp8_quant_heads(x: torch.Tensor, two_pass: bool = False, check: bool = False
     if two_pass and single_pass:
         raise ValueError("fp8_quant_heads: two_pass and single_pass are exclusive")
     ws = None if two_pass else _workspace(lib.zx_fp8_quant_heads_workspace_bytes(O, B, H, R), x.device)
-    err = _err_word(x.device)
+    err = _err_word_if(check, x.device)
     flags = N.ZX_HEADS_TWO_PASS if two_pass else (N.ZX_HEADS_SINGLE_PASS if single_pass else 0)
     N.check(lib.zx_fp8_quant_heads(N.ptr(x), O, B, H, R, N.ptr(codes), N.ptr(scales),
                                    flags, N.ptr(err), N.ptr(ws),
@@ -258,7 +265,7 @@ def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: tor
     lib = N.load()
     ws = _workspace(lib.zx_kv_quant_append_workspace_bytes(L, T, H, D), x.device)
     if err is None:
-        err = _err_word(x.device)
+        err = _err_word_if(check, x.device)
     elif err.dtype != torch.int32 or err.numel() < 1 or err.device != x.device:
         raise ValueError("err must be an int32 tensor on x's device")
     flags = (N.ZX_APPEND_STATIC_SCALES if static_scales else 0) | (N.ZX_APPEND_TWO_PASS if two_pass else 0) | \
@@ -303,7 +310,7 @@ def kv_gather_dequant(pool_layer: torch.Tensor, scales_layer: torch.Tensor, bloc
             if t.shape != (B, H, out_len, D) or t.dtype != torch.bfloat16:
                 raise ValueError(f"out tensors must be bf16 {(B, H, out_len, D)}")
             N.require_device(t, "out")
-    err = _err_word(pool_layer.device)
+    err = _err_word_if(check, pool_layer.device)
     N.check(N.load().zx_kv_gather_dequant(N.ptr(pool_layer), n_pages, H, D, P, N.ptr(scales_layer),
                                           N.ptr(block_tables), block_tables.shape[1], N.ptr(seq_lens), B,
                                           out_len, N.ptr(k), N.ptr(v), N.ptr(err),
@@ -347,7 +354,7 @@ def paged_attention_decode(q: torch.Tensor, pool_layer: torch.Tensor, scales_lay
     lib = N.load()
     mb = block_tables.shape[1]
     ws = _workspace(lib.zx_paged_attention_decode_workspace_bytes(B, Hq, Hkv, D, mb, P), q.device)
-    err = _err_word(q.device)
+    err = _err_word_if(check, q.device)
     N.check(lib.zx_paged_attention_decode(
         N.ptr(q), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer), N.ptr(block_tables), mb,
         N.ptr(seq_lens), B, float(D ** -0.5 if sm_scale is None else sm_scale), N.ptr(out), N.ptr(err), N.ptr(ws),
@@ -440,7 +447,7 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
     sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
     dev = q.device
     if err is None:
-        err = _err_word(dev)
+        err = _err_word_if(check, dev)
     elif err.dtype != torch.int32 or err.numel() < 1 or err.device != dev:
         raise ValueError("err must be an int32 tensor on q's device")
     N.check(N.load().zx_paged_attention_prefill(
@@ -492,7 +499,7 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
     out = torch.empty_like(q)
     sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
     if err is None:
-        err = _err_word(q.device)
+        err = _err_word_if(check, q.device)
     N.check(N.load().zx_paged_attention_ring(
         N.ptr(q), n_q, N.ptr(cu_q), N.ptr(q_pos0), Hq, N.ptr(pool_layer), n_pages, Hkv, D, P, N.ptr(scales_layer),
         N.ptr(block_tables), block_tables.shape[1], N.ptr(kv_begin), N.ptr(kv_end), kv_begin.shape[0], B,
@@ -528,7 +535,7 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     steps = torch.arange(ring_degree + 1, dtype=torch.int64, device=kv_len.device)
     bounds = torch.empty((ring_degree + 1, (B + 3) // 4 * 4), dtype=torch.int32, device=kv_len.device)
     bounds[:, :B] = kv_len.to(torch.int64)[None, :] * steps[:, None] // ring_degree
-    err = _err_word(q.device)
+    err = _err_word_if(check, q.device)
     if single_launch:
         out = paged_attention_ring(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables,
                                    bounds[:-1, :B].contiguous(), bounds[1:, :B].contiguous(), causal=causal,
@@ -575,7 +582,7 @@ def next_use(trace: torch.Tensor, n_pages: int, check: bool = False):
     pu = torch.empty(n, dtype=torch.int32, device=trace.device)
     lib = N.load()
     ws = _workspace(lib.zx_belady_next_use_workspace_bytes(n, n_pages), trace.device)
-    err = _err_word(trace.device)
+    err = _err_word_if(check, trace.device)
     N.check(lib.zx_belady_next_use(N.ptr(trace), n, n_pages, N.ptr(nu), N.ptr(pu), N.ptr(err), N.ptr(ws),
                                    ws.numel(), N.stream_ptr(trace.device)), "belady_next_use")
     if check:
@@ -708,7 +715,7 @@ def belady_tier_plan(sim0: "BeladyTraceSim", sim01: "BeladyTraceSim", check: boo
     src = torch.empty(n, dtype=torch.uint8, device=dev)
     v0 = torch.empty(n, dtype=torch.int32, device=dev)
     v1 = torch.empty(n, dtype=torch.int32, device=dev)
-    err = _err_word(dev)
+    err = _err_word_if(check, dev)
     N.check(N.load().zx_belady_tier_plan(
         N.ptr(sim0.prev_use), N.ptr(sim0.miss_flags), N.ptr(sim01.miss_flags), n,
         N.ptr(sim0.evict_pos), N.ptr(sim0.evict_page), sim0.n_evicted,
