@@ -17,6 +17,8 @@ Eviction policy, capacities, KeyError on unknown ids and the aliasing of CPU ten
 """
 from __future__ import annotations
 
+import threading
+
 import ctypes
 from collections import OrderedDict
 from dataclasses import dataclass
@@ -64,23 +66,27 @@ class _HostKeepAlive:
     """
 
     _pending: list = []  # (event, tensor), in the order the copies were queued
+    _lock = threading.Lock()  # the list is shared by every mover of the process
 
     @classmethod
     def hold(cls, tensor: torch.Tensor, stream: torch.cuda.Stream) -> None:
         ev = torch.cuda.Event()
         ev.record(stream)
-        cls.release_done()
-        cls._pending.append((ev, tensor))
+        with cls._lock:
+            cls._pending = [(e, t) for e, t in cls._pending if not e.query()]
+            cls._pending.append((ev, tensor))
 
     @classmethod
     def release_done(cls) -> None:
-        cls._pending = [(ev, t) for ev, t in cls._pending if not ev.query()]
+        with cls._lock:
+            cls._pending = [(ev, t) for ev, t in cls._pending if not ev.query()]
 
     @classmethod
     def release_all(cls) -> None:
-        for ev, _ in cls._pending:
+        with cls._lock:
+            pending, cls._pending = cls._pending, []
+        for ev, _ in pending:
             ev.synchronize()
-        cls._pending = []
 
 
 def keep_host_alive(tensor: torch.Tensor, stream: torch.cuda.Stream) -> None:
