@@ -12,7 +12,8 @@
 //            rows of 4 KiB (2 x 8 heads x 128 bf16) cannot stay on chip (302 MB at
 //            configs[1] versus ~170 MB of registers + LDS on 256 CUs), and a slab's scale
 //            needs its amax over all tokens, so each step reads one 256-byte slab of every
-//            row, with NB = 4 steps in flight per workgroup, and writes 128 bytes per row.
+//            row, with NB = 4 steps in flight per workgroup, and writes 128 bytes per row,
+//            contiguously per slab or (as the append does) into 16-token pages in random order.
 //            Run as a persistent grid (one 1024-thread workgroup per CU) with the token
 //            share of every workgroup fixed (as the fused append does) and with chunks of
 //            64 tokens dealt out per slab by an atomic counter;
@@ -118,10 +119,12 @@ constexpr int SC_ROW = 4096, SC_SLAB = 256, SC_SLABS_PER_ROW = SC_ROW / SC_SLAB;
 
 struct PatternArgs {
   const char *x;  // [L][T][4096 B]
-  char *out;      // [L * 16][T][128 B]
+  char *out;      // [L * 16][T][128 B], or with `page` the pool [L][T / 16 pages][16 slabs][16][128 B]
   long T;
   int n_slabs, n_chunks, dynamic;
   unsigned *counter;  // [n_slabs], zero at launch (dynamic only)
+  const int *page;    // null, or the page of each group of 16 tokens (a permutation): the
+                      // append's destination, 2 KiB runs of one slab 32 KiB apart
 };
 
 __device__ __forceinline__ sc_v4u pat_load(const PatternArgs &a, int s, int c, int tid) {
@@ -136,7 +139,15 @@ __device__ __forceinline__ void pat_store(const PatternArgs &a, int s, int c, in
   const long tok = (long)c * SC_CT + tid / 16;
   if (c < 0 || s >= a.n_slabs || tok >= a.T) return;
   const sc_v2u o = {v.x ^ v.y, v.z ^ v.w};
-  __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(a.out + ((long)s * a.T + tok) * 128 + (tid % 16) * 8));
+  long off;
+  if (a.page) {
+    const int l = s / SC_SLABS_PER_ROW, j = s % SC_SLABS_PER_ROW;
+    const long pages = (a.T + 15) / 16;
+    off = (((long)l * pages + a.page[tok >> 4]) * SC_SLABS_PER_ROW + j) * 2048 + (tok & 15) * 128;
+  } else {
+    off = ((long)s * a.T + tok) * 128;
+  }
+  __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(a.out + off + (tid % 16) * 8));
 }
 
 __global__ void __launch_bounds__(SC_TPB) append_pattern(PatternArgs a) {
@@ -483,19 +494,35 @@ int main(int argc, char **argv) {
     if ((long)ncu * SC_K < chunks) {
       printf("append pattern skipped: %d CUs x %d chunks < %d chunks per slab\n", ncu, SC_K, chunks);
     } else {
-      for (int dyn = 0; dyn < 2; ++dyn) {
-        PatternArgs a{x, out, T, L * SC_SLABS_PER_ROW, chunks, dyn, counter};
-        const float ms = best_ms(
-            [&] {
-              SC_CHECK(hipMemsetAsync(counter, 0, 4096 * sizeof(unsigned)));
-              append_pattern<<<ncu, SC_TPB>>>(a);
-            },
-            5);
-        printf("append pattern, %s shares (256 B of each 4 KiB row per step, %d steps in flight): %.3f ms, %.1f "
-               "GB/s\n",
-               dyn ? "dynamic" : "static", SC_NB, ms, (in_bytes + out_bytes) / ms / 1e6);
-        fflush(stdout);
+      // a random page order for the paged destination (the same for every layer)
+      const long pages = (T + 15) / 16;
+      int *page_h = static_cast<int *>(malloc(pages * sizeof(int)));
+      for (long i = 0; i < pages; ++i) page_h[i] = (int)i;
+      srand(5);
+      for (long i = pages - 1; i > 0; --i) {
+        const long k = rand() % (i + 1);
+        std::swap(page_h[i], page_h[k]);
       }
+      int *page_d = nullptr;
+      SC_CHECK(hipMalloc(&page_d, pages * sizeof(int)));
+      SC_CHECK(hipMemcpy(page_d, page_h, pages * sizeof(int), hipMemcpyHostToDevice));
+      free(page_h);
+      for (int paged = 0; paged < 2; ++paged)
+        for (int dyn = 0; dyn < 2; ++dyn) {
+          PatternArgs a{x, out, T, L * SC_SLABS_PER_ROW, chunks, dyn, counter, paged ? page_d : nullptr};
+          const float ms = best_ms(
+              [&] {
+                SC_CHECK(hipMemsetAsync(counter, 0, 4096 * sizeof(unsigned)));
+                append_pattern<<<ncu, SC_TPB>>>(a);
+              },
+              5);
+          printf("append pattern, %s shares, %s (256 B of each 4 KiB row per step, %d steps in flight): %.3f ms, "
+                 "%.1f GB/s\n",
+                 dyn ? "dynamic" : "static", paged ? "writes into random pages" : "contiguous writes", SC_NB, ms,
+                 (in_bytes + out_bytes) / ms / 1e6);
+          fflush(stdout);
+        }
+      SC_CHECK(hipFree(page_d));
     }
   }
   if (want(sel, "columns")) {
