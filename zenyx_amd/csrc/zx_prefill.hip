@@ -292,13 +292,20 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     for (int KT = 0; KT < 4; ++KT) tok[KT] = tile_ok(s0 + 16 * KT, ke);
     // S^T tiles: sc[rt][KT] lane (n, kg) holds keys 16 KT + 4 kg + i of row 16 rt + n
     att_f32x4 sc[2][4];
-#pragma unroll
-    for (int KT = 0; KT < 4; ++KT) {
-      att_bf16x8 ka[4];  // A operand: key 16 KT + n, channels 32 kg + 8 c ..+8
+    // A operand: key 16 KT + n, channels 32 kg + 8 c ..+8, read one tile ahead
+    att_bf16x8 kar[2][4];
+    auto ld_ka = [&](int KT, att_bf16x8 (&dst)[4]) {
       const uint8_t *kr = &kst[buf][(16 * KT + n) * PF_KROW + kg * 64];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        ka[c] = __builtin_bit_cast(att_bf16x8, *reinterpret_cast<const att_u32x4 *>(kr + 16 * c));
+        dst[c] = __builtin_bit_cast(att_bf16x8, *reinterpret_cast<const att_u32x4 *>(kr + 16 * c));
+    };
+    ld_ka(0, kar[0]);
+#pragma unroll
+    for (int KT = 0; KT < 4; ++KT) {
+      if (KT + 1 < 4) ld_ka(KT + 1, kar[(KT + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const att_bf16x8 (&ka)[4] = kar[KT & 1];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         att_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -381,14 +388,26 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
       }
     }
     store_step(buf ^ 1, kc, vc);
-    // A operand per 16-channel tile and k-block: V^T[channel 16 jt + n][k 8 kg ..+8]
-#pragma unroll
-    for (int jt = 0; jt < 8; ++jt) {
+    // A operand per 16-channel tile and k-block: V^T[channel 16 jt + n][k 8 kg ..+8],
+    // read PVD tiles ahead of its products (the scheduling barrier keeps the compiler
+    // from sinking the reads next to their use: 2% on the ring workload)
+    constexpr int PVD = 2;
+    att_u32x4 avr[PVD + 1][2];
+    auto ld_av = [&](int jt, att_u32x4 (&dst)[2]) {
       const int ch = 16 * jt + n;
 #pragma unroll
+      for (int kbk = 0; kbk < 2; ++kbk)
+        dst[kbk] = *reinterpret_cast<const att_u32x4 *>(&vtl[buf][ch * PF_VROW + ((((kbk << 2) + kg) ^ jt) << 4)]);
+    };
+#pragma unroll
+    for (int jt = 0; jt < PVD; ++jt) ld_av(jt, avr[jt]);
+#pragma unroll
+    for (int jt = 0; jt < 8; ++jt) {
+      if (jt + PVD < 8) ld_av(jt + PVD, avr[(jt + PVD) % (PVD + 1)]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
       for (int kbk = 0; kbk < 2; ++kbk) {
-        const att_u32x4 av =
-            *reinterpret_cast<const att_u32x4 *>(&vtl[buf][ch * PF_VROW + ((((kbk << 2) + kg) ^ jt) << 4)]);
+        const att_u32x4 av = avr[jt % (PVD + 1)][kbk];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
           if constexpr (F16) {
