@@ -257,35 +257,46 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     vc[0] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 2);
     vc[1] = __builtin_amdgcn_raw_buffer_load_b128(rv, off + D, 0, 2);
   };
-  auto store_step = [&](int buf, const att_u32x4 (&kc)[2], const att_u32x4 (&vc)[2]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {  // K decoded once per block, read as bf16 by the 4 waves
+  // K/V of one step stored into an LDS buffer, in 8 pieces so that the store can be spread
+  // over the matrix products of the step before: 0, 1 the two K rows (decoded once per
+  // block, read as bf16 by the 4 waves); 2 the V decode into v0, v1; 3 .. 6 two V^T channel
+  // pairs each (channel c = 16 g8 + 2 p (+1) gets keys kk0, kk0 + 1, adjacent k slots, as
+  // one word); 7 nothing
+  auto store_piece = [&](int buf, int j, const att_u32x4 (&kc)[2], const att_u32x4 (&vc)[2], uint32_t (&v0)[8],
+                         uint32_t (&v1)[8]) {
+    if (j < 2) {
       uint32_t kb8[8];
       decode16_bf16(make_uint4(kc[j].x, kc[j].y, kc[j].z, kc[j].w), kb8);
       uint4 *kd = reinterpret_cast<uint4 *>(&kst[buf][(kk0 + j) * PF_KROW + 32 * g8]);
       kd[0] = make_uint4(kb8[0], kb8[1], kb8[2], kb8[3]);
       kd[1] = make_uint4(kb8[4], kb8[5], kb8[6], kb8[7]);
-    }
-    // V^T: channel c = 16 g8 + 2 p (+1) gets keys kk0, kk0 + 1 (adjacent k slots) as one word
-    uint32_t v0[8], v1[8];
-    if constexpr (F16) {
-      decode16_f16(make_uint4(vc[0].x, vc[0].y, vc[0].z, vc[0].w), v0);
-      decode16_f16(make_uint4(vc[1].x, vc[1].y, vc[1].z, vc[1].w), v1);
-    } else {
-      decode16_bf16(make_uint4(vc[0].x, vc[0].y, vc[0].z, vc[0].w), v0);
-      decode16_bf16(make_uint4(vc[1].x, vc[1].y, vc[1].z, vc[1].w), v1);
-    }
-    const int slot0 = pf_vslot_byte(16 * g8, kk0);  // channel 16 g8; the others add c * PF_VROW
+    } else if (j == 2) {
+      if constexpr (F16) {
+        decode16_f16(make_uint4(vc[0].x, vc[0].y, vc[0].z, vc[0].w), v0);
+        decode16_f16(make_uint4(vc[1].x, vc[1].y, vc[1].z, vc[1].w), v1);
+      } else {
+        decode16_bf16(make_uint4(vc[0].x, vc[0].y, vc[0].z, vc[0].w), v0);
+        decode16_bf16(make_uint4(vc[1].x, vc[1].y, vc[1].z, vc[1].w), v1);
+      }
+    } else if (j < 7) {
+      const int slot0 = pf_vslot_byte(16 * g8, kk0);  // channel 16 g8; the others add c * PF_VROW
 #pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      uint8_t *row = &vtl[buf][slot0 + 2 * p * PF_VROW];
-      *reinterpret_cast<uint32_t *>(row) = __builtin_amdgcn_perm(v1[p], v0[p], 0x05040100u);
-      *reinterpret_cast<uint32_t *>(row + PF_VROW) = __builtin_amdgcn_perm(v1[p], v0[p], 0x07060302u);
+      for (int pp = 0; pp < 2; ++pp) {
+        const int p = 2 * (j - 3) + pp;
+        uint8_t *row = &vtl[buf][slot0 + 2 * p * PF_VROW];
+        *reinterpret_cast<uint32_t *>(row) = __builtin_amdgcn_perm(v1[p], v0[p], 0x05040100u);
+        *reinterpret_cast<uint32_t *>(row + PF_VROW) = __builtin_amdgcn_perm(v1[p], v0[p], 0x07060302u);
+      }
     }
   };
+  auto store_step = [&](int buf, const att_u32x4 (&kc)[2], const att_u32x4 (&vc)[2]) {
+    uint32_t v0[8], v1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) store_piece(buf, j, kc, vc, v0, v1);
+  };
 
-  // one step: S^T, softmax, then the next step's K/V stored into the other LDS buffer
-  // (free since the last barrier) ahead of the PV products so the two can overlap
+  // one step: S^T, softmax, then the P.V products with the next step's K/V stored between
+  // them
   auto compute_step = [&](int buf, int s0, int kb, int ke, const att_u32x4 (&kc)[2], const att_u32x4 (&vc)[2]) {
     bool tok[4];
 #pragma unroll
@@ -387,7 +398,10 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
         ol[rt] *= alpha[rt];
       }
     }
-    store_step(buf ^ 1, kc, vc);
+    // the next step's K/V goes into the other LDS buffer (free since the last barrier), one
+    // store piece per P.V tile, so that its VALU and LDS work sit beside the products (2%
+    // on the ring workload against storing it whole before them)
+    uint32_t nv0[8], nv1[8];  // the next step's V, decoded by store piece 2
     // A operand per 16-channel tile and k-block: V^T[channel 16 jt + n][k 8 kg ..+8],
     // read PVD tiles ahead of its products (the scheduling barrier keeps the compiler
     // from sinking the reads next to their use: 2% on the ring workload)
@@ -418,6 +432,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
           }
         }
       }
+      store_piece(buf ^ 1, jt, kc, vc, nv0, nv1);
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int kbk = 0; kbk < 2; ++kbk)
