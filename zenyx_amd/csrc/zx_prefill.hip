@@ -236,17 +236,34 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     const int64_t page = bt[pf_page_of(a, (uint32_t)tp)];
     return page >= 0 && page < a.n_pages;
   };
-  auto load_step = [&](int s0, int ke, att_u32x4 (&kc)[2], att_u32x4 (&vc)[2]) {
+  // a step's page, looked up one step before its K/V loads are issued, so that the
+  // block-table read is never waited for on its own (3% on the ring workload).  The row's
+  // byte size fits the resource: page_size >= 16 and max_blocks * page_size < 2^31.
+  const __amdgpu_buffer_rsrc_t rbt = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t *>(bt), (short)0, a.max_blocks * (int)sizeof(int32_t), 0x00020000);
+  struct StepPage {
+    int tc, live;
+    uint32_t bi;
+    int32_t page;
+  };
+  auto lookup_step = [&](int s0, int ke) -> StepPage {
+    StepPage p;
     const int tp = s0 + 16 * wave;  // this wave's 16-key tile (scalar: the buffer resources stay in SGPRs)
-    const int live = max(0, min(16, ke - tp));
-    const int tc = tp < ke ? tp : (ke > 0 ? ke - 1 : 0);
-    const uint32_t bi = pf_page_of(a, (uint32_t)tc);
-    const int64_t page = bt[bi];
-    const bool ok = live > 0 && page >= 0 && page < a.n_pages;
-    e |= (live > 0 && !ok) ? ZX_KERR_PAGE_RANGE : 0;
-    const int nrec = ok ? live * D : 0;
+    p.live = max(0, min(16, ke - tp));
+    p.tc = tp < ke ? tp : (ke > 0 ? ke - 1 : 0);
+    p.bi = pf_page_of(a, (uint32_t)p.tc);
+    // a range-checked load (entries past the block table read as 0; a tile with no key
+    // never uses its page), issued without a branch so the wait for it can be counted
+    p.page = __builtin_amdgcn_raw_buffer_load_b32(rbt, (int)(p.bi * 4u), 0, 0);
+    return p;
+  };
+  auto issue_step = [&](const StepPage &p, att_u32x4 (&kc)[2], att_u32x4 (&vc)[2]) {
+    const int64_t page = __builtin_amdgcn_readfirstlane(p.page);
+    const bool ok = p.live > 0 && page >= 0 && page < a.n_pages;
+    e |= (p.live > 0 && !ok) ? ZX_KERR_PAGE_RANGE : 0;
+    const int nrec = ok ? p.live * D : 0;
     const uint8_t *src =
-        a.pool + (ok ? page * page_bytes + head_off + (int64_t)(tc - (int)bi * a.page_size) * D : 0);
+        a.pool + (ok ? page * page_bytes + head_off + (int64_t)(p.tc - (int)p.bi * a.page_size) * D : 0);
     const __amdgpu_buffer_rsrc_t rk =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(src), (short)0, nrec, 0x00020000);
     const __amdgpu_buffer_rsrc_t rv =
@@ -448,33 +465,49 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
       }
   };
 
-  // steps: data of step s + 1 loaded into registers while step s computes; one barrier
-  // per step (the LDS buffers alternate).  The steps of the ranges follow each other (the
-  // step after a range's last one is the next non-empty range's first), with the running
-  // row maxima, O and row sums carried in registers from range to range.  The last step
-  // also loads and stores a step after it (zero-length loads; that buffer is never read).
+  // steps: data of step s + 1 loaded into registers and the page of step s + 2 looked up
+  // while step s computes; one barrier per step (the LDS buffers alternate).  The steps of
+  // the ranges follow each other (the step after a range's last one is the next non-empty
+  // range's first), with the running row maxima, O and row sums carried in registers from
+  // range to range.  The last step also loads and stores a step after it (zero-length
+  // loads; that buffer is never read).  Positions: p0 the step being computed, p1 the next
+  // one (K/V loading), p2 the one after (page looked up); a position past the last range
+  // stays there (s = 0, ke = 0).
+  struct Pos {
+    int s, rc;
+    Range g;
+  };
+  auto advance = [&](const Pos &p) -> Pos {
+    Pos q = p;
+    if (p.rc >= a.n_ranges) return q;
+    q.s = p.s + PF_KEYS;
+    if (q.s >= p.g.ke_blk) {
+      q.rc = next_range(p.rc + 1, q.g);
+      q.s = q.rc < a.n_ranges ? q.g.s_first : 0;
+    }
+    return q;
+  };
+  auto ke_of = [&](const Pos &p) { return p.rc < a.n_ranges ? p.g.ke : 0; };
   att_u32x4 kc[2], vc[2];
-  int s0 = cur.s_first;
-  if (rc < a.n_ranges) {
-    load_step(s0, cur.ke, kc, vc);
+  Pos p0 = {cur.s_first, rc, cur};
+  if (p0.rc < a.n_ranges) {
+    issue_step(lookup_step(p0.s, p0.g.ke), kc, vc);
     store_step(0, kc, vc);
   }
+  Pos p1 = advance(p0);
+  StepPage pg1 = lookup_step(p1.s, ke_of(p1));
   __syncthreads();
   int buf = 0;
-  while (rc < a.n_ranges) {
-    Range nxt = cur;
-    int rn = rc, s1 = s0 + PF_KEYS;
-    if (s1 >= cur.ke_blk) {
-      rn = next_range(rc + 1, nxt);
-      s1 = rn < a.n_ranges ? nxt.s_first : 0;
-    }
-    load_step(s1, rn < a.n_ranges ? nxt.ke : 0, kc, vc);
-    compute_step(buf, s0, cur.kb, cur.ke, kc, vc);
+  while (p0.rc < a.n_ranges) {
+    const Pos p2 = advance(p1);
+    issue_step(pg1, kc, vc);
+    const StepPage pg2 = lookup_step(p2.s, ke_of(p2));
+    compute_step(buf, p0.s, p0.g.kb, p0.g.ke, kc, vc);
     __syncthreads();
     buf ^= 1;
-    s0 = s1;
-    rc = rn;
-    cur = nxt;
+    p0 = p1;
+    p1 = p2;
+    pg1 = pg2;
   }
 
   // rows: normalise; merge; store channels 16 jt + 4 kg ..+4
