@@ -341,7 +341,12 @@ int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, i
  *   ZX_PREFILL_BF16: also write the (merged) rows to out as bf16.
  * Running every step of a ring with MERGE (INIT on the first) and BF16 on the last gives
  * attention over the union of the steps' key ranges.  Needs head_dim 128 and a page size
- * that is a multiple of 16. */
+ * that is a multiple of 16.
+ * NaN codes (e4m3 0x7F / 0xFF): a NaN K element makes the rows that see its key NaN in
+ * every channel (lse2 -inf); a NaN V element makes its channel NaN in the rows that see
+ * its key, and may also do so in rows before the key whose 64-key step holds it (the
+ * product of the step multiplies their weight 0 by the NaN); a merge keeps a NaN of an
+ * earlier step. */
 enum {
   ZX_PREFILL_MERGE = 1,
   ZX_PREFILL_INIT = 2,

@@ -23,7 +23,7 @@ import torch
 
 from oracle import oracle as O
 from zenyx_amd import kv
-from test_gpu_attention import assert_within_bound
+from test_gpu_attention import assert_within_bound, bf16_to_f32
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -62,7 +62,7 @@ def vmax_rows(pool, scales, bt, cu, kv_begin, kv_end, Hq):
         pages = bt[b, t // P]
         for hq in range(Hq):
             h = hq // (Hq // Hkv)
-            out[cu[b]:cu[b + 1], hq] = dec[pool[pages, 1, h, t % P, :]].max(axis=0) * float(scales[1, h])
+            out[cu[b]:cu[b + 1], hq] = np.nanmax(dec[pool[pages, 1, h, t % P, :]], axis=0) * float(scales[1, h])
     return out
 
 
@@ -212,6 +212,67 @@ def test_ring_ranges_in_device_order(causal):
         assert err == 0
         vmax = c["vmax"]
     assert_precision(bits16(out), want, vmax)
+
+
+def assert_nan_leak_only_in_window(got_bits, want_bits, vmax, precision, leak):
+    """got equals want to the precision bound, NaN compared as a class, except that got may
+    be NaN where want is not inside the boolean mask ``leak``."""
+    g, w = bf16_to_f32(got_bits), bf16_to_f32(want_bits)
+    extra = np.isnan(g) & ~np.isnan(w)
+    assert not (extra & ~leak).any(), f"{(extra & ~leak).sum()} NaN outside the leak window"
+    assert not (np.isnan(w) & ~np.isnan(g)).any(), "a NaN of the oracle is missing"
+    keep = ~extra
+    assert_precision(got_bits[keep], want_bits[keep], vmax[keep], precision)
+    return int(extra.sum())
+
+
+@pytest.mark.parametrize("precision", ["f16", "exact", "bf16"])
+def test_nan_codes_propagate_like_the_oracle(precision):
+    """NaN codes (e4m3 0x7F / 0xFF) in the pages.  A NaN K element makes every score of its
+    key NaN: each row that sees the key is NaN in every channel, with lse2 -inf (the
+    oracle's softmax denominator is NaN), and no other row changes (a masked score never
+    reaches P).  A NaN V element makes its own channel NaN in the rows that see it; since
+    the P.V product of a 64-key step multiplies the weight 0 of a key a row does not see
+    by that key's V, rows before the key whose step holds it may also be NaN in that
+    channel (as in tiled attention generally; the oracle skips such keys), and nothing
+    else.  Checked for one step, and for ring attention over 3 shards in one launch and in
+    separate launches merged through o_acc / lse2, where a NaN of the first step has to
+    survive the later merges, which give it weight 0."""
+    Hq, Hkv, P = 8, 2, 16
+    n_q, q_pos0, lens = [48, 40], [0, 24], [48, 64]
+    print(f"nan codes precision={precision}", flush=True)
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, n_q, q_pos0, lens, seed=31)
+    pool[bt[0, 5 // P], 0, 0, 5 % P, 77] = 0x7F  # K of sequence 0, key 5, KV head 0, channel 77
+    pool[bt[1, 30 // P], 1, 1, 30 % P, 17] = 0xFF  # V of sequence 1, key 30, KV head 1, channel 17
+    kb, ke = np.zeros(2, np.int32), np.asarray(lens, np.int32)
+    sm = float(np.float32(1.0 / np.sqrt(128)))
+    want, wlse, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, kb, ke, True, sm)
+    assert err == 0
+    w = bf16_to_f32(want)
+    # the planted codes reach exactly the rows and channels described (causal: sequence 0's
+    # rows from position 5 on, query heads 0-3; sequence 1's rows from position 30 on,
+    # query heads 4-7, channel 17)
+    assert np.isnan(w[5:48, 0:4]).all() and not np.isnan(w[0:5]).any()
+    assert np.isnan(w[48 + 6:, 4:8, 17]).all() and not np.isnan(w[48:48 + 6]).any()
+    assert np.isnan(w).sum() == 43 * 4 * 128 + 34 * 4
+    assert np.isneginf(wlse[5:48, 0:4]).all()
+    # where the NaN V may also show: sequence 1 (positions 24 + i), heads 4-7, channel 17,
+    # rows less than 64 positions before key 30
+    leak = np.zeros(w.shape, bool)
+    leak[48:48 + 6, 4:8, 17] = True
+    vm = vmax_rows(pool, scales, bt, cu, kb, ke, Hq)
+    out, lse = run_step(q, pool, scales, bt, cu, qp, kb, ke, True, precision)
+    torch.cuda.synchronize()
+    n = assert_nan_leak_only_in_window(bits16(out), want, vm, precision, leak)
+    g = lse.cpu().numpy()
+    np.testing.assert_array_equal(np.isfinite(g), np.isfinite(wlse))
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    for single in (False, True):
+        ring = kv.ring_attention_fp8(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(ke), ring_degree=3,
+                                     causal=True, check=True, single_launch=single, precision=precision)
+        torch.cuda.synchronize()
+        n_ring = assert_nan_leak_only_in_window(bits16(ring), want, vm, precision, leak)
+        print(f"  ring 3 single_launch={single}: {n_ring} NaN in the window (step: {n})", flush=True)
 
 
 def test_prefill_flags_bad_pages():

@@ -520,7 +520,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     const float inv = lt > 0.0f ? vscale / lt : 0.0f;  // V's dequant scale applied once, here
     const int64_t row = (q_lo + r) * a.n_q_heads + hq;
     float wa = 0.0f, wb = 1.0f, lse = lse_new;
-    if ((a.mode & PF_MERGE) && !(a.mode & PF_INIT)) {
+    const bool merge_old = (a.mode & PF_MERGE) && !(a.mode & PF_INIT);
+    if (merge_old) {
       const float lse_old = a.lse2[row];
       const float mm = fmaxf(lse_old, lse_new);
       if (mm == -INFINITY) {
@@ -541,7 +542,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
       float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = o[rt][jt][i] * inv * wb;
-      if (wa != 0.0f) {
+      if (merge_old) {  // also at weight 0, so that a NaN of an earlier step stays (0 x NaN)
         const float4 old = *reinterpret_cast<const float4 *>(a.o_acc + idx);
         v[0] += wa * old.x;
         v[1] += wa * old.y;
