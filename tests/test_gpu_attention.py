@@ -41,7 +41,7 @@ def v_colmax(pool, scales, bt, lens, Hq):
         for hq in range(Hq):
             h = hq // (Hq // Hkv)
             if len(t):
-                out[b, hq] = np.nanmax(dec[pool[pages, 1, h, t % P, :]], axis=0) * float(scales[1, h])
+                out[b, hq] = np.nanmax(dec[pool[pages, 1, h, t % P, :]], axis=0) * abs(float(scales[1, h]))
     return out
 
 
@@ -107,6 +107,22 @@ def test_paged_attention_decode_large_scores_and_custom_scale(dev):
     got = kv.paged_attention_decode(q.to(dev), torch.from_numpy(pool).to(dev), torch.from_numpy(scales).to(dev),
                                     torch.from_numpy(bt).to(dev), torch.from_numpy(lens).to(dev), sm_scale=sm)
     assert_within_one_ulp(bits16(got), want, v_colmax(pool, scales, bt, lens, 32))
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 128), (8, 8, 64)])
+def test_paged_attention_decode_negative_scales(dev, Hq, Hkv, D):
+    """Scales of either sign (a static scale may be negative): K heads 0, 2, .. and V heads
+    1, 3, .. negated, so scores and values change sign per head (matrix-core kernel for
+    D = 128, VALU kernel for D = 64)."""
+    q, pool, scales, bt, lens = make_case(Hq, Hkv, D, 16, [1, 300, 2500], seed=13)
+    scales[0, 0::2] *= -1.0
+    scales[1, 1::2] *= -1.0
+    sm = 1.0 / np.sqrt(D)
+    want, werr = O.paged_attention_decode(bits16(q), pool, scales, bt, lens, sm)
+    assert werr == 0
+    got = kv.paged_attention_decode(q.to(dev), torch.from_numpy(pool).to(dev), torch.from_numpy(scales).to(dev),
+                                    torch.from_numpy(bt).to(dev), torch.from_numpy(lens).to(dev), check=True)
+    assert_within_one_ulp(bits16(got), want, v_colmax(pool, scales, bt, lens, Hq))
 
 
 @pytest.mark.parametrize("D", [64, 128])

@@ -62,7 +62,7 @@ def vmax_rows(pool, scales, bt, cu, kv_begin, kv_end, Hq):
         pages = bt[b, t // P]
         for hq in range(Hq):
             h = hq // (Hq // Hkv)
-            out[cu[b]:cu[b + 1], hq] = np.nanmax(dec[pool[pages, 1, h, t % P, :]], axis=0) * float(scales[1, h])
+            out[cu[b]:cu[b + 1], hq] = np.nanmax(dec[pool[pages, 1, h, t % P, :]], axis=0) * abs(float(scales[1, h]))
     return out
 
 
@@ -212,6 +212,40 @@ def test_ring_ranges_in_device_order(causal):
         assert err == 0
         vmax = c["vmax"]
     assert_precision(bits16(out), want, vmax)
+
+
+@pytest.mark.parametrize("precision", ["f16", "exact"])
+def test_negative_scales(precision):
+    """Scales of either sign (a static scale may be negative): with K's scale negative the
+    scores change sign and every step takes the masked softmax path (the maximum of
+    s * scale is no longer the scale times the maximum of s); V heads with a negative scale
+    flip their output.  A step, causal and not, and ring attention over 3 shards in one
+    launch and in separate launches."""
+    Hq, Hkv, P = 8, 4, 16
+    n_q, q_pos0, lens = [70, 33], [30, 0], [100, 140]
+    print(f"negative scales precision={precision}", flush=True)
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, n_q, q_pos0, lens, seed=37)
+    scales[0, 0::2] *= -1.0
+    scales[1, 1::2] *= -1.0
+    kb, ke = np.zeros(2, np.int32), np.asarray(lens, np.int32)
+    sm = float(np.float32(1.0 / np.sqrt(128)))
+    vm = vmax_rows(pool, scales, bt, cu, kb, ke, Hq)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    for causal in (True, False):
+        want, wlse, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, kb, ke, causal, sm)
+        assert err == 0
+        out, lse = run_step(q, pool, scales, bt, cu, qp, kb, ke, causal, precision)
+        torch.cuda.synchronize()
+        assert_precision(bits16(out), want, vm, precision)
+        g = lse.cpu().numpy()
+        fin = np.isfinite(wlse)
+        np.testing.assert_array_equal(np.isfinite(g), fin)
+        assert np.all(np.abs(g[fin] - wlse[fin]) <= 2e-5 * (1 + np.abs(wlse[fin])) + LSE_EXTRA[precision])
+        for single in (False, True):
+            ring = kv.ring_attention_fp8(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(ke), ring_degree=3,
+                                         causal=causal, check=True, single_launch=single, precision=precision)
+            torch.cuda.synchronize()
+            assert_precision(bits16(ring), want, vm, precision)
 
 
 def assert_nan_leak_only_in_window(got_bits, want_bits, vmax, precision, leak):
