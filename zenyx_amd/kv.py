@@ -514,7 +514,8 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
 def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor, pool_layer: torch.Tensor,
                        scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_len: torch.Tensor,
                        ring_degree: int, causal: bool = True, sm_scale: float | None = None,
-                       check: bool = False, single_launch: bool = True, precision: str = "f16") -> torch.Tensor:
+                       check: bool = False, single_launch: bool = True, precision: str = "f16",
+                       max_q_per_seq: int | None = None) -> torch.Tensor:
     """Ring attention over the FP8 pages on one GPU: the keys [0, kv_len[b]) of every
     sequence are split into ``ring_degree`` shards (the KV blocks a ring would pass
     around), shard r being ring step r.  With ``single_launch`` one launch walks the R
@@ -522,12 +523,17 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     otherwise each step is its own launch (paged_attention_prefill, the unit a ring over R
     GPUs runs) merged into a running fp32 output and log-sum-exp, the last one writing
     bf16.  Either equals attention over all keys (the exchange between devices is what
-    one GPU leaves out).  ``precision``: how P enters P.V (see PRECISIONS)."""
+    one GPU leaves out).  ``precision``: how P enters P.V (see PRECISIONS).
+    ``max_q_per_seq``: a bound on every sequence's query count, when the caller knows one
+    (otherwise it is read back from ``cu_q``, which waits for the device)."""
     _precision_flag(precision)
     if ring_degree < 1:
         raise ValueError("ring_degree must be >= 1")
     n_q, Hq, D = q.shape
-    mq = int((cu_q[1:] - cu_q[:-1]).max().item()) if cu_q.numel() > 1 else 0
+    if max_q_per_seq is None:
+        mq = int((cu_q[1:] - cu_q[:-1]).max().item()) if cu_q.numel() > 1 else 0
+    else:
+        mq = int(max_q_per_seq)
     # Shard r covers keys [kv_len * r // R, kv_len * (r + 1) // R): all bounds in one go,
     # so the loop below only launches the ring steps (rows padded to 16 bytes, the
     # alignment every pointer of the C ABI needs).

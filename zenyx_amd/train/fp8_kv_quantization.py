@@ -210,7 +210,7 @@ class QuantizedRingAttention:
             torch.tensor([m - n for n, m in zip(q_lens, lens)], dtype=torch.int32).to(dev), c.pool[layer],
             c.scales[layer].contiguous(), c._tables(seq_ids), torch.tensor(lens, dtype=torch.int32).to(dev),
             ring_degree=self.ring_degree, causal=self.causal, sm_scale=self.sm_scale, check=True,
-            precision=self.precision)
+            precision=self.precision, max_q_per_seq=max(q_lens, default=0))
         c.check_errors()  # the appends behind these pages (the check above has synchronised)
         return out
 
