@@ -301,16 +301,19 @@ paged_decode_partial_kernel(const uint16_t *__restrict__ q, AttnGeom g, const ui
 //     (n, kg) = token n, channels 32 kg ..+32, converted to bf16 exactly: the B operand
 //     of q.K^T (k = channel; any channel permutation shared with q's A operand works,
 //     since the product sums over channels);
-//   * V values go transposed into LDS (V^T[channel][token], bf16, 80-byte rows, 16-byte
-//     token chunks XOR-swizzled by channel / 32), from where each lane reads the 8
-//     consecutive tokens of one channel that the B operand of P.V needs.
+//   * V values go into LDS as bf16 token rows (288-byte rows: the four rows a 16-lane
+//     group reads fall on distinct banks) with two 16-byte stores per load, and the B
+//     operand of P.V (8 consecutive tokens of one channel per lane) comes back through
+//     gfx950's transposing LDS read, ds_read_b64_tr_b16 (2% faster than storing V^T with
+//     64 two-byte stores per lane and step).
 // P goes through LDS as fp32 into the A-operand layout and is split into bf16 hi + lo
 // (two MFMAs), which keeps the products at ~2^-17 relative error.  Scores land in the C
 // layout: lanes 0-15 hold heads 0-3 of token l % 16, so the softmax bookkeeping is a
 // 16-lane DPP reduction; the O accumulators (8 tiles of 16 channels) live in MFMA
 // results, rows = heads.
-constexpr int AM_VROW = 80;                 // bytes per channel row of V^T (64 + 16 pad)
-constexpr int AM_VBYTES = 128 * AM_VROW;    // one wave's V^T (32 tokens)
+constexpr int AM_VTROW = 288;               // bytes per token row of V (256 + 32 pad)
+constexpr int AM_VBYTES = 32 * AM_VTROW;    // one wave's V (32 tokens)
+typedef short att_i16x4 __attribute__((ext_vector_type(4)));
 constexpr int AM_PBYTES = 4 * 32 * 4;       // one wave's P (4 heads x 32 tokens fp32)
 constexpr int AM_KROW = 144;                // bytes per token row of the K staging (128 + 16 pad)
 constexpr int AM_KBYTES = 32 * AM_KROW;     // one wave's K codes (32 tokens)
@@ -462,23 +465,18 @@ paged_decode_mfma_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8
         l[j] += p;
         if (kg == 0) pl[j * 32 + T * 16 + n] = p;
       }
-    // V^T into LDS: element (channel c, token t) at c * AM_VROW + 16 ((t / 8) ^ (c / 32)) +
-    // 2 (t % 8).  Load i of tile T gave lane l token t = 16 T + 8 i + l / 8, channels
-    // c = 16 (l % 8) + 2 p, +1 (p < 8), so c / 32 = (l % 8) / 2
+    // V into LDS as token rows (AM_VTROW bytes, channels in order, bf16): load i of tile T
+    // gave lane l token t = 16 T + 8 i + l / 8, channels 16 (l % 8) ..+16: 32 bytes
 #pragma unroll
     for (int T = 0; T < 2; ++T)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         uint32_t vb[8];
         decode16_bf16(vc[T][i], vb);
-        const int t = T * 16 + 8 * i + (lane >> 3), g8 = lane & 7;
-        const int base = (((t >> 3) ^ (g8 >> 1)) << 4) + (t & 7) * 2;
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-          uint8_t *row = vt + (16 * g8 + 2 * p) * AM_VROW + base;
-          *reinterpret_cast<uint16_t *>(row) = (uint16_t)(vb[p] & 0xFFFFu);
-          *reinterpret_cast<uint16_t *>(row + AM_VROW) = (uint16_t)(vb[p] >> 16);
-        }
+        const int t = T * 16 + 8 * i + (lane >> 3);
+        uint4 *row = reinterpret_cast<uint4 *>(vt + t * AM_VTROW + 32 * (lane & 7));
+        row[0] = make_uint4(vb[0], vb[1], vb[2], vb[3]);
+        row[1] = make_uint4(vb[4], vb[5], vb[6], vb[7]);
       }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -504,9 +502,16 @@ paged_decode_mfma_kernel(const uint16_t *__restrict__ q, AttnGeom g, const uint8
     // B operand per 16-channel tile: V^T[channel 16 jt + n][tokens 8 kg ..+8]
 #pragma unroll
     for (int jt = 0; jt < 8; ++jt) {
-      const int ch = 16 * jt + n;
-      const att_u32x4 w = *reinterpret_cast<const att_u32x4 *>(vt + ch * AM_VROW + ((kg ^ (ch >> 5)) << 4));
-      const att_bf16x8 bv = __builtin_bit_cast(att_bf16x8, w);
+      // two transposing reads (ds_read_b64_tr_b16): within each 16-lane group kg, lane L
+      // reads channels 16 jt + 4 (L % 4) ..+4 of token 8 kg + L / 4 (+4), and lane n
+      // receives channel 16 jt + n of the four tokens, the B operand's k = 8 kg ..+4 (+4)
+      const uint8_t *src = vt + (8 * kg + (n >> 2)) * AM_VTROW + 2 * (16 * jt + 4 * (n & 3));
+      const att_i16x4 w0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) att_i16x4 *)(src));
+      const att_i16x4 w1 =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) att_i16x4 *)(src + 4 * AM_VTROW));
+      const att_bf16x8 bv = __builtin_bit_cast(
+          att_bf16x8, att_u32x4{__builtin_bit_cast(uint2, w0).x, __builtin_bit_cast(uint2, w0).y,
+                                __builtin_bit_cast(uint2, w1).x, __builtin_bit_cast(uint2, w1).y});
       o[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bv, o[jt], 0, 0, 0);
       o[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bv, o[jt], 0, 0, 0);
     }
