@@ -298,21 +298,33 @@ heads_quant_kernel(const uint4 *x, HeadsGeom g, const float *scales, uint4 *code
   }
 }
 
+// 8 codes -> 8 bf16 (16 bytes)
+__device__ __forceinline__ uint4 dequant8(uint2 c, float s) {
+  float a, b, cc, d, e, f, gg, h;
+  e4m3x4_decode(c.x, a, b, cc, d);
+  e4m3x4_decode(c.y, e, f, gg, h);
+  return make_uint4(pack_bf16(a * s, b * s), pack_bf16(cc * s, d * s), pack_bf16(e * s, f * s),
+                    pack_bf16(gg * s, h * s));
+}
+// Every lane loads 8 codes and stores their 16 bytes, so that each store instruction of a
+// wave writes 1 KiB of whole lines (storing 32 bytes per lane as two 16-byte halves wrote
+// every line by halves: 0.635 against 0.550 ms on 1 Gi elements); the stores are
+// nontemporal, the loads not (the codes of a recent quantisation may still be in the cache)
 __global__ void __launch_bounds__(QH_THREADS)
 heads_dequant_kernel(const uint4 *codes, HeadsGeom g, const float *scales, uint4 *y) {
+  typedef unsigned int nt_u4 __attribute__((ext_vector_type(4)));
   int64_t run_idx, chunk, slab;
   g.locate(blockIdx.x, run_idx, chunk, slab);
   const float s = scales[slab];
-  const uint4 *src = codes + run_idx * g.vec_per_run;
-  uint4 *dst = y + run_idx * g.vec_per_run * 2;
+  const uint2 *src = reinterpret_cast<const uint2 *>(codes + run_idx * g.vec_per_run);
+  nt_u4 *dst = reinterpret_cast<nt_u4 *>(y + run_idx * g.vec_per_run * 2);
+  const int64_t n_half = 2 * g.vec_per_run;
 #pragma unroll
-  for (int k = 0; k < QH_VEC_PER_THREAD; ++k) {
-    int64_t v = chunk * QH_CHUNK_VEC + k * QH_THREADS + threadIdx.x;
-    if (v < g.vec_per_run) {
-      uint4 o0, o1;
-      dequant16(src[v], s, o0, o1);
-      dst[2 * v] = o0;
-      dst[2 * v + 1] = o1;
+  for (int k = 0; k < 2 * QH_VEC_PER_THREAD; ++k) {
+    const int64_t h = chunk * 2 * QH_CHUNK_VEC + k * QH_THREADS + threadIdx.x;
+    if (h < n_half) {
+      const uint4 o = dequant8(src[h], s);
+      __builtin_nontemporal_store(nt_u4{o.x, o.y, o.z, o.w}, dst + h);
     }
   }
 }
