@@ -221,18 +221,22 @@ __global__ void __launch_bounds__(256) column_block(const char *__restrict__ x, 
 
 // ---------------------------------------------------------------- 5./6. cache reuse, chunked passes
 
-// Grid-stride read of n 16-byte vectors (4 in flight per thread), folded into a value that
-// is stored only if it matches a constant (so the loads are kept).  POL 0: default cache
+// Read of n 16-byte vectors, 4 in flight per thread, folded into a value that is stored
+// only if it matches a constant (so the loads are kept).  Each wave takes a contiguous
+// chunk of 4 x 64 vectors per round (its 4 loads are adjacent 1 KiB blocks); the grid
+// strides over chunks.  (A thread's 4 loads a grid stride apart read 15-20% slower: 5.57 /
+// 5.97 TB/s default / nontemporal against 6.40 / 7.15 on 2 GiB.)  POL 0: default cache
 // policy; POL 1: nontemporal.
 template <int POL>
 __global__ void __launch_bounds__(256) read_fold(const sc_v4u *__restrict__ x, long n, unsigned *sink) {
-  const long stride = (long)gridDim.x * 256;
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  const long round = (long)gridDim.x * 4 * 256;
   unsigned m = 0;
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += 4 * stride) {
+  for (long i = (t >> 6) * 256 + (t & 63); i < n; i += round) {
     sc_v4u v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const long k = i + u * stride;
+      const long k = i + u * 64;
       v[u] = k < n ? (POL ? __builtin_nontemporal_load(x + k) : x[k]) : sc_v4u{0, 0, 0, 0};
     }
 #pragma unroll
@@ -241,21 +245,22 @@ __global__ void __launch_bounds__(256) read_fold(const sc_v4u *__restrict__ x, l
   if (m == 0x9E3779B9u) sink[0] = m;
 }
 
-// Grid-stride read of n vectors, 8 bytes written per 16 read (nontemporal stores).
+// The same reads, 8 bytes written per 16 read (nontemporal stores).
 template <int POL>
 __global__ void __launch_bounds__(256) read_write_half(const sc_v4u *__restrict__ x, sc_v2u *__restrict__ out,
                                                        long n) {
-  const long stride = (long)gridDim.x * 256;
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += 4 * stride) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  const long round = (long)gridDim.x * 4 * 256;
+  for (long i = (t >> 6) * 256 + (t & 63); i < n; i += round) {
     sc_v4u v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const long k = i + u * stride;
+      const long k = i + u * 64;
       v[u] = k < n ? (POL ? __builtin_nontemporal_load(x + k) : x[k]) : sc_v4u{0, 0, 0, 0};
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const long k = i + u * stride;
+      const long k = i + u * 64;
       if (k < n) __builtin_nontemporal_store(sc_v2u{v[u].x ^ v[u].y, v[u].z ^ v[u].w}, out + k);
     }
   }
