@@ -27,6 +27,9 @@
 //   chunked  the two-pass design that would rely on it: 1 Gi bf16 elements (2 GiB) as
 //            chunks of C MiB, each read twice (a max pass, then a pass that writes 1 byte
 //            per element), against the same passes over the whole buffer;
+//   slabs    the same two passes over configs[4]'s layer (524,288 rows of 4 KiB) taken by
+//            groups of W-byte columns (W = 256 B is one (kv, head) slab, 128 MiB), each
+//            group read twice in a row, so that its second read can come from the cache;
 //   heads    the bytes of one single-pass per-head quantisation of 1 Gi bf16 elements
 //            (2 GiB read, 1 GiB written) as a plain stream (one 16-byte vector per thread)
 //            and as the persistent structure of the single-pass quantiser with nothing
@@ -35,7 +38,7 @@
 //            per vector) and its buffer refilled in turn; the shares fixed per workgroup
 //            (as the quantiser has them) or dealt out at run time by an atomic counter.
 //
-// Usage: stream_ceiling [plain|pages|append|columns|cache|chunked|heads|all] (default all).
+// Usage: stream_ceiling [plain|pages|append|columns|cache|chunked|slabs|heads|all] (default all).
 // Prints one line per measurement.  Every access is in bounds; nothing waits on another
 // workgroup.  Built by __graft_entry__.build() into measure/bin/stream_ceiling.
 #include <hip/hip_runtime.h>
@@ -216,6 +219,41 @@ __global__ void __launch_bounds__(256) column_block(const char *__restrict__ x, 
       const sc_v2u o = {v[u].x ^ v[u].y, v[u].z ^ v[u].w};
       __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(out + r * (W / 2)) + c);
     }
+  }
+}
+
+// Column group j of W bytes of every 4 KiB row, U rows per thread in flight: WRITE 0 reads
+// and folds (an amax pass), WRITE 1 reads and writes W / 2 bytes per row (an encode pass).
+// REV takes the row tiles from the end first.  POL 1: nontemporal loads.
+template <int U, int WRITE, int POL, int REV>
+__global__ void __launch_bounds__(256) column_pass(const char *__restrict__ x, char *__restrict__ out, long rows,
+                                                  int W, int j, unsigned *sink) {
+  const int lpr = W / 16;
+  const int rpb = 256 / lpr;
+  const long tile = REV ? (long)gridDim.x - 1 - blockIdx.x : (long)blockIdx.x;
+  const long r0 = tile * U * rpb + threadIdx.x / lpr;
+  const int c = threadIdx.x % lpr;
+  sc_v4u v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const long r = r0 + (long)u * rpb;
+    const sc_v4u *p = reinterpret_cast<const sc_v4u *>(x + r * 4096 + (long)j * W) + c;
+    v[u] = r < rows ? (POL ? __builtin_nontemporal_load(p) : *p) : sc_v4u{0, 0, 0, 0};
+  }
+  if (WRITE) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long r = r0 + (long)u * rpb;
+      if (r < rows) {
+        const sc_v2u o = {v[u].x ^ v[u].y, v[u].z ^ v[u].w};
+        __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(out + r * (W / 2)) + c);
+      }
+    }
+  } else {
+    unsigned m = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) m = max(m, max(v[u].x ^ v[u].y, v[u].z ^ v[u].w));
+    if (m == 0x9E3779B9u) sink[0] = m;
   }
 }
 
@@ -625,6 +663,60 @@ int main(int argc, char **argv) {
         printf("chunked two passes, chunks of %ld MiB (%ld launches), first pass %s loads: %.4f ms, %.1f GB/s of "
                "3 GiB algorithmic\n",
                mib, 2 * (total / c), pol ? "nontemporal" : "default", ms, 3.0 * (1L << 30) / ms / 1e6);
+        fflush(stdout);
+      }
+    }
+  }
+  if (want(sel, "slabs")) {
+    // configs[4]'s layer: 524,288 token rows of 4 KiB; a (kv, head) slab is one 256 B column
+    const long rows = 524288, total = rows * 4096;
+    unsigned *sink = counter;
+    for (int rev = 0; rev < 2; ++rev) {
+      for (int W = 256; W <= 4096; W *= 2) {
+        for (int pol = 0; pol < 2; ++pol) {
+          const int lpr = W / 16, rpb = 256 / lpr;
+          constexpr int U = 8;
+          const unsigned blocks = (unsigned)((rows + (long)U * rpb - 1) / ((long)U * rpb));
+          const float ms = best_ms(
+              [&] {
+                for (int j = 0; j < 4096 / W; ++j) {
+                  char *o = out + (long)j * rows * (W / 2);
+                  if (pol)
+                    column_pass<U, 0, 1, 0><<<blocks, 256>>>(x, o, rows, W, j, sink);
+                  else
+                    column_pass<U, 0, 0, 0><<<blocks, 256>>>(x, o, rows, W, j, sink);
+                  if (rev)
+                    column_pass<U, 1, 1, 1><<<blocks, 256>>>(x, o, rows, W, j, sink);
+                  else
+                    column_pass<U, 1, 1, 0><<<blocks, 256>>>(x, o, rows, W, j, sink);
+                }
+              },
+              4);
+          printf("slabs: two passes per group of %d B columns (%ld MiB, %d groups), first pass %s loads, second "
+                 "pass %s: %.4f ms, %.1f GB/s of 3 GiB\n",
+                 W, rows * W >> 20, 4096 / W, pol ? "nontemporal" : "default",
+                 rev ? "back to front" : "front to back", ms, 1.5 * total / ms / 1e6);
+          fflush(stdout);
+        }
+      }
+    }
+    for (int W = 256; W <= 4096; W *= 4) {  // the first pass alone
+      const int lpr = W / 16, rpb = 256 / lpr;
+      constexpr int U = 8;
+      const unsigned blocks = (unsigned)((rows + (long)U * rpb - 1) / ((long)U * rpb));
+      for (int pol = 0; pol < 2; ++pol) {
+        const float ms = best_ms(
+            [&] {
+              for (int j = 0; j < 4096 / W; ++j) {
+                if (pol)
+                  column_pass<U, 0, 1, 0><<<blocks, 256>>>(x, out, rows, W, j, sink);
+                else
+                  column_pass<U, 0, 0, 0><<<blocks, 256>>>(x, out, rows, W, j, sink);
+              }
+            },
+            4);
+        printf("slabs: read-only pass per group of %d B columns, %s loads: %.4f ms, %.1f GB/s of 2 GiB\n", W,
+               pol ? "nontemporal" : "default", ms, (double)total / ms / 1e6);
         fflush(stdout);
       }
     }

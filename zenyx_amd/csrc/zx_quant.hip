@@ -424,12 +424,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t q_rsrc(const void *base, int64
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, 0x00020000);
 }
 
-// Pass 1: per-(layer, slab) amax.  Persistent grid sweeping the rows front to back;
-// pass 2 runs back to front, so it starts on rows the memory-side cache may still hold
-// (worth about 0.5% at 524,288-token layers on MI355X).
+// Pass 1: per-(layer, slab) amax.  Persistent grid sweeping the rows front to back with
+// default-policy loads; pass 2 runs back to front, so it starts on rows the memory-side
+// cache still holds (about 5% of pass 2 at 524,288-token layers on MI355X).  Each block
+// ends with one maximum per slab: stored into part[layer][block][slab] when a partials
+// buffer is given (reduced by finalize_partials_kernel), else combined by atomicMax into
+// amax_bits, which must start at zero.  Atomics from every block onto one line serialize
+// at the memory side (about 3 ns each on MI355X), so the partials path is the fast one.
 template <int U>
 __global__ void __launch_bounds__(1024)
-kv_amax_rows_kernel(const uint16_t *x, RowGeom8 g, uint32_t *amax_bits /* [L][2H] */) {
+kv_amax_rows_kernel(const uint16_t *x, RowGeom8 g, uint32_t *amax_bits /* [L][2H] */,
+                    uint32_t *part /* [L][gridDim.x][2H] or null */) {
   const int t = threadIdx.x;
   const int c = t % g.vpr8, rs = t / g.vpr8;
   const int layer = blockIdx.y;
@@ -449,7 +454,37 @@ kv_amax_rows_kernel(const uint16_t *x, RowGeom8 g, uint32_t *amax_bits /* [L][2H
     for (int k = 0; k < U; ++k) m = absmax_acc(m, v[k]);
   }
   const uint32_t mx = group_max(fold16(m), g.lps);
-  if (c % g.lps == 0 && mx) atomicMax(&amax_bits[(int64_t)layer * g.n_slabs + c / g.lps], mx << 16);
+  if (!part) {
+    if (c % g.lps == 0 && mx) atomicMax(&amax_bits[(int64_t)layer * g.n_slabs + c / g.lps], mx << 16);
+    return;
+  }
+  // one value per slab and block: the block's rpb row groups (threads c, vpr8 + c, ...)
+  // hold the same slabs and are folded through LDS (at most 1024 threads)
+  __shared__ uint32_t red[1024];
+  red[t] = mx;
+  __syncthreads();
+  if (rs == 0 && c % g.lps == 0) {
+    uint32_t v = mx;
+    for (int k = 1; k < g.rpb; ++k) v = max(v, red[k * g.vpr8 + c]);
+    part[((int64_t)layer * gridDim.x + blockIdx.x) * g.n_slabs + c / g.lps] = v << 16;
+  }
+}
+
+// Per-(layer, slab) maximum over the gx block partials of kv_amax_rows_kernel, turned into
+// the slab's scale.  One 256-thread block per (layer, slab).
+__global__ void __launch_bounds__(256)
+finalize_partials_kernel(const uint32_t *part, int32_t gx, int32_t n_slabs, float *scales) {
+  const int64_t i = blockIdx.x;  // layer * n_slabs + slab
+  const int64_t layer = i / n_slabs, slab = i % n_slabs;
+  const uint32_t *p = part + layer * gx * (int64_t)n_slabs + slab;
+  uint32_t v = 0;
+  for (int b = threadIdx.x; b < gx; b += 256) v = max(v, p[(int64_t)b * n_slabs]);
+  v = group_max(v, 64);
+  __shared__ uint32_t red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    scales[i] = scale_from_amax_bits(max(max(red[0], red[1]), max(red[2], red[3])));
 }
 
 // 0x80 in each byte of w whose low 7 bits are all set (an e4m3 NaN code), else 0.
@@ -582,20 +617,46 @@ static RowGeom8 row_geom8(const RowGeom &g) {
   return r;
 }
 
+#ifndef KA_BPC
+#define KA_BPC 4  // amax blocks per CU (of 256 threads at 4 KiB rows)
+#endif
+
+// Blocks per layer of the amax pass: KA_BPC per CU over all layers, at most one per tile.
+static int64_t amax_grid_x(int64_t n_tok, int32_t rpb, int32_t n_layers) {
+  const int64_t tiles = ceil_div(n_tok, (int64_t)KA_U * rpb);
+  const int64_t want = std::max<int64_t>(1, ceil_div((int64_t)num_cus() * KA_BPC, n_layers));
+  return std::max<int64_t>(1, std::min(tiles, want));
+}
+
+// Bytes of the partials buffer kv_scales_impl can use: [L][blocks per layer][2H] words.
+static size_t amax_partials_bytes(int32_t n_layers, int32_t n_heads) {
+  const int64_t gx = std::max<int64_t>(1, ceil_div((int64_t)num_cus() * KA_BPC, n_layers));
+  return align256((size_t)gx * n_layers * 2 * n_heads * sizeof(uint32_t));
+}
+
+// Dynamic scales of every (layer, slab).  With `part` (amax_partials_bytes of device
+// memory) the blocks store their maxima and one reduction kernel finishes; without it they
+// combine by atomics into `scales` (cleared first).
 static int kv_scales_impl(const uint16_t *x, const RowGeom &g, int32_t n_layers, float *scales,
-                          hipStream_t st) {
-  int rc = fill_u32(reinterpret_cast<uint32_t *>(scales), (int64_t)n_layers * g.n_slabs, 0, st);
-  if (rc) return rc;
+                          uint32_t *part, hipStream_t st) {
+  const int64_t n = (int64_t)n_layers * g.n_slabs;
+  int rc;
+  if (part && g.n_tok > 0) {
+    const RowGeom8 r = row_geom8(g);
+    const unsigned gx = (unsigned)amax_grid_x(g.n_tok, r.rpb, n_layers);
+    kv_amax_rows_kernel<KA_U><<<dim3(gx, n_layers), r.vpr8 * r.rpb, 0, st>>>(x, r, nullptr, part);
+    if ((rc = check_launch("kv_amax_rows"))) return rc;
+    finalize_partials_kernel<<<(unsigned)n, 256, 0, st>>>(part, (int32_t)gx, g.n_slabs, scales);
+    return check_launch("finalize_partials");
+  }
+  if ((rc = fill_u32(reinterpret_cast<uint32_t *>(scales), n, 0, st))) return rc;
   if (g.n_tok > 0) {
     const RowGeom8 r = row_geom8(g);
-    const int64_t tiles = ceil_div(g.n_tok, (int64_t)KA_U * r.rpb);
-    const int64_t want = ceil_div((int64_t)num_cus() * 4, n_layers);  // 4 blocks per CU: 1% faster than 8
-    const unsigned gx = (unsigned)(tiles < want ? tiles : (want < 1 ? 1 : want));
+    const unsigned gx = (unsigned)amax_grid_x(g.n_tok, r.rpb, n_layers);
     kv_amax_rows_kernel<KA_U><<<dim3(gx, n_layers), r.vpr8 * r.rpb, 0, st>>>(
-        x, r, reinterpret_cast<uint32_t *>(scales));
+        x, r, reinterpret_cast<uint32_t *>(scales), nullptr);
     if ((rc = check_launch("kv_amax_rows"))) return rc;
   }
-  int64_t n = (int64_t)n_layers * g.n_slabs;
   finalize_scales_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(scales, n);
   return check_launch("finalize_scales");
 }
@@ -784,14 +845,14 @@ extern "C" int zx_kv_scales(const uint16_t *x, int64_t x_layer_stride, int32_t n
   if (rc) return rc;
   ZX_REQUIRE(n_layers == 1 || x_layer_stride >= n_tok * 2LL * n_heads * head_dim,
              "kv_scales: layer stride smaller than a layer");
-  return kv_scales_impl(x, g, n_layers, scales, as_stream(stream));
+  return kv_scales_impl(x, g, n_layers, scales, nullptr, as_stream(stream));
 }
 
 extern "C" size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32_t n_heads,
                                                      int32_t head_dim) {
   (void)head_dim;
   return align256((size_t)(n_tok > 0 ? n_tok : 0) * sizeof(int64_t)) +
-         append_fused_workspace_bytes(n_layers, n_heads);
+         std::max(append_fused_workspace_bytes(n_layers, n_heads), amax_partials_bytes(n_layers, n_heads));
 }
 
 namespace {
@@ -825,7 +886,7 @@ int kv_quant_append_impl(const uint16_t *x, int64_t x_layer_stride, int32_t n_la
   ZX_REQUIRE(!(flags & ~(ZX_APPEND_STATIC_SCALES | ZX_APPEND_TWO_PASS | ZX_APPEND_SATURATE)),
              "kv_quant_append: unknown flag bits 0x%x", (unsigned)flags);
   const bool dynamic = !(flags & ZX_APPEND_STATIC_SCALES);
-  if (n_tok == 0) return dynamic ? kv_scales_impl(x, g, n_layers, scales, st) : ZX_OK;
+  if (n_tok == 0) return dynamic ? kv_scales_impl(x, g, n_layers, scales, nullptr, st) : ZX_OK;
   int64_t *tok_off = reinterpret_cast<int64_t *>(workspace);
   kv_token_offsets_kernel<<<(unsigned)ceil_div(n_tok, 256), 256, 0, st>>>(
       cu_seqlens, start_pos, n_seqs, block_tables, max_blocks, page_size, n_pages, page_bytes, head_dim,
@@ -838,7 +899,9 @@ int kv_quant_append_impl(const uint16_t *x, int64_t x_layer_stride, int32_t n_la
     if (rc != ZX_ERR_UNSUPPORTED) return rc;
     clear_error();  // this device cannot run the single-pass kernel: two passes below
   }
-  if (dynamic && (rc = kv_scales_impl(x, g, n_layers, scales, st))) return rc;
+  // the two passes: the tail of the workspace (the single pass's region) holds the amax partials
+  uint32_t *part = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + align256((size_t)n_tok * sizeof(int64_t)));
+  if (dynamic && (rc = kv_scales_impl(x, g, n_layers, scales, part, st))) return rc;
   const RowGeom8 r = row_geom8(g);
   const int64_t tiles = ceil_div(n_tok, (int64_t)KQ_U * r.rpb);
   if (tiles >= (1LL << 31)) return fail(ZX_ERR_UNSUPPORTED, "kv_quant_append: too many rows");
