@@ -115,80 +115,92 @@ __global__ void __launch_bounds__(256) page_runs(const char *__restrict__ pool, 
 // ---------------------------------------------------------------- 3. append pattern
 
 constexpr int SC_TPB = 1024;
-constexpr int SC_CT = 64;  // tokens per chunk: 64 x 16 vectors = one 16-byte vector per lane
-constexpr int SC_K = 6;    // chunks a workgroup holds per slab
-constexpr int SC_NB = 4;   // slabs in flight per workgroup
-constexpr int SC_ROW = 4096, SC_SLAB = 256, SC_SLABS_PER_ROW = SC_ROW / SC_SLAB;
+constexpr int SC_ROW = 4096;
+// Column width W of one step (256 B: one (kv, head) slab; 512 B: two adjacent slabs taken
+// as one step), with the bytes a workgroup holds the same for both: chunks of
+// 1024 / (W / 16) tokens (one 16-byte vector per lane), K chunks per step, NB steps in flight.
+template <int W> struct ScGeom;
+template <> struct ScGeom<256> { static constexpr int K = 6, NB = 4; };
+template <> struct ScGeom<512> { static constexpr int K = 12, NB = 2; };
+constexpr int SC_CT = 64;  // tokens per chunk at W = 256
+constexpr int SC_K = ScGeom<256>::K, SC_NB = ScGeom<256>::NB;
+constexpr int SC_SLAB = 256, SC_SLABS_PER_ROW = SC_ROW / SC_SLAB;
 
 struct PatternArgs {
   const char *x;  // [L][T][4096 B]
-  char *out;      // [L * 16][T][128 B], or with `page` the pool [L][T / 16 pages][16 slabs][16][128 B]
+  char *out;      // [L * 4096 / W][T][W / 2 B], or with `page` the pool [L][T / 16 pages][16 slabs][16][128 B]
   long T;
-  int n_slabs, n_chunks, dynamic;
+  int n_slabs, n_chunks, dynamic;  // n_slabs: column steps (L * 4096 / W)
   unsigned *counter;  // [n_slabs], zero at launch (dynamic only)
   const int *page;    // null, or the page of each group of 16 tokens (a permutation): the
                       // append's destination, 2 KiB runs of one slab 32 KiB apart
 };
 
+template <int W>
 __device__ __forceinline__ sc_v4u pat_load(const PatternArgs &a, int s, int c, int tid) {
-  const long tok = (long)c * SC_CT + tid / 16;
+  constexpr int LPT = W / 16, CT = SC_TPB / LPT, SPR = SC_ROW / W;
+  const long tok = (long)c * CT + tid / LPT;
   if (c < 0 || s >= a.n_slabs || tok >= a.T) return sc_v4u{0, 0, 0, 0};
-  const int l = s / SC_SLABS_PER_ROW, j = s % SC_SLABS_PER_ROW;
+  const int l = s / SPR, j = s % SPR;
   return __builtin_nontemporal_load(
-      reinterpret_cast<const sc_v4u *>(a.x + ((long)l * a.T + tok) * SC_ROW + j * SC_SLAB + (tid % 16) * 16));
+      reinterpret_cast<const sc_v4u *>(a.x + ((long)l * a.T + tok) * SC_ROW + j * W + (tid % LPT) * 16));
 }
 
+template <int W>
 __device__ __forceinline__ void pat_store(const PatternArgs &a, int s, int c, int tid, sc_v4u v) {
-  const long tok = (long)c * SC_CT + tid / 16;
+  constexpr int LPT = W / 16, CT = SC_TPB / LPT, SPR = SC_ROW / W;
+  const long tok = (long)c * CT + tid / LPT;
   if (c < 0 || s >= a.n_slabs || tok >= a.T) return;
   const sc_v2u o = {v.x ^ v.y, v.z ^ v.w};
   long off;
   if (a.page) {
-    const int l = s / SC_SLABS_PER_ROW, j = s % SC_SLABS_PER_ROW;
+    const int l = s / SPR, jj = (s % SPR) * (W / 256) + (tid % LPT) / 16;  // the 256 B slab
     const long pages = (a.T + 15) / 16;
-    off = (((long)l * pages + a.page[tok >> 4]) * SC_SLABS_PER_ROW + j) * 2048 + (tok & 15) * 128;
+    off = (((long)l * pages + a.page[tok >> 4]) * SC_SLABS_PER_ROW + jj) * 2048 + (tok & 15) * 128 + (tid % 16) * 8;
   } else {
-    off = ((long)s * a.T + tok) * 128;
+    off = ((long)s * a.T + tok) * (W / 2) + (tid % LPT) * 8;
   }
-  __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(a.out + off + (tid % 16) * 8));
+  __builtin_nontemporal_store(o, reinterpret_cast<sc_v2u *>(a.out + off));
 }
 
+template <int W>
 __global__ void __launch_bounds__(SC_TPB) append_pattern(PatternArgs a) {
-  __shared__ int base[SC_NB];
+  constexpr int K = ScGeom<W>::K, NB = ScGeom<W>::NB;
+  __shared__ int base[NB];
   const int tid = threadIdx.x, w = blockIdx.x, G = gridDim.x;
-  sc_v4u buf[SC_NB][SC_K];
-  int cid[SC_NB][SC_K];
-  // chunk ids of slab s for buffer i (the same on every lane of the workgroup)
+  sc_v4u buf[NB][K];
+  int cid[NB][K];
+  // chunk ids of step s for buffer i (the same on every lane of the workgroup)
   auto assign = [&](int s, int i) {
     if (!a.dynamic) {
       const int c0 = (int)((long)w * a.n_chunks / G), c1 = (int)((long)(w + 1) * a.n_chunks / G);
 #pragma unroll
-      for (int k = 0; k < SC_K; ++k) cid[i][k] = c0 + k < c1 ? c0 + k : -1;
+      for (int k = 0; k < K; ++k) cid[i][k] = c0 + k < c1 ? c0 + k : -1;
     } else {
       __syncthreads();
-      if (tid == 0) base[i] = s < a.n_slabs ? (int)atomicAdd(&a.counter[s], (unsigned)SC_K) : a.n_chunks;
+      if (tid == 0) base[i] = s < a.n_slabs ? (int)atomicAdd(&a.counter[s], (unsigned)K) : a.n_chunks;
       __syncthreads();
       const int b = base[i];
 #pragma unroll
-      for (int k = 0; k < SC_K; ++k) cid[i][k] = b + k < a.n_chunks ? b + k : -1;
+      for (int k = 0; k < K; ++k) cid[i][k] = b + k < a.n_chunks ? b + k : -1;
     }
   };
 #pragma unroll
-  for (int i = 0; i < SC_NB; ++i) {
+  for (int i = 0; i < NB; ++i) {
     assign(i, i);
 #pragma unroll
-    for (int k = 0; k < SC_K; ++k) buf[i][k] = pat_load(a, i, cid[i][k], tid);
+    for (int k = 0; k < K; ++k) buf[i][k] = pat_load<W>(a, i, cid[i][k], tid);
   }
-  const int s_pad = (a.n_slabs + SC_NB - 1) / SC_NB * SC_NB;
-  for (int s0 = 0; s0 < s_pad; s0 += SC_NB) {
+  const int s_pad = (a.n_slabs + NB - 1) / NB * NB;
+  for (int s0 = 0; s0 < s_pad; s0 += NB) {
 #pragma unroll
-    for (int i = 0; i < SC_NB; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const int s = s0 + i;
 #pragma unroll
-      for (int k = 0; k < SC_K; ++k) pat_store(a, s, cid[i][k], tid, buf[i][k]);
-      assign(s + SC_NB, i);
+      for (int k = 0; k < K; ++k) pat_store<W>(a, s, cid[i][k], tid, buf[i][k]);
+      assign(s + NB, i);
 #pragma unroll
-      for (int k = 0; k < SC_K; ++k) buf[i][k] = pat_load(a, s + SC_NB, cid[i][k], tid);
+      for (int k = 0; k < K; ++k) buf[i][k] = pat_load<W>(a, s + NB, cid[i][k], tid);
     }
   }
 }
@@ -556,7 +568,7 @@ int main(int argc, char **argv) {
           const float ms = best_ms(
               [&] {
                 SC_CHECK(hipMemsetAsync(counter, 0, 4096 * sizeof(unsigned)));
-                append_pattern<<<ncu, SC_TPB>>>(a);
+                append_pattern<256><<<ncu, SC_TPB>>>(a);
               },
               5);
           printf("append pattern, %s shares, %s (256 B of each 4 KiB row per step, %d steps in flight): %.3f ms, "
@@ -565,6 +577,25 @@ int main(int argc, char **argv) {
                  (in_bytes + out_bytes) / ms / 1e6);
           fflush(stdout);
         }
+      // two adjacent slabs per step (512 B of each row), half as many steps in flight
+      const int chunks512 = (int)((T + 31) / 32);
+      if ((long)ncu * ScGeom<512>::K >= chunks512) {
+        for (int paged = 0; paged < 2; ++paged)
+          for (int dyn = 0; dyn < 2; ++dyn) {
+            PatternArgs a{x, out, T, L * (SC_ROW / 512), chunks512, dyn, counter, paged ? page_d : nullptr};
+            const float ms = best_ms(
+                [&] {
+                  SC_CHECK(hipMemsetAsync(counter, 0, 4096 * sizeof(unsigned)));
+                  append_pattern<512><<<ncu, SC_TPB>>>(a);
+                },
+                5);
+            printf("append pattern, %s shares, %s (512 B of each 4 KiB row per step, %d steps in flight): %.3f ms, "
+                   "%.1f GB/s\n",
+                   dyn ? "dynamic" : "static", paged ? "writes into random pages" : "contiguous writes",
+                   ScGeom<512>::NB, ms, (in_bytes + out_bytes) / ms / 1e6);
+            fflush(stdout);
+          }
+      }
       SC_CHECK(hipFree(page_d));
     }
   }
