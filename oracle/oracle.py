@@ -287,6 +287,18 @@ def legacy_reciprocal_check(dtype: str, scale_stride: int = 1):
     return int(bad), int(pairs.value)
 
 
+def legacy_fast_check(dtype: str, scale_stride: int = 1):
+    """(mismatching codes, pairs compared) of the GPU's fast legacy encoder (reciprocal +
+    Markstein, no range guard, integer rounding by adding 1.5 * 2^23) against the reference
+    code, over every reachable (scale, x) pair (zxo_legacy_fast_check)."""
+    L = lib()
+    L.zxo_legacy_fast_check.restype = ctypes.c_int64
+    L.zxo_legacy_fast_check.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int64)]
+    pairs = ctypes.c_int64(0)
+    bad = L.zxo_legacy_fast_check(_DT[dtype], int(scale_stride), ctypes.byref(pairs))
+    return int(bad), int(pairs.value)
+
+
 def int8_legacy_dequant(q: np.ndarray, scale: float) -> np.ndarray:
     q = np.ascontiguousarray(q, dtype=np.int8)
     y = np.empty(q.shape, np.uint16)

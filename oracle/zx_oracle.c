@@ -488,6 +488,50 @@ int64_t zxo_legacy_reciprocal_check(int dtype, int scale_stride, int64_t *pairs)
   return bad;
 }
 
+/* The GPU's fast encoder for bf16 / f16 slabs with a finite scale, where every input obeys
+ * |x| <= amax: q = x / s from r = 1 / s and one Markstein correction (no range guard),
+ * rounded to the storage dtype, clamped to +-127, then rounded to an integer by adding
+ * 1.5 * 2^23 (the low byte of the sum is the two's-complement code).  Checked against
+ * the reference code rint(dtype(x / s)) (clamped, NaN -> 0) for every finite x with |x| at
+ * most the largest amax of each scale; every scale_stride-th reachable scale.  Returns
+ * the number of differing pairs; *pairs the number compared. */
+int64_t zxo_legacy_fast_check(int dtype, int scale_stride, int64_t *pairs) {
+  int64_t bad = 0, n = 0, k = 0;
+  const float lo = to_dtype(1e-8f, dtype);
+  const uint32_t fin = dtype == 0 ? 0x7F80u : 0x7C00u; /* first non-finite magnitude */
+  uint32_t ab = 0;
+  while (ab < fin) {
+    /* the run of amax patterns [ab, ae) sharing one scale */
+    float a = dtype == 0 ? zxo_bf16_to_f32((uint16_t)ab) : zxo_f16_to_f32((uint16_t)ab);
+    const float s = to_dtype((a < lo ? lo : a) / 127.0f, dtype);
+    uint32_t ae = ab + 1;
+    while (ae < fin) {
+      float a2 = dtype == 0 ? zxo_bf16_to_f32((uint16_t)ae) : zxo_f16_to_f32((uint16_t)ae);
+      if (to_dtype((a2 < lo ? lo : a2) / 127.0f, dtype) != s) break;
+      ++ae;
+    }
+    const uint32_t top = ae - 1; /* the largest |x| pattern the run allows */
+    ab = ae;
+    const float r = 1.0f / s;
+    if (!isfinite(s) || !isfinite(r) || (k++ % scale_stride)) continue;
+    for (uint32_t mag = 0; mag <= top; ++mag)
+      for (uint32_t sg = 0; sg < 2; ++sg) {
+        const uint16_t xb = (uint16_t)(mag | (sg << 15));
+        const float x = dtype == 0 ? zxo_bf16_to_f32(xb) : zxo_f16_to_f32(xb);
+        float w = rintf(to_dtype(x / s, dtype));
+        w = isnan(w) ? 0.0f : fminf(fmaxf(w, -127.0f), 127.0f);
+        const float q0 = x * r;
+        float v = to_dtype(fmaf(fmaf(-q0, s, x), r, q0), dtype);
+        v = fminf(fmaxf(v, -127.0f), 127.0f);
+        const int8_t g = (int8_t)(f2u(v + 12582912.0f) & 0xFFu);
+        bad += (int8_t)w != g;
+        ++n;
+      }
+  }
+  if (pairs) *pairs = n;
+  return bad;
+}
+
 /* ---------------------------------------------------------------- Belady */
 
 /* belady.py:39-51 over integer slots: the largest key > -1 among resident slots, ties to

@@ -511,6 +511,16 @@ def test_legacy_reciprocal_quotient_matches_division(dt):
     assert bad == 0
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_legacy_fast_encoder_matches_division(dt):
+    """The GPU's fast legacy encoder (no range guard, integer rounding by adding 1.5 * 2^23)
+    gives the reference code for every reachable pair: every finite x with |x| at most the
+    largest amax of its scale, every 61st scale (the full set, stride 1, was run too)."""
+    bad, pairs = O.legacy_fast_check(dt, 61)
+    assert pairs > 5_000_000
+    assert bad == 0
+
+
 def test_torch_restatements_of_append_and_gather_match_c():
     """The torch CPU restatements bench.py times as the multi-threaded CPU baseline give
     the C oracle's scales, pool bytes and gathered values bit for bit."""

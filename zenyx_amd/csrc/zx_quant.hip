@@ -37,6 +37,8 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v) {
 
 // ================================================================== legacy int8
 
+typedef unsigned int nt_u4 __attribute__((ext_vector_type(4)));  // for the nontemporal builtins
+
 // Storage dtypes of the legacy path: magnitude mask and "is NaN" threshold of the raw bits.
 template <int DT> struct Dt;
 template <> struct Dt<ZX_BF16> {
@@ -146,7 +148,32 @@ __device__ __forceinline__ int8_t legacy_code(float xv, float s, float r) {
   return v != v ? (int8_t)0 : (int8_t)fminf(fmaxf(v, -127.0f), 127.0f);  // NaN -> 0, as torch CPU
 }
 
-template <int DT, bool VEC>
+// Four codes (one word) of the fast path, for bf16 / f16 slabs with a finite scale, where
+// every input obeys |x| <= amax, so every quotient is finite and below ~170: the quotient
+// as in legacy_code with no range guard, rounded to the storage dtype, clamped to +-127
+// (v_med3), then rounded to an integer by adding 1.5 * 2^23 (round half to even, as
+// rint; the low byte of the sum is the two's-complement code).  The same codes as
+// legacy_code for every reachable (scale, x) pair: checked exhaustively on the CPU
+// (zxo_legacy_fast_check).
+template <int DT>
+__device__ __forceinline__ uint32_t legacy_fast4(uint32_t u0, uint32_t u1, float s, float r) {
+  const uint32_t w[2] = {u0, u1};
+  uint32_t b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint16_t h = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+    const float x = Dt<DT>::load(&h, 0);
+    const float q0 = x * r;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0);
+    b[j] = __float_as_uint(__builtin_amdgcn_fmed3f(Dt<DT>::round(q), -127.0f, 127.0f) + 12582912.0f);
+  }
+  return __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu);
+}
+
+// NT: nontemporal loads, for inputs of 256 MiB and more (5% at 1 Gi bf16 elements); below
+// that the default policy leaves the input in the Infinity Cache for the quant pass (7% at
+// configs[0]'s 151 MB).
+template <int DT, bool VEC, bool NT>
 __global__ void legacy_amax_slabs_kernel(const void *x, int64_t slab_len, uint32_t *amax_bits) {
   using V = LegacyVec<DT>;
   const int64_t base = (int64_t)blockIdx.y * slab_len;
@@ -162,7 +189,16 @@ __global__ void legacy_amax_slabs_kernel(const void *x, int64_t slab_len, uint32
 #pragma unroll
       for (int u = 0; u < LEGACY_U; ++u) {
         const int64_t v = v0 + u * lr.step_u;
-        xw[u] = v < nv ? xv[v] : make_uint4(0u, 0u, 0u, 0u);
+        if (v < nv) {
+          if constexpr (NT) {
+            const nt_u4 t = __builtin_nontemporal_load(reinterpret_cast<const nt_u4 *>(xv) + v);
+            xw[u] = make_uint4(t.x, t.y, t.z, t.w);
+          } else {
+            xw[u] = xv[v];
+          }
+        } else {
+          xw[u] = make_uint4(0u, 0u, 0u, 0u);
+        }
       }
 #pragma unroll
       for (int u = 0; u < LEGACY_U; ++u) m = max(m, V::absmax(xw[u]));
@@ -199,11 +235,16 @@ __device__ __forceinline__ void legacy_quant_range(const void *x, int64_t base, 
         uint32_t c[V::W / 4];
 #pragma unroll
         for (int k = 0; k < V::W / 4; ++k) {
-          uint32_t w = 0;
+          if constexpr (FAST && DT != ZX_F32) {
+            const uint32_t xw4[4] = {xw[u].x, xw[u].y, xw[u].z, xw[u].w};
+            c[k] = legacy_fast4<DT>(xw4[2 * k], xw4[2 * k + 1], s, r);
+          } else {
+            uint32_t w = 0;
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            w |= (uint32_t)(uint8_t)legacy_code<DT, FAST>(V::elem(xw[u], 4 * k + j), s, r) << (8 * j);
-          c[k] = w;
+            for (int j = 0; j < 4; ++j)
+              w |= (uint32_t)(uint8_t)legacy_code<DT, FAST>(V::elem(xw[u], 4 * k + j), s, r) << (8 * j);
+            c[k] = w;
+          }
         }
         if (v < nv) {
           if constexpr (V::W == 8)
@@ -342,7 +383,6 @@ __device__ __forceinline__ uint4 dequant8(uint2 c, float s) {
 // nontemporal, the loads not (the codes of a recent quantisation may still be in the cache)
 __global__ void __launch_bounds__(QH_THREADS)
 heads_dequant_kernel(const uint4 *codes, HeadsGeom g, const float *scales, uint4 *y) {
-  typedef unsigned int nt_u4 __attribute__((ext_vector_type(4)));
   int64_t run_idx, chunk, slab;
   g.locate(blockIdx.x, run_idx, chunk, slab);
   const float s = scales[slab];
@@ -683,13 +723,17 @@ int legacy_quant_launch(const void *x, int64_t n_slabs, int64_t slab_len, int8_t
   const bool vec = (uintptr_t)x % 16 == 0 && (uintptr_t)q % V::W == 0 &&
                    (n_slabs == 1 || (slab_len * V::ES) % 16 == 0);
   const dim3 grid(legacy_blocks_per_slab(n_slabs, slab_len), (unsigned)n_slabs);
+  const bool large = (double)n_slabs * slab_len * V::ES >= (double)(256 << 20);
   int rc;
   if (vec) {
-    legacy_amax_slabs_kernel<DT, true><<<grid, 256, 0, st>>>(x, slab_len, amax);
+    if (large)
+      legacy_amax_slabs_kernel<DT, true, true><<<grid, 256, 0, st>>>(x, slab_len, amax);
+    else
+      legacy_amax_slabs_kernel<DT, true, false><<<grid, 256, 0, st>>>(x, slab_len, amax);
     if ((rc = check_launch("legacy_amax"))) return rc;
     legacy_quant_slabs_kernel<DT, true><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
   } else {
-    legacy_amax_slabs_kernel<DT, false><<<grid, 256, 0, st>>>(x, slab_len, amax);
+    legacy_amax_slabs_kernel<DT, false, false><<<grid, 256, 0, st>>>(x, slab_len, amax);
     if ((rc = check_launch("legacy_amax"))) return rc;
     legacy_quant_slabs_kernel<DT, false><<<grid, 256, 0, st>>>(x, slab_len, amax, q, scales);
   }
