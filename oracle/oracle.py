@@ -299,6 +299,17 @@ def legacy_fast_check(dtype: str, scale_stride: int = 1):
     return int(bad), int(pairs.value)
 
 
+def fp8_product_check(scale_stride: int = 1):
+    """(differing codes, pairs compared) of e4m3(x * RN(1 / s)) against e4m3(x / s) over
+    dynamic scales s = amax / 448 and |x| <= amax (zxo_fp8_product_check)."""
+    L = lib()
+    L.zxo_fp8_product_check.restype = ctypes.c_int64
+    L.zxo_fp8_product_check.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_int64)]
+    pairs = ctypes.c_int64(0)
+    bad = L.zxo_fp8_product_check(int(scale_stride), ctypes.byref(pairs))
+    return int(bad), int(pairs.value)
+
+
 def int8_legacy_dequant(q: np.ndarray, scale: float) -> np.ndarray:
     q = np.ascontiguousarray(q, dtype=np.int8)
     y = np.empty(q.shape, np.uint16)

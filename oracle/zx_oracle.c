@@ -532,6 +532,29 @@ int64_t zxo_legacy_fast_check(int dtype, int scale_stride, int64_t *pairs) {
   return bad;
 }
 
+/* Is the Markstein correction of the FP8 encoders needed with dynamic scales?  For every
+ * finite bf16 amax a > 0 (s = zxo_fp8_scale(a), r = RN(1 / s)) and every bf16 x with
+ * |x| <= a, compares the code of RN(x / s) (the reference) with the code of the plain
+ * product RN(x * r).  Every scale_stride-th amax.  Returns the differing pairs; *pairs
+ * the number compared. */
+int64_t zxo_fp8_product_check(int scale_stride, int64_t *pairs) {
+  int64_t bad = 0, n = 0, k = 0;
+  for (uint32_t ab = 1; ab < 0x7F80u; ++ab) {
+    if (k++ % scale_stride) continue;
+    const float a = zxo_bf16_to_f32((uint16_t)ab);
+    const float s = zxo_fp8_scale(a);
+    const float r = 1.0f / s;
+    for (uint32_t mag = 0; mag <= ab; ++mag)
+      for (uint32_t sg = 0; sg < 2; ++sg) {
+        const float x = zxo_bf16_to_f32((uint16_t)(mag | (sg << 15)));
+        bad += zxo_e4m3_encode(x / s) != zxo_e4m3_encode(x * r);
+        ++n;
+      }
+  }
+  if (pairs) *pairs = n;
+  return bad;
+}
+
 /* ---------------------------------------------------------------- Belady */
 
 /* belady.py:39-51 over integer slots: the largest key > -1 among resident slots, ties to

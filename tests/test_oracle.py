@@ -521,6 +521,14 @@ def test_legacy_fast_encoder_matches_division(dt):
     assert bad == 0
 
 
+def test_fp8_encoders_need_the_correction_step():
+    """Why the FP8 encoders keep the Markstein step even with dynamic scales (|x| <= amax):
+    the plain product x * RN(1 / s) gives another e4m3 code than x / s on some pairs."""
+    bad, pairs = O.fp8_product_check(101)
+    assert pairs > 10_000_000
+    assert bad > 0
+
+
 def test_torch_restatements_of_append_and_gather_match_c():
     """The torch CPU restatements bench.py times as the multi-threaded CPU baseline give
     the C oracle's scales, pool bytes and gathered values bit for bit."""
