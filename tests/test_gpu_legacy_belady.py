@@ -63,6 +63,34 @@ def test_int8_legacy_slabs_match_per_tensor_and_oracle(dev, dt, shape):
         np.testing.assert_array_equal(raw(y[i]), O.int8_legacy_dequant(wq, ws))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_int8_legacy_every_input_below_amax(dev, dt):
+    """The vector path's fast encoder (no NaN or range guard, integer rounding by adding
+    1.5 * 2^23) on complete input sets: slab i holds every bit pattern of the format whose
+    magnitude is at most the pattern a_i (both signs, so a_i is the slab's amax), zero
+    padded.  The a_i cover scales from the 1e-8 floor to the format's largest value, the
+    quotients 127 / 127.5 / 128 at the clamp, and (f16) subnormal and zero scales, whose
+    slabs take the division path.  Codes, scales and dequantised values equal the oracle's."""
+    tops = {"bf16": [0x0001, 0x2F00, 0x3280, 0x3A83, 0x3C00, 0x3F80, 0x42FE, 0x42FF, 0x4300, 0x4480, 0x4700,
+                     0x5000, 0x6A00, 0x7F7F],
+            "f16": [0x0001, 0x0010, 0x0100, 0x0300, 0x0400, 0x0C00, 0x1400, 0x2000, 0x3C00, 0x57F0, 0x57F8,
+                    0x5800, 0x7000, 0x7BFF]}[dt]
+    L = 1 << 17
+    rows = np.zeros((len(tops), L), np.uint16)
+    for i, a in enumerate(tops):
+        mags = np.arange(a + 1, dtype=np.uint16)
+        v = np.concatenate([mags, mags | np.uint16(0x8000)])
+        rows[i, :v.size] = v
+    x = torch.from_numpy(rows.view(np.int16)).view(DTYPES[dt])
+    q, sc = kv.int8_legacy_quant_slabs(x.to(dev))
+    y = kv.int8_legacy_dequant_slabs(q, sc)
+    for i in range(len(tops)):
+        wq, ws = O.int8_legacy_quant(rows[i], dt)
+        np.testing.assert_array_equal(q[i].cpu().numpy(), wq, err_msg=f"amax pattern {tops[i]:#06x}")
+        assert np.float32(sc[i].float().item()).tobytes() == np.float32(ws).tobytes()
+        np.testing.assert_array_equal(raw(y[i]), O.int8_legacy_dequant(wq, ws))
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
 def test_int8_legacy_unaligned_view(dev, dt):
     """A view starting one element in (not 16-byte aligned) takes the element-by-element
