@@ -65,6 +65,29 @@ def make_kv_cache(L, B, H, T, D, seed, outlier_heads=0):
     return x.to(torch.bfloat16)
 
 
+@pytest.mark.parametrize("mode", ["two", "single"])
+def test_fp8_heads_every_input_below_amax(dev, mode):
+    """Complete input sets through both quantiser paths: slab (o, h) holds every bf16 bit
+    pattern whose magnitude is at most the pattern a (both signs, so a is the slab's
+    amax), zero padded; a runs from below the 1e-8 scale floor to the largest finite bf16.
+    Codes, scales and dequantised values equal the oracle's."""
+    tops = [0x0001, 0x2F00, 0x3280, 0x3A83, 0x3C00, 0x3F80, 0x43E0, 0x43E8, 0x4400, 0x4700, 0x5000, 0x6A00,
+            0x7A00, 0x7F7F, 0x3E4C, 0x40A1]
+    run = 1 << 17
+    rows = np.zeros((len(tops), run), np.uint16)
+    for i, a in enumerate(tops):
+        mags = np.arange(a + 1, dtype=np.uint16)
+        v = np.concatenate([mags, mags | np.uint16(0x8000)])
+        rows[i, :v.size] = v
+    x = torch.from_numpy(rows.view(np.int16)).view(torch.bfloat16).reshape(2, 1, len(tops) // 2, run)
+    codes, scales = kv.fp8_quant_heads(x.to(dev), two_pass=mode == "two", single_pass=mode == "single", check=True)
+    wc, ws = O.fp8_quant_heads(bits16(x))
+    np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+    np.testing.assert_array_equal(codes.cpu().numpy(), wc)
+    y = kv.fp8_dequant_heads(codes, scales)
+    assert_bf16_equal(bits16(y), O.fp8_dequant_heads(wc, ws))
+
+
 @pytest.mark.parametrize("shape,seed", [((2, 1, 12, 256, 64), 0), ((3, 2, 4, 48, 128), 1),
                                         ((1, 3, 2, 16, 256), 2)])
 def test_fp8_quant_dequant_heads_bit_exact(dev, shape, seed):

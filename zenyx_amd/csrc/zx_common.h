@@ -74,11 +74,15 @@ __device__ __forceinline__ void e4m3x4_decode(uint32_t w, float &a, float &b, fl
 // Correctly rounded x / s given r = RN(1/s) (Markstein's FMA correction: with r within
 // half an ulp of 1/s and q0 within one ulp of x/s, RN(q0 + RN(x - q0*s)*r) = RN(x/s)).
 // Valid for finite normal s and finite x; quotients below 2^-126 may differ from RN(x/s)
-// in the last place, which no e4m3 code can tell apart (they all encode to +-0).
+// in the last place, which no e4m3 code can tell apart (they all encode to +-0).  The
+// residual is formed as e = RN(q0 s - x) = -RN(x - q0 s) and the result as
+// RN(q0 - e r): the same value, and for s > 0 the zero of x = +-0 keeps its sign (with
+// x - q0 s, the sum of the two opposite zeros made -0 / s come out +0; a negative s
+// reaches here through quant_scale's sign flip, which makes it positive).
 __device__ __forceinline__ float div_by_scale(float x, float s, float r) {
-  float q = x * r;
-  float e = __builtin_fmaf(-q, s, x);
-  return __builtin_fmaf(e, r, q);
+  const float q = x * r;
+  const float e = __builtin_fmaf(q, s, -x);
+  return __builtin_fmaf(-e, r, q);
 }
 
 // FP8 scale from the largest |x| bit pattern of a slab (fp32 bits; > 0x7F800000 is NaN).
@@ -100,17 +104,22 @@ __device__ __forceinline__ float scale_from_amax_bits(uint32_t bits) {
 // In those two cases the NaN codes that come out (0x7F or 0xFF: the sign of a NaN result
 // depends on the operands) are set to 0x7F by nan_codes_positive.  With a finite scale
 // the fix-up is switched off (an overflowing negative quotient keeps its 0xFF), so every
-// slab takes the same branch-free path.
+// slab takes the same branch-free path.  A finite negative scale (a static one) divides
+// -x by -s instead (the inputs' sign bits flipped as they are unpacked): the same
+// quotient, with the zeros signed as IEEE division signs them.
 struct QuantScale {
   float s, r;
   uint32_t nan_fix;  // 0x80808080 for a non-finite scale, else 0
+  uint32_t xflip;    // 0x80008000 for a finite negative scale (flips two bf16 signs), else 0
 };
 __device__ __forceinline__ QuantScale quant_scale(float sc) {
   const uint32_t b = __float_as_uint(sc) & 0x7FFFFFFFu;
+  const bool neg = sc < 0.0f && b < 0x7F800000u;
   QuantScale q;
-  q.s = b == 0x7F800000u ? 1.0f : sc;
-  q.r = b == 0x7F800000u ? 0.0f : 1.0f / sc;
+  q.s = b == 0x7F800000u ? 1.0f : (neg ? -sc : sc);
+  q.r = b == 0x7F800000u ? 0.0f : 1.0f / q.s;
   q.nan_fix = b >= 0x7F800000u ? 0x80808080u : 0u;
+  q.xflip = neg ? 0x80008000u : 0u;
   return q;
 }
 
@@ -124,6 +133,8 @@ __device__ __forceinline__ uint32_t nan_codes_positive(uint32_t c, uint32_t fix)
 
 // Four bf16 (two 32-bit words) -> four e4m3 codes.
 __device__ __forceinline__ uint32_t quant4(uint32_t u0, uint32_t u1, const QuantScale &q) {
+  u0 ^= q.xflip;
+  u1 ^= q.xflip;
   return nan_codes_positive(e4m3x4(div_by_scale(bf_lo(u0), q.s, q.r), div_by_scale(bf_hi(u0), q.s, q.r),
                                    div_by_scale(bf_lo(u1), q.s, q.r), div_by_scale(bf_hi(u1), q.s, q.r)),
                             q.nan_fix);
