@@ -186,6 +186,41 @@ def make_append_case(L, H, D, P, lens, seed, extra_pages=7, start=None):
     return x.to(torch.bfloat16), cu, bt, n_pages, sp
 
 
+@pytest.mark.parametrize("two_pass", [False, True])
+def test_kv_quant_append_every_input_below_amax(dev, two_pass):
+    """Complete input sets through the single-pass and the two-pass append: the slab of
+    (kv, head) holds every bf16 bit pattern whose magnitude is at most its pattern a (both
+    signs, so a is the slab's amax: -0 included), zero padded, over 1,024 tokens of two
+    sequences with pages in random order.  Scales and pool bytes equal the oracle's."""
+    H, D, P, T = 8, 128, 16, 1024
+    tops = [0x0001, 0x2F00, 0x3280, 0x3A83, 0x3C00, 0x3F80, 0x43E0, 0x43E8, 0x4400, 0x4700, 0x5000, 0x6A00,
+            0x7A00, 0x7F7F, 0x3E4C, 0x40A1]
+    x = np.zeros((1, T, 2, H, D), np.uint16)
+    for i, a in enumerate(tops):
+        mags = np.arange(a + 1, dtype=np.uint16)
+        v = np.zeros(T * D, np.uint16)
+        both = np.concatenate([mags, mags | np.uint16(0x8000)])
+        v[:both.size] = both
+        x[0, :, i // H, i % H, :] = v.reshape(T, D)
+    lens = [400, 624]
+    cu = torch.tensor([0, 400, 1024], dtype=torch.int32)
+    n_pages = 80
+    g = torch.Generator().manual_seed(5)
+    perm = torch.randperm(n_pages, generator=g).to(torch.int32)
+    bt = torch.full((2, 40), -1, dtype=torch.int32)
+    bt[0, :25] = perm[:25]
+    bt[1, :39] = perm[25:64]
+    pool = torch.zeros((1, n_pages, 2, H, P, D), dtype=torch.uint8)
+    wpool = pool.numpy().copy()
+    wsc, werr = O.kv_quant_append(x, cu.numpy(), None, bt.numpy(), wpool, P)
+    assert werr == 0 and sum(lens) == T
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    pool_d = pool.to(dev)
+    sc = kv.kv_quant_append(xt.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass)
+    np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
+    np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
+
+
 @pytest.mark.parametrize("H,D,P", [(8, 128, 16), (12, 64, 64), (2, 256, 5)])
 def test_kv_quant_append_bit_exact(dev, H, D, P):
     L = 3
