@@ -219,6 +219,13 @@ def test_kv_quant_append_every_input_below_amax(dev, two_pass):
     sc = kv.kv_quant_append(xt.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass)
     np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
     np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
+    # and back: every e4m3 code (-0 included) through the paged gather + dequant
+    seq_lens = torch.tensor(lens, dtype=torch.int32)
+    wk, wv, werr = O.kv_gather_dequant(wpool[0], wsc[0], bt.numpy(), seq_lens.numpy(), 640)
+    assert werr == 0
+    k, v = kv.kv_gather_dequant(pool_d[0], sc[0], bt.to(dev), seq_lens.to(dev), 640, check=True)
+    assert_bf16_equal(bits16(k), wk)
+    assert_bf16_equal(bits16(v), wv)
 
 
 @pytest.mark.parametrize("H,D,P", [(8, 128, 16), (12, 64, 64), (2, 256, 5)])
