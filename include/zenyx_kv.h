@@ -155,8 +155,9 @@ size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32
  * of its tokens) and written to `scales`; then |x / s| <= 448 (1 + 2^-23) for every
  * finite x and no code overflows (a NaN input makes its slab's scale, and so every code
  * of the slab, NaN, as torch's amax does).  Static scales (a decode step reusing the
- * prefill's scales) may be normal fp32 numbers of either sign, +-inf (treated as +inf)
- * or NaN; zero and subnormal static scales are outside the contract.  With a finite
+ * prefill's scales) may be normal fp32 numbers of either sign, +-inf (finite inputs
+ * then encode as the zero x / s signs: sign(x) XOR sign(s)) or NaN; zero and subnormal
+ * static scales are outside the contract.  With a finite
  * static scale a token larger than 464 |s| does not fit e4m3: its code is the NaN code
  * (the torch cast's result) and ZX_KERR_OVERFLOW is set in *err, or, with
  * ZX_APPEND_SATURATE, the code is +-448 (and the bit is still set).  Rows whose page id

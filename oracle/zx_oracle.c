@@ -131,7 +131,7 @@ uint8_t zxo_fp8_code(float x, float s) {
   if (isnan(s)) return 0x7F;
   if (isinf(s)) {
     if (isnan(x) || isinf(x)) return 0x7F;
-    return (uint8_t)((f2u(x) >> 24) & 0x80);
+    return (uint8_t)(((f2u(x) ^ f2u(s)) >> 24) & 0x80); /* x / +-inf: a zero signed as IEEE */
   }
   return zxo_e4m3_encode(x / s);
 }

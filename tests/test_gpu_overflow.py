@@ -81,6 +81,35 @@ def test_static_append_overflow_matches_oracle(dev, saturate, D):
                            static_scales=True, saturate=saturate, check=True)
 
 
+@pytest.mark.parametrize("saturate", [False, True])
+def test_static_append_every_input(dev, saturate):
+    """Every bf16 bit pattern (zeros of both signs, subnormals, +-inf, NaNs of both signs)
+    in each of four slabs, appended under static scales 0.75, -0.75, 2.5e-3 (most finite
+    inputs overflow) and -inf: codes and the error word equal the oracle's."""
+    H, D, P = 2, 128, 16
+    lens = [200, 312]
+    bt, n_pages = _tables(lens, P, 2, 11)
+    allbf = np.arange(65536, dtype=np.uint16).reshape(512, D)
+    x = np.empty((1, 512, 2, H, D), np.uint16)
+    for kvi in range(2):
+        for h in range(H):
+            x[0, :, kvi, h] = allbf
+    sc = torch.tensor([[[0.75, -0.75], [2.5e-3, -float("inf")]]], dtype=torch.float32)
+    cu = np.array([0, 200, 512], np.int32)
+    want = np.zeros((1, n_pages, 2, H, P, D), np.uint8)
+    _, werr = O.kv_quant_append(x, cu, None, bt, want, P, scales=sc.numpy(), saturate=saturate)
+    pool = torch.zeros(want.shape, dtype=torch.uint8, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    kv.kv_quant_append(xt.to(dev), torch.from_numpy(cu).to(dev), torch.from_numpy(bt).to(dev), pool,
+                       scales=sc.to(dev), static_scales=True, saturate=saturate, err=err)
+    assert int(err.item()) == werr
+    got = pool.cpu().numpy()
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} codes differ, e.g. (layer, page, kv, head, slot, d) {bad[:4].tolist()}: " \
+                          f"gpu {[hex(got[tuple(i)]) for i in bad[:4]]} oracle {[hex(want[tuple(i)]) for i in bad[:4]]}"
+
+
 def test_static_append_without_overflow_sets_no_bit(dev):
     L, H, D, P = 2, 8, 128, 16
     lens = [33, 64]

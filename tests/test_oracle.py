@@ -215,8 +215,9 @@ def _small_tables(rng, lens, P):
 def test_static_append_overflow_matches_torch(saturate):
     """Static scales: a finite token beyond 464 |s| gets the torch cast's NaN code and
     sets bit 8; with saturation it gets clamp(x / s, -448, 448)'s code instead.  Slabs
-    with a non-finite scale keep the plain cast either way.  Pinned by torch's division
-    and float8_e4m3fn cast (and torch.clamp for saturation)."""
+    with a non-finite scale keep the plain cast either way (a -inf scale: zeros signed
+    opposite to x).  Pinned by torch's division and float8_e4m3fn cast (and torch.clamp
+    for saturation)."""
     rng = np.random.default_rng(11)
     L, H, D, P = 2, 3, 64, 4
     lens = [3, 6, 1]
@@ -228,7 +229,7 @@ def test_static_append_overflow_matches_torch(saturate):
     x = x.to(torch.bfloat16)
     x.view(torch.int16)[0, 2, 0, 1, 3] = -63  # 0xFFC1: a NaN with the sign bit set
     sc = torch.tensor([[[0.01, -0.02, 0.5], [1.0, float("inf"), -0.004]],
-                       [[0.03, 2.0, -0.1], [0.007, 1e3, -1e-3]]], dtype=torch.float32)
+                       [[-float("inf"), 2.0, -0.1], [0.007, 1e3, -1e-3]]], dtype=torch.float32)
     xb = x.view(torch.int16).numpy().view(np.uint16)
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     pool = np.zeros((L, n_pages, 2, H, P, D), np.uint8)

@@ -96,7 +96,7 @@ __device__ __forceinline__ float scale_from_amax_bits(uint32_t bits) {
 // Encode parameters of one slab (uniform across the slab).  A finite scale s encodes
 // RN_e4m3(RN(x / s)) through div_by_scale(x, s, r = RN(1/s)).  The other cases follow
 // the torch evaluation of x / s -> e4m3fn:
-//   * s = +-inf (the slab holds an infinity and no NaN): a finite x gives a zero with
+//   * s = +inf (the slab holds an infinity and no NaN): a finite x gives a zero with
 //     the sign of x, +-inf gives inf/inf = NaN -> 0x7F.  The same arithmetic with s' = 1,
 //     r' = 0 gives exactly the signed zeros, and a NaN for +-inf;
 //   * s = NaN (the slab holds a NaN): every code is 0x7F; s' = r' = NaN make every
@@ -104,17 +104,17 @@ __device__ __forceinline__ float scale_from_amax_bits(uint32_t bits) {
 // In those two cases the NaN codes that come out (0x7F or 0xFF: the sign of a NaN result
 // depends on the operands) are set to 0x7F by nan_codes_positive.  With a finite scale
 // the fix-up is switched off (an overflowing negative quotient keeps its 0xFF), so every
-// slab takes the same branch-free path.  A finite negative scale (a static one) divides
-// -x by -s instead (the inputs' sign bits flipped as they are unpacked): the same
-// quotient, with the zeros signed as IEEE division signs them.
+// slab takes the same branch-free path.  A negative scale (a static one) divides -x by
+// -s instead (the inputs' sign bits flipped as they are unpacked): the same quotient,
+// with the zeros signed as IEEE division signs them (-inf: x / -inf = -sign(x) 0).
 struct QuantScale {
   float s, r;
   uint32_t nan_fix;  // 0x80808080 for a non-finite scale, else 0
-  uint32_t xflip;    // 0x80008000 for a finite negative scale (flips two bf16 signs), else 0
+  uint32_t xflip;    // 0x80008000 for a negative scale (flips two bf16 signs), else 0
 };
 __device__ __forceinline__ QuantScale quant_scale(float sc) {
   const uint32_t b = __float_as_uint(sc) & 0x7FFFFFFFu;
-  const bool neg = sc < 0.0f && b < 0x7F800000u;
+  const bool neg = sc < 0.0f;  // false for NaN and -0
   QuantScale q;
   q.s = b == 0x7F800000u ? 1.0f : (neg ? -sc : sc);
   q.r = b == 0x7F800000u ? 0.0f : 1.0f / q.s;
