@@ -49,6 +49,7 @@ struct PrefillArgs {
   int32_t *err;
   int64_t n_pages;
   int32_t n_q_heads, n_kv_heads, page_size, max_blocks, mode, causal, n_ranges, n_seqs;
+  int32_t n_qt;  // query tiles per sequence (the grid is n_qt x head groups x sequences)
   uint32_t p_magic;
   int32_t p_shift;
   float sm_log2e;  // sm_scale * log2 e
@@ -110,18 +111,24 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   constexpr bool EXACT = PM == PF_P_EXACT, F16 = PM == PF_P_F16;
   constexpr int D = 128;
   constexpr int QT = 32 * 4 / G;  // query rows per block
-  const int b = blockIdx.z;
+  // one-dimensional grid, query tile slowest: the last query tiles see the most keys under
+  // a causal mask, so every (head group, sequence)'s last tile is launched first, then
+  // every second-to-last, ... (globally longest first: the shortest blocks make the tail)
+  const int n_hg = a.n_q_heads / G;
+  const int64_t per_rank = (int64_t)n_hg * a.n_seqs;
+  const int64_t qt_rev = (int64_t)blockIdx.x / per_rank;
+  const int rem = (int)((int64_t)blockIdx.x - qt_rev * per_rank);
+  const int hg = rem % n_hg, b = rem / n_hg;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kg = lane >> 4;
   const int64_t q_lo = a.cu_q[b];
   const int n_qb = a.cu_q[b + 1] - a.cu_q[b];
-  // the last query tiles see the most keys under a causal mask: they are launched first
-  const int64_t row0_64 = (int64_t)(gridDim.x - 1 - blockIdx.x) * QT;
+  const int64_t row0_64 = ((int64_t)a.n_qt - 1 - qt_rev) * QT;
   if (row0_64 >= n_qb) return;
   const int row0_blk = (int)row0_64;
   const int grp = a.n_q_heads / a.n_kv_heads;
-  const int hq = blockIdx.y * G + wave % G;
+  const int hq = hg * G + wave % G;
   const int h = hq / grp;
   const int wrow0 = row0_blk + 32 * (wave / G);  // this wave's first row (in the sequence)
   const int64_t qp0 = a.q_pos0[b];
@@ -130,8 +137,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   const int64_t v_off = (int64_t)a.n_kv_heads * a.page_size * D;
   const int32_t *bt = a.bt + (int64_t)b * a.max_blocks;
   int32_t e = 0;
-  // rows past gridDim.x * QT (max_q_per_seq too small) are not computed: flag it
-  if (blockIdx.x == 0 && (int64_t)gridDim.x * QT < n_qb) e |= ZX_KERR_POS_RANGE;
+  // rows past n_qt * QT (max_q_per_seq too small) are not computed: flag it
+  if (qt_rev == 0 && (int64_t)a.n_qt * QT < n_qb) e |= ZX_KERR_POS_RANGE;
   const int kmax = a.max_blocks * a.page_size;  // < 2^31 (checked by the host)
   // keys past the block's last query position never count when causal
   const int last_row = min(row0_blk + QT, n_qb) - 1;
@@ -631,8 +638,10 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
     a.p_magic = (uint32_t)(((1ULL << (31 + shift)) + page_size - 1) / page_size);
   }
   const int QT = 32 * 4 / G;
-  const dim3 grid((unsigned)ceil_div(max_q_per_seq, QT), (unsigned)(n_q_heads / G), (unsigned)n_seqs);
-  ZX_REQUIRE(grid.x < (1u << 31) && n_seqs <= 65535, "paged_attention_prefill: too many query tiles or sequences");
+  a.n_qt = (int32_t)ceil_div(max_q_per_seq, QT);
+  const int64_t n_blocks = (int64_t)a.n_qt * (n_q_heads / G) * n_seqs;
+  ZX_REQUIRE(n_blocks < (1LL << 31), "paged_attention_prefill: too many query tiles or sequences");
+  const dim3 grid((unsigned)n_blocks);
   hipStream_t st = as_stream(stream);
   const int pm = (flags & ZX_PREFILL_EXACT_P) ? PF_P_EXACT : ((flags & ZX_PREFILL_FAST_P) ? PF_P_BF16 : PF_P_F16);
   switch (G * 4 + pm) {
