@@ -641,12 +641,15 @@ paged_decode_combine_kernel(const float *__restrict__ part, AttnGeom g, const fl
 using namespace zx;
 
 // Positions per block: a multiple of ATT_SPLIT_MIN, as long as the grid still has about
-// two blocks per CU (long sequences in small batches get more, shorter splits).
+// eight blocks per CU, four per resident slot (long sequences in small batches get more,
+// shorter splits).  With one block per slot (configs[2]: 64 sequences x 8 head groups =
+// 512 blocks of 32k positions) the launch ends with the slowest CU; four per slot let the
+// dispatcher even that out (1% on configs[2]; eight per slot costs more in partials).
 static void att_splits(int32_t n_seqs, int32_t head_groups, int32_t max_blocks, int32_t page_size,
                        int64_t &n_splits, int64_t &split_len) {
   const int64_t max_len = (int64_t)max_blocks * page_size;
   const int64_t most = ceil_div(max_len, ATT_SPLIT_MIN);
-  int64_t want = ceil_div(2LL * num_cus(), (int64_t)n_seqs * head_groups);
+  int64_t want = ceil_div(8LL * num_cus(), (int64_t)n_seqs * head_groups);
   want = want < 1 ? 1 : (want > most ? most : want);
   split_len = ceil_div(ceil_div(max_len, want), ATT_SPLIT_MIN) * ATT_SPLIT_MIN;
   n_splits = ceil_div(max_len, split_len);
