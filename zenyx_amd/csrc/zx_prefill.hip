@@ -434,8 +434,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     uint32_t nv0[8], nv1[8];  // the next step's V, decoded by store piece 2
     // A operand per 16-channel tile and k-block: V^T[channel 16 jt + n][k 8 kg ..+8],
     // read PVD tiles ahead of its products (the scheduling barrier keeps the compiler
-    // from sinking the reads next to their use: 2% on the ring workload)
-    constexpr int PVD = 2;
+    // from sinking the reads next to their use: 2% on the ring workload; one tile ahead
+    // measured 2% faster than two once the blocks were launched longest first)
+    constexpr int PVD = 1;
     att_u32x4 avr[PVD + 1][2];
     auto ld_av = [&](int jt, att_u32x4 (&dst)[2]) {
       const int ch = 16 * jt + n;
