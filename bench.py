@@ -308,18 +308,21 @@ def belady_leg(torch, dev, skip_cpu):
     return out
 
 
-def dropin_belady_leg(torch, dev, capacity, n_positions, seconds=2.0):
+def dropin_belady_leg(torch, dev, capacity, n_positions, seconds=1.5, distinct=2_000_000):
     """The drop-in BeladyApproxCache (belady.py:14-55's interface) at configs[3]'s resident
     set: ``capacity`` ids resident with random next uses, then a stream of new ids, each an
     update_future + touch that misses and evicts the farthest next use.  Evictions per
     second over ~``seconds`` (host bookkeeping, the slot-update and argmax kernels and one
-    stream synchronisation per eviction)."""
+    stream synchronisation per eviction), measured twice: right after the fill, and again
+    once ``distinct`` ids in all have been given a next use (update_future only: the
+    reference's next_use dictionary keeps every id it was told about), so the second rate
+    shows whether the cost per eviction grows with the ids the cache has seen."""
     import numpy as np
 
     from zenyx_amd.streaming import BeladyApproxCache
 
     rng = np.random.default_rng(0)
-    keys = rng.integers(0, n_positions, capacity + 200_000)
+    keys = rng.integers(0, n_positions, distinct + 400_000)
     cache = BeladyApproxCache(capacity, device=dev)
     for i in range(capacity):
         cache.update_future(i, int(keys[i]))
@@ -329,18 +332,33 @@ def dropin_belady_leg(torch, dev, capacity, n_positions, seconds=2.0):
         cache.update_future(nxt, int(keys[nxt]))
         cache.touch(nxt)
         nxt += 1
-    t0 = time.perf_counter()
-    k = 0
-    while k % 64 or time.perf_counter() - t0 < seconds:
+
+    def window():
+        nonlocal nxt
+        t0 = time.perf_counter()
+        k = 0
+        while k % 64 or time.perf_counter() - t0 < seconds:
+            cache.update_future(nxt, int(keys[nxt]))
+            assert len(cache.touch(nxt)) == 1
+            nxt += 1
+            k += 1
+        return k, time.perf_counter() - t0
+
+    k1, dt1 = window()
+    seen1 = nxt
+    while nxt < distinct:  # ids told about but never touched
         cache.update_future(nxt, int(keys[nxt]))
-        assert len(cache.touch(nxt)) == 1
         nxt += 1
-        k += 1
-    dt = time.perf_counter() - t0
-    log(f"drop-in BeladyApproxCache at {capacity} resident ids: {k / dt:.0f} evictions/s")
+    k2, dt2 = window()
+    log(f"drop-in BeladyApproxCache at {capacity} resident ids: {k1 / dt1:.0f} evictions/s with {seen1} ids seen, "
+        f"{k2 / dt2:.0f} with {nxt} ids seen")
     return {"workload": f"BeladyApproxCache(capacity={capacity}): {capacity} resident ids with random next uses, "
-                        "then update_future + touch of new ids, each evicting one",
-            "evictions": k, "seconds": round(dt, 3), "evictions_per_s": round(k / dt, 1)}
+                        "then update_future + touch of new ids, each evicting one; timed again after "
+                        f"{distinct} distinct ids have been given a next use",
+            "evictions": k1, "seconds": round(dt1, 3), "evictions_per_s": round(k1 / dt1, 1),
+            "ids_seen": seen1,
+            "after_growth": {"ids_seen": nxt, "evictions": k2, "seconds": round(dt2, 3),
+                             "evictions_per_s": round(k2 / dt2, 1)}}
 
 
 def curriculum_leg(torch, dev, skip_cpu):

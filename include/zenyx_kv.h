@@ -61,6 +61,16 @@ const char *zx_last_error(void);
 /* ABI version of the library (bumped on any change of a signature or of a default). */
 int zx_abi_version(void);
 
+/* Bound, in microseconds, of one wait without progress inside the cooperative
+ * single-pass kernels (zx_kv_quant_append's and zx_fp8_quant_heads' single pass, whose
+ * workgroups exchange slab maxima).  When a wait runs out the kernel raises a global
+ * abort flag, every wave exits, ZX_KERR_SPIN is ORed into the call's error word and
+ * the outputs of that call are undefined.  Default 2,000,000 (2 s); a negative value
+ * restores it; 0 makes the first wait without progress give up, which exercises the
+ * release path.  Applies to launches issued after the call, process-wide.  No
+ * counterpart in the reference (its Phase-8 code is absent); for tests and operators. */
+int zx_set_wait_bound_us(int64_t us);
+
 /* ---------------------------------------------------------------------------
  * Legacy per-tensor int8 storage.  Replaces zenyx/streaming/precision.py:8-12.
  *   s = max(amax(|x|), 1e-8) / 127, every step rounded to x's dtype as torch does
@@ -220,22 +230,28 @@ int zx_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, const uint8_
                               void *workspace, size_t workspace_bytes, zx_stream_t stream);
 
 /* ---------------------------------------------------------------------------
- * Belady victim selection.  Replaces zenyx/streaming/belady.py:39-51: among slots
- * with resident[i] != 0, pick the largest keys[i] that is > -1; ties go to the
- * smallest slot index.  out (device int64[2]) receives {slot, key}, or {-1, -1}
- * when no slot qualifies.  workspace: >= zx_belady_argmax_workspace_bytes(n_slots).
+ * Belady victim selection.  Replaces zenyx/streaming/belady.py:39-51: among the
+ * candidate slots (resident[i] != 0; every slot when resident is NULL), pick the
+ * largest keys[i] that is > -1; ties go to the smallest rank[i] (when rank is given:
+ * the drop-in cache passes each resident id's registration order there, since its
+ * slots are reused), then to the smallest slot index.  out (device int64[2]) receives
+ * {slot, key}, or {-1, -1} when no slot qualifies.
+ * workspace: >= zx_belady_argmax_workspace_bytes(n_slots).
  */
 size_t zx_belady_argmax_workspace_bytes(int64_t n_slots);
-int zx_belady_argmax(const int64_t *keys, const uint8_t *resident, int64_t n_slots, int64_t *out,
-                     void *workspace, size_t workspace_bytes, zx_stream_t stream);
+int zx_belady_argmax(const int64_t *keys, const uint8_t *resident, const int64_t *rank, int64_t n_slots,
+                     int64_t *out, void *workspace, size_t workspace_bytes, zx_stream_t stream);
 
 /* Slot updates of the drop-in cache's device tables (BeladyApproxCache.update_future and
- * .touch, belady.py:22-37): for i < n, keys[slot[i]] = key[i] and resident[slot[i]] = res[i];
- * each slot at most once per call.  slot / key / res may live in pinned host memory (the
- * kernel reads them directly) and must stay valid until the update has run.  A slot
- * outside [0, n_slots) is skipped and sets ZX_KERR_PAGE_RANGE in *err (may be NULL). */
-int zx_belady_update_slots(int64_t *keys, uint8_t *resident, int64_t n_slots, const int64_t *slot,
-                           const int64_t *key, const uint8_t *res, int64_t n, int32_t *err, zx_stream_t stream);
+ * .touch, belady.py:22-37): for i < n, keys[slot[i]] = key[i], and resident[slot[i]] =
+ * res[i] and rank[slot[i]] = rank_in[i] for the tables given (resident with res, rank
+ * with rank_in; either pair may be NULL); each slot at most once per call.  slot / key /
+ * res / rank_in may live in pinned host memory (the kernel reads them directly) and must
+ * stay valid until the update has run.  A slot outside [0, n_slots) is skipped and sets
+ * ZX_KERR_PAGE_RANGE in *err (may be NULL). */
+int zx_belady_update_slots(int64_t *keys, uint8_t *resident, int64_t *rank, int64_t n_slots,
+                           const int64_t *slot, const int64_t *key, const uint8_t *res,
+                           const int64_t *rank_in, int64_t n, int32_t *err, zx_stream_t stream);
 
 /* Next/previous use of every trace position: next_use[i] = smallest j > i with
  * trace[j] == trace[i], else ZX_NEVER; prev_use[i] = largest j < i, else -1.

@@ -52,7 +52,7 @@ def lib() -> ctypes.CDLL:
             "zxo_kv_gather_dequant": (i32, [P, i64, i32, i32, i32, P, P, i32, P, i32, i32, P, P]),
             "zxo_int8_legacy_quant": (f32, [P, ctypes.c_int, i64, P]),
             "zxo_int8_legacy_dequant": (None, [P, f32, i64, P]),
-            "zxo_belady_argmax": (None, [P, P, i64, P]),
+            "zxo_belady_argmax": (None, [P, P, P, i64, P]),
             "zxo_next_use": (None, [P, i64, i32, P, P]),
             "zxo_belady_simulate": (i64, [P, i64, i32, i64, P, P, i64, P, P]),
             "zxo_belady_tiers": (i64, [P, i64, i32, i64, i64, P, P, P]),
@@ -319,11 +319,14 @@ def int8_legacy_dequant(q: np.ndarray, scale: float) -> np.ndarray:
 
 # ------------------------------------------------------------------ Belady
 
-def belady_argmax(keys: np.ndarray, resident: np.ndarray):
+def belady_argmax(keys: np.ndarray, resident: np.ndarray | None, rank: np.ndarray | None = None):
     keys = np.ascontiguousarray(keys, dtype=np.int64)
-    resident = np.ascontiguousarray(resident, dtype=np.uint8)
+    if resident is not None:
+        resident = np.ascontiguousarray(resident, dtype=np.uint8)
+    if rank is not None:
+        rank = np.ascontiguousarray(rank, dtype=np.int64)
     out = np.empty(2, np.int64)
-    lib().zxo_belady_argmax(_p(keys), _p(resident), keys.size, _p(out))
+    lib().zxo_belady_argmax(_p(keys), _p(resident), _p(rank), keys.size, _p(out))
     return int(out[0]), int(out[1])
 
 

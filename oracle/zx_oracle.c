@@ -560,10 +560,20 @@ int64_t zxo_fp8_product_check(int scale_stride, int64_t *pairs) {
 /* belady.py:39-51 over integer slots: the largest key > -1 among resident slots, ties to
  * the smallest slot (the reference breaks ties by set iteration order, which Python does
  * not fix).  out = {slot, key} or {-1, -1}. */
-void zxo_belady_argmax(const int64_t *keys, const uint8_t *resident, int64_t n, int64_t *out) {
-  int64_t best = -1, bestk = -1;
-  for (int64_t i = 0; i < n; ++i)
-    if (resident[i] && keys[i] > bestk) { bestk = keys[i]; best = i; }
+/* belady.py:44-50 over slots: the largest key > -1 among candidates (resident[i] != 0, or
+ * every slot when resident is NULL); ties to the smallest rank (the slot index when rank
+ * is NULL), then the smallest slot. */
+void zxo_belady_argmax(const int64_t *keys, const uint8_t *resident, const int64_t *rank, int64_t n, int64_t *out) {
+  int64_t best = -1, bestk = -1, bestr = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    if (resident && !resident[i]) continue;
+    const int64_t r = rank ? rank[i] : i;
+    if (keys[i] > bestk || (best >= 0 && keys[i] == bestk && r < bestr)) {
+      bestk = keys[i];
+      bestr = r;
+      best = i;
+    }
+  }
   out[0] = best;
   out[1] = best < 0 ? -1 : bestk;
 }

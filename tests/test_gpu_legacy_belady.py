@@ -127,6 +127,9 @@ def test_belady_argmax_matches_oracle(dev):
         res = (rng.random(n) < 0.6).astype(np.uint8)
         out = kv.belady_argmax(torch.from_numpy(keys).to(dev), torch.from_numpy(res).to(dev)).cpu().tolist()
         assert tuple(out) == O.belady_argmax(keys, res)
+        rank = rng.permutation(n).astype(np.int64) // 3  # ranks with ties
+        out = kv.belady_argmax(torch.from_numpy(keys).to(dev), None, torch.from_numpy(rank).to(dev)).cpu().tolist()
+        assert tuple(out) == O.belady_argmax(keys, None, rank)
     # nothing qualifies: every resident key <= -1 (belady.py:45-51 returns None)
     keys = np.full(10, -1, np.int64)
     out = kv.belady_argmax(torch.from_numpy(keys).to(dev), torch.ones(10, dtype=torch.uint8, device=dev))

@@ -357,19 +357,25 @@ def test_belady_heap_matches_linear_scan_larger(seed):
 
 def test_belady_argmax_matches_lexsort():
     """belady.py:44-50 semantics (largest key > -1 among residents; ties to the smallest
-    slot) against numpy's lexsort on random inputs with many ties and negative keys."""
+    rank, then the smallest slot) against numpy's lexsort on random inputs with many ties
+    and negative keys; without ranks the slot index is the rank, without a residency
+    array every slot is a candidate."""
     rng = np.random.default_rng(11)
     for n in (1, 5, 64, 1000):
         for _ in range(20):
             keys = rng.integers(-3, 6, n).astype(np.int64)
             res = (rng.random(n) < 0.5).astype(np.uint8)
-            ok = np.nonzero((res == 1) & (keys > -1))[0]
-            if ok.size == 0:
-                want = (-1, -1)
-            else:
-                order = np.lexsort((ok, -keys[ok]))  # key descending, then slot ascending
-                want = (int(ok[order[0]]), int(keys[ok[order[0]]]))
-            assert O.belady_argmax(keys, res) == want
+            rank = rng.integers(0, max(2, n // 3), n).astype(np.int64)  # ties in rank too
+            for r_arg, use_res in ((None, True), (rank, True), (rank, False)):
+                cand = (res == 1) if use_res else np.ones(n, bool)
+                ok = np.nonzero(cand & (keys > -1))[0]
+                r = ok if r_arg is None else r_arg[ok]
+                if ok.size == 0:
+                    want = (-1, -1)
+                else:
+                    order = np.lexsort((ok, r, -keys[ok]))  # key descending, rank, slot ascending
+                    want = (int(ok[order[0]]), int(keys[ok[order[0]]]))
+                assert O.belady_argmax(keys, res if use_res else None, r_arg) == want
 
 
 def test_next_use_matches_dictionary_scan():

@@ -5,6 +5,7 @@ device is present, every operation raises instead of falling back to anything el
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
 import threading
@@ -29,7 +30,7 @@ ZX_PREFILL_MERGE, ZX_PREFILL_INIT, ZX_PREFILL_BF16, ZX_PREFILL_FAST_P, ZX_PREFIL
 ZX_HEADS_TWO_PASS = 1
 ZX_HEADS_SINGLE_PASS = 2
 ZX_NEVER = 0x7FFFFFFF
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P = ctypes.c_void_p
 _I64, _I32, _SZ, _INT = ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t, ctypes.c_int
@@ -38,6 +39,7 @@ _I64, _I32, _SZ, _INT = ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t, ctypes.
 SIGNATURES = {
     "zx_last_error": (ctypes.c_char_p, []),
     "zx_abi_version": (_INT, []),
+    "zx_set_wait_bound_us": (_INT, [_I64]),
     "zx_int8_legacy_quant": (_INT, [_P, _INT, _I64, _P, _P, _P, _SZ, _P]),
     "zx_int8_legacy_dequant": (_INT, [_P, _P, _INT, _I64, _P, _P]),
     "zx_int8_legacy_quant_slabs_workspace_bytes": (_SZ, [_I64]),
@@ -56,8 +58,8 @@ SIGNATURES = {
     "zx_kv_gather_dequant": (_INT, [_P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _P,
                                     _P, _P, _P]),
     "zx_belady_argmax_workspace_bytes": (_SZ, [_I64]),
-    "zx_belady_argmax": (_INT, [_P, _P, _I64, _P, _P, _SZ, _P]),
-    "zx_belady_update_slots": (_INT, [_P, _P, _I64, _P, _P, _P, _I64, _P, _P]),
+    "zx_belady_argmax": (_INT, [_P, _P, _P, _I64, _P, _P, _SZ, _P]),
+    "zx_belady_update_slots": (_INT, [_P, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P]),
     "zx_belady_next_use_workspace_bytes": (_SZ, [_I64, _I32]),
     "zx_belady_next_use": (_INT, [_P, _I64, _I32, _P, _P, _P, _P, _SZ, _P]),
     "zx_belady_simulate_workspace_bytes": (_SZ, [_I64, _I32]),
@@ -103,6 +105,9 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = args
             if lib.zx_abi_version() != ABI_VERSION:
                 raise RuntimeError(f"{LIB_PATH} has ABI {lib.zx_abi_version()}, expected {ABI_VERSION}")
+            from ._streams import teardown
+
+            atexit.register(teardown)
             _lib = lib
     return _lib
 

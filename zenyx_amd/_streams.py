@@ -39,3 +39,22 @@ def copy_stream(device: torch.device | int | str | None = None, direction: str =
 
 def all_copy_streams() -> list:
     return list(_pool.values())
+
+
+def teardown() -> None:
+    """Finish the library's device work before the interpreter shuts down: wait for the
+    copy streams and the devices they belong to (and the current one), then drop the host tensors and
+    events kept for copies in flight (they would otherwise be destroyed during
+    finalisation, after the HIP runtime may have begun its own teardown).  Registered
+    with atexit when the library is first loaded; safe to call more than once."""
+    if not torch.cuda.is_initialized():
+        return
+    used = {torch.cuda.current_device()} | {idx for idx, _ in _pool}
+    for s in all_copy_streams():
+        s.synchronize()
+    for idx in sorted(used):
+        with torch.cuda.device(idx):
+            torch.cuda.synchronize()
+    from .streaming.kv_tiering import _HostKeepAlive
+
+    _HostKeepAlive.release_all()

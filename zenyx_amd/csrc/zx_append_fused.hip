@@ -434,7 +434,7 @@ int append_fused(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, in
   a.abort_flag = reinterpret_cast<uint32_t *>(w);
   a.slots = reinterpret_cast<uint32_t *>(w + 256);
   a.err = err;
-  a.spin_ticks = 200000000ull;  // 2 s without progress, at 100 MHz
+  a.spin_ticks = wait_bound_ticks();  // default 2 s without progress (zx_set_wait_bound_us)
   // the abort flag and every slot start at zero: one fill kernel (not a memset, so the
   // sequence stays valid inside a captured graph) over the header and the slots
   if ((rc = fill_u32(a.abort_flag, (256 + S * G * 4) / 4, 0, st))) return rc;

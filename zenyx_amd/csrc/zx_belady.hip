@@ -7,82 +7,77 @@ namespace zx {
 // ------------------------------------------------------------------ argmax
 
 struct Best {
-  int64_t key, slot;
+  int64_t key, rank, slot;
 };
 
-// a beats b: larger key, ties to the smaller slot; {-1, -1} is "none".
-__device__ __forceinline__ bool beats(int64_t ka, int64_t sa, int64_t kb, int64_t sb) {
-  if (sa < 0) return false;
-  if (sb < 0) return true;
-  return ka > kb || (ka == kb && sa < sb);
+// a beats b: larger key, ties to the smaller rank, then the smaller slot; slot -1 is
+// "none".
+__device__ __forceinline__ bool beats(const Best &a, const Best &b) {
+  if (a.slot < 0) return false;
+  if (b.slot < 0) return true;
+  if (a.key != b.key) return a.key > b.key;
+  if (a.rank != b.rank) return a.rank < b.rank;
+  return a.slot < b.slot;
 }
 
-__device__ __forceinline__ void wave_best(int64_t &k, int64_t &s) {
+__device__ __forceinline__ Best shfl_best(const Best &b, int off) {
+  return Best{__shfl_xor(b.key, off, 64), __shfl_xor(b.rank, off, 64), __shfl_xor(b.slot, off, 64)};
+}
+
+__device__ __forceinline__ void wave_best(Best &b) {
   for (int off = 32; off >= 1; off >>= 1) {
-    int64_t k2 = __shfl_xor(k, off, 64);
-    int64_t s2 = __shfl_xor(s, off, 64);
-    if (beats(k2, s2, k, s)) {
-      k = k2;
-      s = s2;
-    }
+    const Best o = shfl_best(b, off);
+    if (beats(o, b)) b = o;
   }
 }
 
 constexpr int AM_THREADS = 256;
 constexpr int AM_MAX_BLOCKS = 1024;
 
-__device__ __forceinline__ void block_best(int64_t &k, int64_t &s) {
-  __shared__ int64_t kk[AM_THREADS / 64], ss[AM_THREADS / 64];
-  wave_best(k, s);
+__device__ __forceinline__ void block_best(Best &b) {
+  __shared__ Best sb[AM_THREADS / 64];
+  wave_best(b);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  if (lane == 0) {
-    kk[wid] = k;
-    ss[wid] = s;
-  }
+  if (lane == 0) sb[wid] = b;
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x == 0)
     for (int w = 1; w < AM_THREADS / 64; ++w)
-      if (beats(kk[w], ss[w], k, s)) {
-        k = kk[w];
-        s = ss[w];
-      }
-  }
+      if (beats(sb[w], b)) b = sb[w];
 }
 
+// resident == nullptr: every slot is a candidate; rank == nullptr: a slot's rank is its
+// index (ties to the smaller slot).
 __global__ void __launch_bounds__(AM_THREADS)
-argmax_partial_kernel(const int64_t *keys, const uint8_t *resident, int64_t n, Best *part) {
-  int64_t bk = -1, bs = -1;
+argmax_partial_kernel(const int64_t *keys, const uint8_t *resident, const int64_t *rank, int64_t n, Best *part) {
+  Best best{-1, 0, -1};
   for (int64_t i = (int64_t)blockIdx.x * AM_THREADS + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * AM_THREADS) {
     // belady.py:48-50: a slot qualifies when its key is strictly greater than -1
-    if (resident[i] && keys[i] > -1 && beats(keys[i], i, bk, bs)) {
-      bk = keys[i];
-      bs = i;
-    }
+    const Best c{keys[i], rank ? rank[i] : i, i};
+    if ((!resident || resident[i]) && c.key > -1 && beats(c, best)) best = c;
   }
-  block_best(bk, bs);
-  if (threadIdx.x == 0) part[blockIdx.x] = Best{bk, bs};
+  block_best(best);
+  if (threadIdx.x == 0) part[blockIdx.x] = best;
 }
 
 __global__ void __launch_bounds__(AM_THREADS)
 argmax_final_kernel(const Best *part, int n_part, int64_t *out) {
-  int64_t bk = -1, bs = -1;
+  Best best{-1, 0, -1};
   for (int i = threadIdx.x; i < n_part; i += AM_THREADS)
-    if (beats(part[i].key, part[i].slot, bk, bs)) {
-      bk = part[i].key;
-      bs = part[i].slot;
-    }
-  block_best(bk, bs);
+    if (beats(part[i], best)) best = part[i];
+  block_best(best);
   if (threadIdx.x == 0) {
-    out[0] = bs;
-    out[1] = bs < 0 ? -1 : bk;
+    out[0] = best.slot;
+    out[1] = best.slot < 0 ? -1 : best.key;
   }
 }
 
-// Slot updates of the drop-in cache: keys[slot[i]] = key[i], resident[slot[i]] = res[i]
-// (the host passes each slot once).  The update arrays may live in pinned host memory.
-__global__ void update_slots_kernel(int64_t *keys, uint8_t *resident, int64_t n_slots, const int64_t *slot,
-                                    const int64_t *key, const uint8_t *res, int64_t n, int32_t *err) {
+// Slot updates of the drop-in cache: keys[slot[i]] = key[i], and resident[slot[i]] =
+// res[i] / rank[slot[i]] = rank_in[i] when those tables are given (the host passes each
+// slot once).  The update arrays may live in pinned host memory.
+__global__ void update_slots_kernel(int64_t *keys, uint8_t *resident, int64_t *rank, int64_t n_slots,
+                                    const int64_t *slot, const int64_t *key, const uint8_t *res,
+                                    const int64_t *rank_in, int64_t n, int32_t *err) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int64_t s = slot[i];
@@ -91,7 +86,8 @@ __global__ void update_slots_kernel(int64_t *keys, uint8_t *resident, int64_t n_
     return;
   }
   keys[s] = key[i];
-  resident[s] = res[i];
+  if (resident) resident[s] = res[i];
+  if (rank) rank[s] = rank_in[i];
 }
 
 static int argmax_blocks(int64_t n) {
@@ -337,32 +333,34 @@ extern "C" size_t zx_belady_argmax_workspace_bytes(int64_t n_slots) {
   return (size_t)argmax_blocks(n_slots > 0 ? n_slots : 1) * sizeof(Best);
 }
 
-extern "C" int zx_belady_argmax(const int64_t *keys, const uint8_t *resident, int64_t n_slots, int64_t *out,
-                                void *workspace, size_t workspace_bytes, zx_stream_t stream) {
+extern "C" int zx_belady_argmax(const int64_t *keys, const uint8_t *resident, const int64_t *rank, int64_t n_slots,
+                                int64_t *out, void *workspace, size_t workspace_bytes, zx_stream_t stream) {
   clear_error();
-  ZX_REQUIRE(out && (n_slots == 0 || (keys && resident)), "belady_argmax: null pointer");
+  ZX_REQUIRE(out && (n_slots == 0 || keys), "belady_argmax: null pointer");
   ZX_REQUIRE(n_slots >= 0, "belady_argmax: negative size");
   const int nb = argmax_blocks(n_slots > 0 ? n_slots : 1);
   if (!workspace || workspace_bytes < (size_t)nb * sizeof(Best))
     return fail(ZX_ERR_WORKSPACE, "belady_argmax: workspace too small");
   hipStream_t st = as_stream(stream);
   Best *part = reinterpret_cast<Best *>(workspace);
-  argmax_partial_kernel<<<nb, AM_THREADS, 0, st>>>(keys, resident, n_slots, part);
+  argmax_partial_kernel<<<nb, AM_THREADS, 0, st>>>(keys, resident, rank, n_slots, part);
   int rc = check_launch("belady_argmax_partial");
   if (rc) return rc;
   argmax_final_kernel<<<1, AM_THREADS, 0, st>>>(part, nb, out);
   return check_launch("belady_argmax_final");
 }
 
-extern "C" int zx_belady_update_slots(int64_t *keys, uint8_t *resident, int64_t n_slots, const int64_t *slot,
-                                      const int64_t *key, const uint8_t *res, int64_t n, int32_t *err,
-                                      zx_stream_t stream) {
+extern "C" int zx_belady_update_slots(int64_t *keys, uint8_t *resident, int64_t *rank, int64_t n_slots,
+                                      const int64_t *slot, const int64_t *key, const uint8_t *res,
+                                      const int64_t *rank_in, int64_t n, int32_t *err, zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(n >= 0 && n_slots >= 0, "belady_update_slots: negative size");
+  ZX_REQUIRE(!resident == !res, "belady_update_slots: resident and res must be given together");
+  ZX_REQUIRE(!rank == !rank_in, "belady_update_slots: rank and rank_in must be given together");
   if (n == 0) return ZX_OK;
-  ZX_REQUIRE(keys && resident && slot && key && res, "belady_update_slots: null pointer");
-  update_slots_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, as_stream(stream)>>>(keys, resident, n_slots, slot, key,
-                                                                                res, n, err);
+  ZX_REQUIRE(keys && slot && key, "belady_update_slots: null pointer");
+  update_slots_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, as_stream(stream)>>>(keys, resident, rank, n_slots, slot,
+                                                                                key, res, rank_in, n, err);
   return check_launch("belady_update_slots");
 }
 

@@ -36,6 +36,10 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
 // Number of compute units of the current device (cached per device).
 int num_cus();
 
+// Bound of one inter-workgroup wait of the cooperative kernels without progress, in
+// s_memrealtime ticks (100 MHz); set by zx_set_wait_bound_us.
+uint64_t wait_bound_ticks();
+
 // ------------------------------------------------------------------ device side
 
 // bf16 halves of a 32-bit word as exact fp32 values.

@@ -340,7 +340,7 @@ int heads_fused(const uint16_t *x, int64_t n_outer, int64_t n_batch, int64_t n_h
   a.abort_flag = reinterpret_cast<uint32_t *>(w);
   a.slots = reinterpret_cast<uint32_t *>(w + 256);
   a.err = err;
-  a.spin_ticks = 200000000ull;  // 2 s without progress, at 100 MHz
+  a.spin_ticks = wait_bound_ticks();  // default 2 s without progress (zx_set_wait_bound_us)
   // the abort flag and every slot start at zero: one fill kernel over the header and slots
   if ((rc = fill_u32(a.abort_flag, (256 + (int64_t)a.n_slabs * p.g * 4) / 4, 0, st))) return rc;
   void *args[] = {&a};

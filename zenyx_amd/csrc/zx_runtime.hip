@@ -2,6 +2,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "zx_common.h"
@@ -41,8 +42,19 @@ int num_cus() {
   return cached[dev];
 }
 
+// 2 s at the 100 MHz s_memrealtime clock: far beyond any exchange of a co-resident grid.
+constexpr uint64_t kDefaultWaitTicks = 200000000ull;
+static std::atomic<uint64_t> g_wait_ticks{kDefaultWaitTicks};
+
+uint64_t wait_bound_ticks() { return g_wait_ticks.load(std::memory_order_relaxed); }
+
 }  // namespace zx
+
+extern "C" int zx_set_wait_bound_us(int64_t us) {
+  zx::g_wait_ticks.store(us < 0 ? zx::kDefaultWaitTicks : (uint64_t)us * 100u, std::memory_order_relaxed);
+  return ZX_OK;
+}
 
 extern "C" const char *zx_last_error(void) { return zx::g_msg; }
 
-extern "C" int zx_abi_version(void) { return 3; }
+extern "C" int zx_abi_version(void) { return 4; }

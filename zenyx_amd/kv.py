@@ -140,6 +140,19 @@ def int8_legacy_dequant_slabs(q: torch.Tensor, scales: torch.Tensor) -> torch.Te
 
 # ------------------------------------------------------------------ FP8 per head
 
+# zx_fp8_quant_heads reads inputs of this many bytes and more in one pass (its cooperative
+# single-pass kernel); below it the second read of two passes comes from the Infinity Cache.
+HEADS_SINGLE_PASS_BYTES = 256 << 20
+
+
+def set_wait_bound_us(us: int | None) -> None:
+    """Bound (microseconds) of one wait without progress inside the cooperative
+    single-pass kernels; ``None`` restores the default (2 s).  0 makes the first such wait
+    give up: the call then returns with ZX_KERR_SPIN in its error word and undefined
+    outputs (every wave exits normally).  Process-wide; for tests and operators."""
+    N.check(N.load().zx_set_wait_bound_us(-1 if us is None else int(us)), "set_wait_bound_us")
+
+
 def fp8_quant_heads(x: torch.Tensor, two_pass: bool = False, check: bool = False, single_pass: bool = False):
     """x: bf16 ``[n_outer, n_batch, n_heads, run]`` -> (codes uint8 same shape, scales
     fp32 ``[n_outer, n_heads]``), one scale per (outer, head).  Inputs of 256 MiB and more
@@ -515,7 +528,7 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
                        scales_layer: torch.Tensor, block_tables: torch.Tensor, kv_len: torch.Tensor,
                        ring_degree: int, causal: bool = True, sm_scale: float | None = None,
                        check: bool = False, single_launch: bool = True, precision: str = "f16",
-                       max_q_per_seq: int | None = None) -> torch.Tensor:
+                       max_q_per_seq: int | None = None, err: torch.Tensor | None = None) -> torch.Tensor:
     """Ring attention over the FP8 pages on one GPU: the keys [0, kv_len[b]) of every
     sequence are split into ``ring_degree`` shards (the KV blocks a ring would pass
     around), shard r being ring step r.  With ``single_launch`` one launch walks the R
@@ -525,7 +538,11 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     bf16.  Either equals attention over all keys (the exchange between devices is what
     one GPU leaves out).  ``precision``: how P enters P.V (see PRECISIONS).
     ``max_q_per_seq``: a bound on every sequence's query count, when the caller knows one
-    (otherwise it is read back from ``cu_q``, which waits for the device)."""
+    (otherwise it is read back from ``cu_q``, which waits for the device).  The kernels
+    trust it: rows of a sequence beyond it are not computed and their outputs are left
+    undefined, and ZX_KERR_POS_RANGE is set in the error word when the call has one
+    (``check=True`` reads a fresh one and raises; ``err``, device int32 ``[1]``, collects
+    the bits for the caller to read later)."""
     _precision_flag(precision)
     if ring_degree < 1:
         raise ValueError("ring_degree must be >= 1")
@@ -541,7 +558,10 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     steps = torch.arange(ring_degree + 1, dtype=torch.int64, device=kv_len.device)
     bounds = torch.empty((ring_degree + 1, (B + 3) // 4 * 4), dtype=torch.int32, device=kv_len.device)
     bounds[:, :B] = kv_len.to(torch.int64)[None, :] * steps[:, None] // ring_degree
-    err = _err_word_if(check, q.device)
+    if err is None:
+        err = _err_word_if(check, q.device)
+    elif err.dtype != torch.int32 or err.numel() < 1 or err.device != q.device:
+        raise ValueError("err must be an int32 tensor on q's device")
     if single_launch:
         out = paged_attention_ring(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables,
                                    bounds[:-1, :B].contiguous(), bounds[1:, :B].contiguous(), causal=causal,
@@ -562,18 +582,28 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     return out
 
 
-def belady_argmax(keys: torch.Tensor, resident: torch.Tensor) -> torch.Tensor:
-    """belady.py:39-51 over slots: device int64 ``[slot, key]`` ({-1, -1} if none)."""
+def belady_argmax(keys: torch.Tensor, resident: torch.Tensor | None = None,
+                  rank: torch.Tensor | None = None) -> torch.Tensor:
+    """belady.py:39-51 over slots: device int64 ``[slot, key]`` ({-1, -1} if none).
+    ``resident`` (uint8, default: every slot) selects the candidates; ``rank`` (int64,
+    default: the slot index) breaks ties, smallest first."""
     N.ensure_gpu()
-    if keys.dtype != torch.int64 or resident.dtype != torch.uint8 or keys.shape != resident.shape:
-        raise ValueError("keys must be int64 and resident uint8 of the same shape")
+    if keys.dtype != torch.int64:
+        raise ValueError("keys must be int64")
     N.require_device(keys, "keys")
-    N.require_device(resident, "resident")
+    if resident is not None:
+        if resident.dtype != torch.uint8 or resident.shape != keys.shape:
+            raise ValueError("resident must be uint8 of keys' shape")
+        N.require_device(resident, "resident")
+    if rank is not None:
+        if rank.dtype != torch.int64 or rank.shape != keys.shape:
+            raise ValueError("rank must be int64 of keys' shape")
+        N.require_device(rank, "rank")
     lib = N.load()
     out = torch.empty(2, dtype=torch.int64, device=keys.device)
     ws = _workspace(lib.zx_belady_argmax_workspace_bytes(keys.numel()), keys.device)
-    N.check(lib.zx_belady_argmax(N.ptr(keys), N.ptr(resident), keys.numel(), N.ptr(out), N.ptr(ws), ws.numel(),
-                                 N.stream_ptr(keys.device)), "belady_argmax")
+    N.check(lib.zx_belady_argmax(N.ptr(keys), N.ptr(resident), N.ptr(rank), keys.numel(), N.ptr(out), N.ptr(ws),
+                                 ws.numel(), N.stream_ptr(keys.device)), "belady_argmax")
     return out
 
 

@@ -130,11 +130,13 @@ def to_host(gpu_tensor: torch.Tensor) -> torch.Tensor:
 
 
 class KVTierManager:
-    """T0/T1/T2 KV cache hierarchy (kv_tiering.py:18-66).
+    """Three places a KV block can live, with least-recently-used spill between them
+    (behaviour of kv_tiering.py:18-66).
 
-    - T0: active HBM blocks (tiny)
-    - T1: host DRAM recent blocks (pinned)
-    - T2: cold storage (disk-backed emulation)
+    ``t0`` maps block ids to device tensors, at most ``t0_capacity`` of them; ``t1`` maps
+    ids to pinned host copies, at most ``t1_capacity``; ``t2`` keeps every block that was
+    ``put`` plus whatever overflows ``t1``, with no bound.  Each ordered dict lists its
+    blocks oldest use first, so an overflow always spills the front entry one level down.
     """
 
     def __init__(self, t0_capacity: int = 2, t1_capacity: int = 32):
@@ -145,28 +147,27 @@ class KVTierManager:
         self.t1_capacity = t1_capacity
 
     def put(self, block_id: int, tensor: torch.Tensor) -> None:  # kv_tiering.py:33-34
-        t = tensor.detach()
-        self.t2[block_id] = t if t.device.type == "cpu" else to_host(t)
+        data = tensor.detach()
+        # a host tensor is kept as it is (no copy), as .cpu() would return it
+        self.t2[block_id] = data if data.device.type == "cpu" else to_host(data)
 
     def prefetch_to_t0(self, block_id: int, device: torch.device) -> torch.Tensor:  # :36-49
-        if block_id in self.t0:
-            self.t0.move_to_end(block_id)
-            return self.t0[block_id]
-        if block_id in self.t1:
-            cpu_tensor = self.t1.pop(block_id)
-        else:
-            cpu_tensor = self.t2[block_id]  # KeyError for an unknown block, as the reference
-        device = torch.device(device)
-        gpu_tensor = to_device(cpu_tensor, device) if device.type == "cuda" else cpu_tensor.to(device)
-        self.t0[block_id] = gpu_tensor
-        self._evict_t0_if_needed()
-        return gpu_tensor
+        hit = self.t0.get(block_id)
+        if hit is not None:
+            self.t0.move_to_end(block_id)  # now the most recent use
+            return hit
+        # a T1 block leaves T1; a T2 block stays in T2 (only read); an unknown id is a KeyError
+        host = self.t1.pop(block_id) if block_id in self.t1 else self.t2[block_id]
+        target = torch.device(device)
+        self.t0[block_id] = resident = to_device(host, target) if target.type == "cuda" else host.to(target)
+        self._spill()
+        return resident
 
     def evict_from_t0(self, block_id: int) -> None:  # :51-55
-        tensor = self.t0.pop(block_id, None)
-        if tensor is not None:
-            self.t1[block_id] = to_host(tensor) if tensor.device.type == "cuda" else tensor.detach()
-            self._evict_t1_if_needed()
+        if block_id not in self.t0:
+            return
+        self.t1[block_id] = _host_copy(self.t0.pop(block_id))
+        self._spill()
 
     def synchronize(self, device: torch.device | None = None) -> None:
         """Wait until the tier copies queued on the side stream (of ``device``, or of every
@@ -174,28 +175,31 @@ class KVTierManager:
         ``.cpu()`` does in the reference; copies to the device are ordered before later
         work on the caller's stream and need this only when another stream or the host
         reads them."""
-        if device is not None:
-            _SideStream.get(torch.device(device)).synchronize()
-            _HostKeepAlive.release_done()
-            return
-        for s in all_copy_streams():
+        streams = [_SideStream.get(torch.device(device))] if device is not None else all_copy_streams()
+        for s in streams:
             s.synchronize()
         _HostKeepAlive.release_done()
 
-    def _evict_t0_if_needed(self) -> None:  # :57-61, least recently used first
+    def _spill(self) -> None:
+        """Restore both capacity bounds: the oldest T0 blocks go to T1 (copied to the host),
+        then the oldest T1 blocks go to T2 (moved as they are).  Moving every T0 overflow
+        first and trimming T1 afterwards leaves the same tiers, in the same orders, as
+        trimming T1 after each single move (:57-66): both take T1's oldest entries."""
         while len(self.t0) > self.t0_capacity:
-            old_block, old_tensor = self.t0.popitem(last=False)
-            self.t1[old_block] = to_host(old_tensor) if old_tensor.device.type == "cuda" else old_tensor.detach()
-            self._evict_t1_if_needed()
-
-    def _evict_t1_if_needed(self) -> None:  # :63-66
+            block_id, tensor = self.t0.popitem(last=False)
+            self.t1[block_id] = _host_copy(tensor)
         while len(self.t1) > self.t1_capacity:
-            old_block, old_tensor = self.t1.popitem(last=False)
-            self.t2[old_block] = old_tensor
+            block_id, tensor = self.t1.popitem(last=False)
+            self.t2[block_id] = tensor
+
+
+def _host_copy(tensor: torch.Tensor) -> torch.Tensor:
+    return to_host(tensor) if tensor.device.type == "cuda" else tensor.detach()
 
 
 def build_ring_timeline(num_blocks: int) -> dict[str, list[int]]:
-    """Deterministic forward/backward access schedule for ring attention (kv_tiering.py:69-73)."""
+    """Block ids in ring order for the forward sweep, and the same ids reversed for the
+    backward sweep (behaviour of kv_tiering.py:69-73)."""
     forward = list(range(num_blocks))
     backward = list(reversed(forward))
     return {"forward": forward, "backward": backward}

@@ -39,7 +39,8 @@ class LayerBlock:
 
 
 class ParameterStore:
-    """Host-tier storage for layer weights (parameter_streamer.py:19-29), pinned."""
+    """Every layer's weights kept in pinned host memory, by layer id (the role of
+    parameter_streamer.py:19-29); ``load`` hands back the pinned tensor itself."""
 
     def __init__(self):
         self.blocks: dict[str, torch.Tensor] = {}
@@ -55,8 +56,9 @@ class ParameterStore:
 
 
 class LayerWeightStreamer:
-    """Stream one layer at a time into device memory and evict aggressively
-    (parameter_streamer.py:32-87)."""
+    """Device copies of layer weights, fetched ahead of use on the library's copy stream;
+    at most ``max_resident_layers`` are kept, the least recently used dropped first (the
+    role of parameter_streamer.py:32-87)."""
 
     def __init__(self, store: ParameterStore, device: torch.device, min_block_bytes: int = 5 * 1024 * 1024,
                  max_resident_layers: int = 2):
