@@ -191,7 +191,11 @@ int zx_kv_quant_append(const uint16_t *x, int64_t x_layer_stride, int32_t n_laye
  * ZX_ERR_WORKSPACE before launching anything (at 8 heads, D = 128 and 32 layers: up to
  * about 980,000 tokens).  Calls no allocating routine.  Every call on one GPU uses the
  * same scratch: calls that overlap on one GPU (different streams, or host threads) race;
- * calls in one stream are ordered. */
+ * calls in one stream are ordered.  Under stream capture: make one call on the device
+ * outside the capture first (it looks up the scratch address and the single pass's
+ * occupancy, which are then cached); captured calls (single pass, two passes and static
+ * scales alike) replay with the results of an eager call.  A captured graph's replays
+ * share the scratch with every other call on that GPU. */
 #define ZX_KV_APPEND_NOALLOC_SCRATCH_BYTES (8u << 20)
 int zx_kv_quant_append_noalloc(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers,
                                int64_t n_tok, int32_t n_heads, int32_t head_dim,

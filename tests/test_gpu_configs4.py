@@ -95,26 +95,35 @@ def _assert_bf16_bits(got, want):
 
 def test_configs4_streamed_step(dev):
     """bench.py's configs[4] step end to end (bench.configs4_step over
-    LayerStreamedKVCache): layers 0, 7 and 19 are written back to pinned DRAM after their
-    append, their slots reused by layers 60, 67 and 79, and prefetched back into slots the
-    backward gathers freed; layers 60 and 79 stay resident.  For each, after the backward
-    gather: the layer's 16 scales and 2,048 sampled (sequence, position) rows of the
-    gathered K and V (all heads and channels) bit-exact against the oracle."""
+    LayerStreamedKVCache): layers 0-19 are written back to pinned DRAM after their append,
+    their slots reused by layers 60-79, and prefetched back into slots the backward
+    gathers freed; layers 20-79 stay resident.  After the backward gather:
+      * all 80 layers' 16 scales bit-exact against fp32(max(amax, 1e-8) / 448) of the
+        layer's input (amax by torch on the device, exact for bf16; the division by numpy
+        in IEEE fp32);
+      * the whole gathered K and V of layer 7 (spilled and prefetched back) and layer 60
+        (resident): every value bit-exact against the oracle's torch restatement of the
+        append followed by its gather;
+      * 2,048 sampled (sequence, position) rows of layers 0, 19 and 79 against the C
+        oracle."""
     C = bench.C5
-    H, D, P, B, Tb = C["H"], C["D"], C["P"], C["B"], C["Tb"]
+    L, H, D, P, B, Tb = C["L"], C["H"], C["D"], C["P"], C["B"], C["Tb"]
     c = bench.configs4_setup(torch, dev)
     cache = c["cache"]
     assert cache.n_spill == 20 and cache.S == 60
-    sample = (0, 7, 19, 60, 79)
+    whole = (7, 60)
+    sample = (0, 19, 79)
     rng = np.random.default_rng(17)
     S = 2048
     picks = {l: (rng.integers(0, B, S), rng.integers(0, Tb, S)) for l in sample}
-    got = {}
+    got, got_whole = {}, {}
 
     def on_gather(layer, k, v):
         if layer in picks:
             b, pos = (torch.from_numpy(a).to(dev) for a in picks[layer])
             got[layer] = (k[b, :, pos].clone(), v[b, :, pos].clone())  # [S, H, D]
+        if layer in whole:
+            got_whole[layer] = (k.cpu(), v.cpu())  # [B, H, Tb, D] each
 
     print("configs[4] streamed step: 80 layers forward + backward", flush=True)
     bench.configs4_step(torch, dev, c, on_gather)
@@ -122,6 +131,26 @@ def test_configs4_streamed_step(dev):
     cache.check_errors()
     scales = cache.scales.cpu().numpy()
     x = c["x"]
+    for layer in range(L):
+        bench.make_c5_layer(torch, dev, layer, x)
+        amax = x.abs().amax(dim=(0, 3)).float().cpu().numpy()  # [2, H], exact
+        want = np.maximum(amax, np.float32(1e-8)).astype(np.float32) / np.float32(448.0)
+        np.testing.assert_array_equal(scales[layer].view(np.uint32), want.view(np.uint32))
+    print(f"all {L} layers' scales bit-exact", flush=True)
+    # identity tables: the gathered values do not depend on which pages hold the codes
+    seq_tables = np.arange(B * Tb // P, dtype=np.int32).reshape(B, Tb // P)
+    cu = np.arange(0, B * Tb + 1, Tb, dtype=np.int32)
+    for layer in whole:
+        bench.make_c5_layer(torch, dev, layer, x)
+        wsc, wpool = O.kv_quant_append_torch(x.cpu(), cu, seq_tables, B * Tb // P, P)
+        np.testing.assert_array_equal(scales[layer].view(np.uint32), wsc.numpy().view(np.uint32))
+        wk, wv = O.kv_gather_dequant_torch(wpool, wsc, seq_tables, np.full(B, Tb, np.int32), Tb)
+        for name, g_, w_ in (("K", got_whole[layer][0], wk), ("V", got_whole[layer][1], wv)):
+            gi, wi = g_.view(torch.int16), w_.view(torch.int16)
+            assert torch.equal(gi, wi), f"layer {layer} {name}: {(gi != wi).sum().item()} values differ"
+        where = "spilled to pinned DRAM and prefetched back" if layer < cache.n_spill else "resident"
+        print(f"layer {layer} ({where}): every gathered value ({2 * wk.numel()}) bit-exact", flush=True)
+        del wpool, wk, wv
     for layer in sample:
         bench.make_c5_layer(torch, dev, layer, x)
         xb = bits16(x)
@@ -134,5 +163,5 @@ def test_configs4_streamed_step(dev):
         _assert_bf16_bits(gv, deq[1].transpose(1, 0, 2))
         where = "spilled to pinned DRAM and prefetched back" if layer < cache.n_spill else "resident"
         print(f"layer {layer} ({where}): scales and {S} gathered rows bit-exact", flush=True)
-    del c, cache, x, got
+    del c, cache, x, got, got_whole
     torch.cuda.empty_cache()

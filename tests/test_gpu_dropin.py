@@ -293,8 +293,26 @@ def test_tiering_manager_plan_matches_oracle(dev):
     n = len(trace)
     d2h, h2d = m.transfers(n // 2, n)
     assert len(h2d) > 0 and len(d2h) >= 0
-    r = m.replay_transfers(n // 2, n)
+    r = m.replay_transfers(n // 2, n, check_bytes=True)
     assert r["h2d_pages"] == len(h2d) and r["d2h_pages"] == len(d2h)
+
+
+def test_tier_replay_both_directions_round_trip(dev):
+    """A budget below one layer's pages: inside a layer's forward window, victims used again
+    later are written back (D2H) while pages evicted earlier come back (H2D), on the two
+    copy streams at once.  Every page's bytes must be intact on both sides afterwards (a
+    copy that ran before the one bringing its page in would leave filler)."""
+    m = BeladyKVCacheTieringManager(num_devices=8, context_length=8 * 64 * 32, num_layers=3, num_kv_heads=8,
+                                    head_dim=128, page_tokens=64, hbm_budget_bytes=100 * 128 * 1024)
+    assert m.capacity == 100 and m.pages_per_shard == 32  # 256 pages per layer
+    m.plan()
+    per_layer = len(m.sequence) // 2 // 3
+    d2h, h2d = m.transfers(per_layer, 2 * per_layer)
+    assert len(d2h) > 0 and len(h2d) > 0
+    assert len(np.intersect1d(d2h, h2d)) > 0  # pages written back and fetched again in the window
+    for max_batch in (16, 1024):  # short chunks (many cross-stream waits) and the default
+        r = m.replay_transfers(per_layer, 2 * per_layer, check_bytes=True, max_batch=max_batch)
+        assert r["d2h_pages"] == len(d2h) and r["h2d_pages"] == len(h2d) and r["chunks"] > 1
 
 
 def test_quantized_ring_attention_over_paged_cache(dev):

@@ -1,16 +1,16 @@
 """Parity at BASELINE's full sizes, on the exact workloads bench.py times.
 
 * configs[1] (seed 1: 32 layers x 74,902 tokens, 8 KV heads, D = 128, page 16, outlier
-  heads x50): one fused append of all layers; all 512 scales bit-exact against the
-  oracle's amax over each whole layer, one whole layer's pool (every code) against the
-  oracle's torch restatement, and 2,048 sampled token rows of three more layers (all K/V,
-  heads and channels) against the C oracle's append of those rows.
-* configs[2] (64 x 32,768 positions, 300,000-page pool): the full gather; 4,096 sampled
-  positions of every (sequence, head) checked bit-exact against the oracle's dequant.
+  heads x50): one fused append of all layers; all 512 scales bit-exact against the C
+  oracle's amax over each whole layer, and every layer's pool (every code of all 32
+  layers) against the oracle's torch restatement of the append.
+* configs[2] (64 x 32,768 positions, 300,000-page pool): the full gather, every gathered
+  bf16 of all 64 sequences (K and V) bit-exact against the oracle's torch restatement.
 * the decode attention over the same pool, two whole sequences checked against the
   oracle within the stated tolerance (one bf16 ulp plus 2^-17 max|V|).
-* ring attention at bench.py's ring workload (4 x 8,192 causal): sampled rows against the
-  oracle at ring degree 1 and 8, and ring 8 against ring 1 on every output.
+* ring attention at bench.py's ring workload (4 x 8,192 causal): 128 rows (blocks of 8
+  consecutive rows spread over the causal range of every sequence) against the oracle
+  at ring degree 1 and 8, and ring 8 against ring 1 on every output.
 * configs[3] (1M tokens, 80 layers, ring 8, 64 GB budget: 20,971,520 accesses): the whole
   Belady schedule of the GPU simulator -- every eviction's position and page, and the
   miss flags of every access -- against the C heap oracle.
@@ -35,45 +35,26 @@ def bits16(t: torch.Tensor) -> np.ndarray:
 
 
 def test_configs1_full_append(dev):
-    """configs[1]: all 32 layers' 16 scales against the oracle's amax over each whole layer;
-    one whole layer's pool (4,688 pages, every code) against the torch restatement of the
-    append (bit-identical to the C oracle, tests/test_oracle.py); 2,048 sampled rows of
-    three more layers against the C oracle."""
+    """all 32 layers' 16 scales against the C oracle's amax over each whole
+    layer, and every layer's pool (4,688 pages, every code) against the torch restatement
+    of the append (bit-identical to the C oracle, tests/test_oracle.py)."""
     W = bench.make_append_workload(torch, dev, seed=1)
     print(f"configs[1]: {W['T']} tokens x {W['L']} layers", flush=True)
     sc = kv.kv_quant_append(W["x"], W["cu"], W["bt"], W["pool"], check=True)
     torch.cuda.synchronize()
-    L, H, D, P, T = W["L"], W["H"], W["D"], W["P"], W["T"]
+    L, H, P = W["L"], W["H"], W["P"]
     cu, bt = W["cu_host"].numpy(), W["bt_host"].numpy()
     got_sc = sc.cpu().numpy()
     for layer in range(L):
-        xb = bits16(W["x"][layer])  # [T, 2, H, D]
-        wsc = O.kv_scales(xb[None])[0]
+        x_l = W["x"][layer].cpu()  # [T, 2, H, D]
+        wsc = O.kv_scales(x_l.view(torch.int16).numpy().view(np.uint16)[None])[0]
         np.testing.assert_array_equal(got_sc[layer].view(np.uint32), wsc.view(np.uint32))
-    print(f"all {L * 2 * H} scales bit-exact", flush=True)
-    whole = 22
-    wsc_t, wpool = O.kv_quant_append_torch(W["x"][whole].cpu(), cu, bt, W["n_pages"], P)
-    np.testing.assert_array_equal(got_sc[whole].view(np.uint32), wsc_t.numpy().view(np.uint32))
-    gpool = W["pool"][whole].cpu()
-    assert torch.equal(gpool, wpool), f"layer {whole}: {(gpool != wpool).sum().item()} codes differ"
-    print(f"layer {whole}: the whole pool ({gpool.numel()} codes) bit-exact", flush=True)
-    rng = np.random.default_rng(11)
-    for layer in (0, 13, 31):
-        xb = bits16(W["x"][layer])
-        wsc = O.kv_scales(xb[None])[0]
-        S = 2048
-        tok = np.sort(rng.choice(T, S, replace=False))
-        b = np.searchsorted(cu, tok, side="right") - 1
-        pos = tok - cu[b]
-        page = bt[b, pos // P]
-        got = W["pool"][layer].cpu().numpy()[page, :, :, pos % P, :]  # [S, 2, H, D]
-        compact = np.zeros((1, S // P, 2, H, P, D), np.uint8)
-        _, werr = O.kv_quant_append(np.ascontiguousarray(xb[tok])[None], np.array([0, S], np.int32), None,
-                                    np.arange(S // P, dtype=np.int32)[None], compact, P, scales=wsc[None])
-        assert werr == 0
-        want = compact[0].transpose(0, 3, 1, 2, 4).reshape(S, 2, H, D)
-        np.testing.assert_array_equal(got, want)
-        print(f"layer {layer}: {S} rows bit-exact", flush=True)
+        wsc_t, wpool = O.kv_quant_append_torch(x_l, cu, bt, W["n_pages"], P)
+        np.testing.assert_array_equal(got_sc[layer].view(np.uint32), wsc_t.numpy().view(np.uint32))
+        gpool = W["pool"][layer].cpu()
+        assert torch.equal(gpool, wpool), f"layer {layer}: {(gpool != wpool).sum().item()} codes differ"
+    print(f"all {L * 2 * H} scales and every code of all {L} layers ({W['pool'].numel()} bytes) bit-exact",
+          flush=True)
 
 
 def test_configs2_full_gather_and_attention(dev):
@@ -82,24 +63,21 @@ def test_configs2_full_gather_and_attention(dev):
     sc = G["scales"][G["layer"]].contiguous()
     k, v = kv.kv_gather_dequant(G["pool"], sc, G["bt"], G["seq_lens"], T, check=True)
     torch.cuda.synchronize()
-    rng = np.random.default_rng(5)
-    S = 4096
-    t = np.sort(rng.choice(T, S, replace=False))
     bt = G["bt_host"].numpy()
     scl = G["scales_host"][G["layer"]].numpy()
-    dec = O.e4m3_decode(np.arange(256, dtype=np.uint8))
-    for b in (0, 21, 63):
-        pages = torch.from_numpy(bt[b, t // P].astype(np.int64)).to(dev)
-        codes = G["pool"][pages].cpu().numpy()  # [S, 2, H, P, D]
-        for kvi, out in ((0, k), (1, v)):
-            c = codes[np.arange(S), kvi, :, t % P, :]  # [S, H, D]
-            want = O.bf16_rne(dec[c] * scl[kvi][None, :, None])
-            got = bits16(out[b][:, t, :]).transpose(1, 0, 2)  # [S, H, D]
-            np.testing.assert_array_equal(got, want)
-    print("gather: 3 sequences x 4096 positions bit-exact", flush=True)
-    del k, v
+    pool_host = G["pool"].cpu()
+    lens = G["seq_lens"].cpu().numpy()
+    for b in range(B):  # every gathered value, one sequence at a time
+        wk, wv = O.kv_gather_dequant_torch(pool_host, torch.from_numpy(scl), bt[b:b + 1], lens[b:b + 1], T)
+        for name, got, want in (("K", k[b], wk[0]), ("V", v[b], wv[0])):
+            g_ = got.cpu().view(torch.int16)
+            w_ = want.view(torch.int16)
+            assert torch.equal(g_, w_), f"sequence {b} {name}: {(g_ != w_).sum().item()} values differ"
+    print(f"gather: all {B} sequences x {T} positions (K and V, {2 * k.numel()} values) bit-exact", flush=True)
+    del k, v, pool_host
     torch.cuda.empty_cache()
 
+    dec = O.e4m3_decode(np.arange(256, dtype=np.uint8))
     Hq = 32
     q = torch.randn((B, Hq, D), generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
     out = kv.paged_attention_decode(q.to(dev), G["pool"], sc, G["bt"], G["seq_lens"], check=True)
@@ -151,18 +129,20 @@ def test_ring_attention_bench_shape(dev):
         for h in range(H):
             vmax[b, h] = np.maximum.accumulate(dec[codes[pages, 1, h, t % P, :]], axis=0) * float(sc[1, h])
     q_bits = bits16(R["q_host"])
-    for b, row in ((0, 0), (0, 1), (0, 4095), (0, 8191), (3, 17), (3, 8190)):
-        i = b * T + row
-        want, _, err = O.paged_attention_prefill(q_bits[i:i + 1], np.array([0, 1], np.int32),
-                                                 np.array([row], np.int32), codes, sc, bt[b:b + 1],
+    blocks = [(b, r0) for b in range(R["B"]) for r0 in (0, 1000 + 1500 * b, 4096 + 700 * b, T - 8)]
+    for b, r0 in blocks:  # 4 blocks of 8 consecutive rows per sequence: 128 rows
+        i = b * T + r0
+        rows = np.arange(r0, r0 + 8)
+        want, _, err = O.paged_attention_prefill(q_bits[i:i + 8], np.array([0, 8], np.int32),
+                                                 np.array([r0], np.int32), codes, sc, bt[b:b + 1],
                                                  np.zeros(1, np.int32), np.full(1, T, np.int32), True, sm)
         assert err == 0
-        vm = np.repeat(vmax[b, :, row], grp, axis=0)[None]  # [1, Hq, D]
+        vm = np.repeat(vmax[b][:, rows], grp, axis=0).transpose(1, 0, 2)  # [8, Hq, D]
         for ring in (1, 8, "8s"):
-            assert_within_bound(bits16(outs[ring][i:i + 1]), want, vm, 2.0 ** -10, ulps=2)
-        assert_within_one_ulp(bits16(outs["1x"][i:i + 1]), want, vm)
-    print("ring 1, ring 8 (one launch) and ring 8 (eight launches), and ring 1 exact: 6 rows x 32 heads within "
-          "tolerance of the oracle", flush=True)
+            assert_within_bound(bits16(outs[ring][i:i + 8]), want, vm, 2.0 ** -10, ulps=2)
+        assert_within_one_ulp(bits16(outs["1x"][i:i + 8]), want, vm)
+    print(f"ring 1, ring 8 (one launch) and ring 8 (eight launches), and ring 1 exact: {8 * len(blocks)} rows x "
+          "32 heads within tolerance of the oracle", flush=True)
     for other in (8, "8s"):
         for b in range(R["B"]):  # one sequence at a time (float32 is exact for bf16 values and their differences)
             a = outs[1][b * T:(b + 1) * T].float().cpu().numpy()

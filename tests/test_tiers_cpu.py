@@ -175,3 +175,41 @@ def test_fifo_slots_rejects_bad_sequences():
         fifo_slots([0], [1], [1], [2], 4)
     with pytest.raises(ValueError):  # three resident pages in two slots
         fifo_slots([0, 1, 2], [1, 2, 3], [], [], 2)
+
+
+def test_replay_chunks_respect_cross_direction_order():
+    """BeladyKVCacheTieringManager._chunks on random move lists: every chunk waits only for
+    a chunk of the other direction issued before it, and every move whose page last moved
+    the other way is covered by that wait (or by an earlier chunk of its own stream, which
+    waited already), so the two copy streams run in a valid order without a cycle."""
+    import numpy as np
+
+    from zenyx_amd.train.belayd_kv_cache_tiering import BeladyKVCacheTieringManager as M
+
+    rng = np.random.default_rng(3)
+    for n, pages, cap in [(50, 5, 4), (400, 40, 16), (3000, 300, 64), (3000, 3000, 1024)]:
+        page = rng.integers(0, pages, n)
+        kind = np.empty(n, np.int8)
+        state = {}
+        for i, p in enumerate(page):  # alternate per page, as D2H / H2D of one page do
+            kind[i] = state.get(int(p), int(rng.integers(0, 2)))
+            state[int(p)] = 1 - kind[i]
+        chunks = M._chunks(kind, page, cap)
+        issued = {0: 0, 1: 0}
+        chunk_of = {}  # move index -> (direction, chunk index)
+        waited = {0: -1, 1: -1}  # highest chunk of the other direction each stream has waited for
+        seen = set()
+        for k, idx, wait in chunks:
+            assert wait < issued[1 - k], "a chunk waits for one not issued yet"
+            waited[k] = max(waited[k], wait)
+            assert 0 < len(idx) <= cap and all(kind[i] == k for i in idx)
+            for i in idx:
+                chunk_of[i] = (k, issued[k])
+                seen.add(i)
+            issued[k] += 1
+            for i in idx:  # this move's page's previous move in the other direction is covered
+                prev = [j for j in range(i) if page[j] == page[i]]
+                if prev and kind[prev[-1]] != k:
+                    pk, pc = chunk_of[prev[-1]]
+                    assert pc <= waited[k]
+        assert seen == set(range(n))

@@ -78,3 +78,46 @@ def test_noalloc_append_refuses_more_than_its_scratch(dev):
     assert b"scratch" in lib.zx_last_error()
     torch.cuda.synchronize(dev)
     assert int(err.item()) == 0 and not pool.any()  # nothing ran
+
+
+@pytest.mark.parametrize("mode", ["single_pass", "two_pass", "static"])
+def test_noalloc_append_in_a_captured_graph(dev, mode):
+    """The allocation-free append captured into a HIP graph (torch.cuda.CUDAGraph) after
+    one eager call (which takes the scratch address and the occupancy figures), then
+    replayed three times with eager work and synchronisations between the replays: each
+    replay's pool, scales and error word equal zx_kv_quant_append's eager result bit for
+    bit.  The cooperative single pass, the two passes and the static path all capture."""
+    L, H, D, P = 3, 8, 128, 16
+    x, cu, bt, n_pages = _case(L, H, D, P, [700, 33, 1500, 1], seed=5, dev=dev)
+    static = mode == "static"
+    flags = {"single_pass": 0, "two_pass": N.ZX_APPEND_TWO_PASS, "static": N.ZX_APPEND_STATIC_SCALES}[mode]
+    pool_e = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8, device=dev)
+    if static:
+        sc_e = torch.rand((L, 2, H), generator=torch.Generator().manual_seed(1)).to(dev) * 0.01 + 0.002
+    else:
+        sc_e = torch.empty((L, 2, H), dtype=torch.float32, device=dev)
+    err_e = torch.zeros(1, dtype=torch.int32, device=dev)
+    kv.kv_quant_append(x, cu, bt, pool_e, scales=sc_e, static_scales=static, two_pass=mode == "two_pass", err=err_e)
+    pool_g = torch.zeros_like(pool_e)
+    sc_g = sc_e.clone()
+    err_g = torch.zeros(1, dtype=torch.int32, device=dev)
+    N.check(_noalloc(x, cu, bt, pool_g, sc_g, flags, err_g), "kv_quant_append_noalloc (eager)")
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
+        rc = _noalloc(x, cu, bt, pool_g, sc_g, flags, err_g)
+    assert rc == N.ZX_OK, N.load().zx_last_error()
+    for rep in range(3):
+        pool_g.zero_()  # the eager pool started from zeros too
+        err_g.zero_()
+        if not static:
+            sc_g.fill_(-1.0)
+        torch.cuda.synchronize(dev)
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(pool_g, pool_e), f"replay {rep}: {(pool_g != pool_e).sum().item()} codes differ"
+        assert torch.equal(sc_g.view(torch.int32), sc_e.view(torch.int32)), f"replay {rep}: scales differ"
+        assert int(err_g.item()) == int(err_e.item()), f"replay {rep}: error word differs"
+        x.mul_(1.0)  # eager work between replays

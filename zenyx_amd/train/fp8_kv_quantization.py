@@ -146,8 +146,10 @@ class PagedFP8KVCache:
         return self._rows_cache[1]
 
     def _tables(self, seq_ids) -> torch.Tensor:
-        """Device int32 ``[len(seq_ids), width]`` block tables of seq_ids, -1 past their pages."""
-        return self._bt.index_select(0, self._rows(seq_ids))
+        """Device int32 ``[len(seq_ids), width]`` block tables of seq_ids, -1 past their pages;
+        width = the most pages any of them holds (the kernels size their work by it)."""
+        width = max(1, max(len(self.pages.get(s, ())) for s in seq_ids))
+        return self._bt[:, :width].index_select(0, self._rows(seq_ids))
 
     def _lengths(self, seq_ids) -> torch.Tensor:
         """Device int32 tokens stored per sequence of seq_ids."""
@@ -166,8 +168,9 @@ class PagedFP8KVCache:
         cu = [0]
         for v in lengths:
             cu.append(cu[-1] + v)
-        t = torch.tensor([list(lengths) + [0], cu], dtype=torch.int32).to(self.device)
-        return t[0, :n], t[1]
+        w = (n + 4) // 4 * 4  # rows padded to 16 bytes: each part starts 16-byte aligned
+        t = torch.tensor([list(lengths) + [0] * (w - n), cu + [0] * (w - n - 1)], dtype=torch.int32).to(self.device)
+        return t[0, :n], t[1, :n + 1]
 
     def _reserve(self, seq_id, new_len: int, taken: list, entries: list) -> None:
         pages = self.pages.setdefault(seq_id, [])
@@ -238,7 +241,7 @@ class PagedFP8KVCache:
             self._write_entries(entries)
             counts, cu = self._counts(lengths)
             rows = self._rows(seq_ids)
-            kv.kv_quant_append(x.to(self.device), cu, self._bt.index_select(0, rows), self.pool, scales=self.scales,
+            kv.kv_quant_append(x.to(self.device), cu, self._tables(seq_ids), self.pool, scales=self.scales,
                                start_pos=self._len.index_select(0, rows),
                                static_scales=not dyn, saturate=(not dyn) and self.overflow == "saturate",
                                err=word)
