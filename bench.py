@@ -759,8 +759,10 @@ def ring_attention_leg(torch, dev, steps, warmup, skip_cpu):
                                     ("ring8_exact", 8, True, "exact"), ("ring1_bf16p", 1, True, "bf16")):
         fn = lambda: kv.ring_attention_fp8(q, cu, qp, pool, sc, bt, kl, ring_degree=ring, causal=True,  # noqa: E731
                                            single_launch=single, precision=prec, max_q_per_seq=T)
-        # the kernel's first ~25 launches run slower, settling from ~3.5 ms to ~2.8 ms (kernel
-        # trace of the default mode): time the steady state
+        # the first ~15-25 launches of a leg run slower while the GPU's clock rises: each
+        # launch takes the same number of cycles (GRBM_GUI_ACTIVE ~44 M summed over the
+        # XCDs) while the duration falls from ~3.0 ms to ~2.4 ms (about 1.86 -> 2.28 GHz per
+        # XCD); at least 25 warm-up calls, so the timed calls run at the settled clock
         ms, _, _ = time_steps(torch, fn, steps, max(warmup, 25))
         tf = flops / (ms * 1e-3) / 1e12
         how = "one launch walking the shards" if single else "one launch per shard, merged through HBM"
