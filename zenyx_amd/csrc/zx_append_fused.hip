@@ -5,10 +5,13 @@
 // them can be encoded.  Instead of reading the input twice (amax pass + quant pass), one
 // cooperative persistent launch keeps each workgroup's share of a slab on chip:
 //   * workgroup w (one per CU) owns tokens [w*T/G, (w+1)*T/G) of every slab;
-//   * 15 data waves keep NB = 4 slabs of their share in registers.  At step s a wave
-//     reduces the max of slab s+3 (loaded during step s-1), hands it to the workgroup,
-//     waits for slab s's scale, encodes slab s and refills that buffer with slab s+4, so
+//   * 15 data waves keep NB = 5 slabs of their share in registers.  At step s a wave
+//     reduces the max of slab s+4 (loaded during step s-1), hands it to the workgroup,
+//     waits for slab s's scale, encodes slab s and refills that buffer with slab s+5, so
 //     loads stay in flight continuously and no block-wide barrier is ever taken;
+//   * slabs go in the order (K head 0, V head 0, K head 1, ...) of each layer, with K and
+//     V swapped on odd workgroups, so half the chip reads one half of the token rows while
+//     the other half reads the other;
 //   * a wave's max goes to an LDS slot (ds_max + arrival count); the control wave (the
 //     16th) stores the workgroup's max plus one into its own device-coherent slot of
 //     slab s (slots start at zero), reads all G slots of a slab with one wave-wide load
@@ -105,6 +108,20 @@ template <int K, bool WIDE> struct ThreadMap {
 __device__ __forceinline__ int64_t vec_src(const FusedArgs &a, int v) {
   const int64_t row_bytes = 4LL * a.n_heads * a.head_dim;
   return (int64_t)(v >> a.vpt_log2) * row_bytes + (v & ((1 << a.vpt_log2) - 1)) * 16;
+}
+
+// Slab order.  Each layer's slabs go as (K head 0, V head 0, K head 1, V head 1, ...), with
+// K and V swapped on odd workgroups: at any time half the chip reads the K half of the
+// token rows and half the V half (2 KiB apart at H = 8, D = 128).  Concurrent reads that
+// all sit at the same offset inside 4 KiB rows load the memory system unevenly: on MI355X
+// a walk over one 256-byte column of every row reads ~7% slower than one that takes
+// column j from half the rows and column j + 8 from the other half.  Sequence index q ->
+// physical slab l * 2H + kv * H + h: the index of scales, exchange slots and pool slabs.
+__device__ __forceinline__ int phys_slab(const FusedArgs &a, int q) {
+  const int two_h = 2 * a.n_heads;
+  const int l = q / two_h, r = q - l * two_h;
+  const int kv = (r & 1) ^ (int)(blockIdx.x & 1);
+  return l * two_h + kv * a.n_heads + (r >> 1);
 }
 
 __device__ __forceinline__ const char *slab_src(const FusedArgs &a, int s, int64_t t_lo) {
@@ -221,7 +238,7 @@ __device__ __forceinline__ bool control_loop(const FusedArgs &a, FusedShared &sh
       ZX_COMPILER_FENCE();
       const uint32_t mx = ld_lds(&sh.max[slot]);
       if (lane == 0) {
-        __hip_atomic_store(&a.slots[(int64_t)next_pub * G + blockIdx.x], mx + 1u, __ATOMIC_RELAXED,
+        __hip_atomic_store(&a.slots[(int64_t)phys_slab(a, next_pub) * G + blockIdx.x], mx + 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
         sh.max[slot] = 0;
         sh.cnt[slot] = 0;
@@ -230,7 +247,7 @@ __device__ __forceinline__ bool control_loop(const FusedArgs &a, FusedShared &sh
       progress = true;
     }
     if (next_res < next_pub) {
-      const uint32_t *row = a.slots + (int64_t)next_res * G;
+      const uint32_t *row = a.slots + (int64_t)phys_slab(a, next_res) * G;
       uint32_t mx = 0;
       bool full = true;
       for (uint32_t i = lane; i < G; i += 64) {
@@ -243,7 +260,7 @@ __device__ __forceinline__ bool control_loop(const FusedArgs &a, FusedShared &sh
         const float sc = scale_from_amax_bits(mx << 16);
         const int slot = next_res & (FA_SLOTS - 1);
         if (lane == 0) {
-          if (blockIdx.x == 0) a.scales[next_res] = sc;
+          if (blockIdx.x == 0) a.scales[phys_slab(a, next_res)] = sc;
           sh.scale[slot] = sc;
           ZX_COMPILER_FENCE();
           __hip_atomic_store(&sh.ready[slot], (uint32_t)(next_res + 1), __ATOMIC_RELAXED,
@@ -293,8 +310,9 @@ __global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArg
   if (threadIdx.x == 0) sh.abort = 0;
   __syncthreads();
 
+  const int S_pad = (int)ceil_div(S, NB) * NB;
   if (threadIdx.x >= FA_DATA_THREADS) {  // control wave
-    if (!control_loop(a, sh, S, (int)ceil_div(S, NB) * NB, G, NB) && threadIdx.x == FA_DATA_THREADS) {
+    if (!control_loop(a, sh, S, S_pad, G, NB) && threadIdx.x == FA_DATA_THREADS) {
       __hip_atomic_fetch_or(a.abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (a.err) atomicOr(a.err, ZX_KERR_SPIN);
       __hip_atomic_store(&sh.abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -330,33 +348,31 @@ __global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArg
 
   // Slabs past the end are clamped to the last one: the loads stay unconditional (and
   // valid) and their maxes are simply not contributed.
-  auto clamp = [&](int s) { return s < S ? s : S - 1; };
+  auto slab = [&](int q) { return phys_slab(a, q < S ? q : S - 1); };
   uint4 buf[NB][K];
 #pragma unroll
-  for (int i = 0; i < NB; ++i) load_share<K, WIDE>(a, m, clamp(i), t_base, buf[i]);
+  for (int i = 0; i < NB; ++i) load_share<K, WIDE>(a, m, slab(i), t_base, buf[i]);
 #pragma unroll
-  for (int i = 0; i + 1 < NB; ++i)
-    contribute(sh, i, share_max<K, SPILL, WIDE>(a, m, clamp(i), t_lo, nv, buf[i]), i < S);
+  for (int i = 0; i + 1 < NB; ++i) contribute(sh, i, share_max<K, SPILL, WIDE>(a, m, slab(i), t_lo, nv, buf[i]), i < S);
 
-  // step s (buffer i = s % NB): reduce s + NB - 1 (loaded during step s - 1), wait for
-  // slab s's scale, encode s, refill the buffer with s + NB.  Reducing first hands the
+  // step q (buffer i = q % NB): reduce q + NB - 1 (loaded during step q - 1), wait for
+  // slab q's scale, encode q, refill the buffer with q + NB.  Reducing first hands the
   // max to the control wave before this wave blocks on a scale, so the device-wide round
-  // trip of slab s + NB - 1 starts as early as its data allows.  The slab count is padded
+  // trip of slab q + NB - 1 starts as early as its data allows.  The slab count is padded
   // to a multiple of NB so every unrolled step is unconditional (padded steps encode into
   // the dummy slot; the control wave marks them ready at the end); an aborted wait leaves
   // the kernel directly.
-  const int S_pad = (int)ceil_div(S, NB) * NB;
-  for (int s0 = 0; s0 < S_pad; s0 += NB) {
+  for (int q0 = 0; q0 < S_pad; q0 += NB) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const int s = s0 + i;
+      const int q = q0 + i;
       const int j = (i + NB - 1) % NB;  // constant after unrolling
-      contribute(sh, s + NB - 1, share_max<K, SPILL, WIDE>(a, m, clamp(s + NB - 1), t_lo, nv, buf[j]),
-                 s + NB - 1 < S);
+      const int r = q + NB - 1;
+      contribute(sh, r, share_max<K, SPILL, WIDE>(a, m, slab(r), t_lo, nv, buf[j]), r < S);
       float sc;
-      if (!wait_ready(sh, s, sc)) return;
-      encode_share<K, SPILL, WIDE>(a, m, s, t_lo, nv, buf[i], sc, s < S ? slab_dst(a, s) : nullptr, dummy);
-      load_share<K, WIDE>(a, m, clamp(s + NB), t_base, buf[i]);
+      if (!wait_ready(sh, q, sc)) return;
+      encode_share<K, SPILL, WIDE>(a, m, slab(q), t_lo, nv, buf[i], sc, q < S ? slab_dst(a, slab(q)) : nullptr, dummy);
+      load_share<K, WIDE>(a, m, slab(q + NB), t_base, buf[i]);
     }
   }
 }
@@ -366,11 +382,12 @@ __global__ void __launch_bounds__(FA_THREADS, 1) kv_append_fused_kernel(FusedArg
 #ifndef FA_K_CHOICE
 #define FA_K_CHOICE 5
 #endif
-#ifndef FA_NB_CHOICE
-#define FA_NB_CHOICE 4
-#endif
+// Register buffers: 5 (four slabs of look-ahead, 127 VGPRs) where the data path is
+// straight-line code; 4 where the re-read loops (SPILL) or 64-bit stores (WIDE) need the
+// registers (NB = 5 spills there).  On configs[1], NB = 3 / 4 / 5 run 3.33 / 3.15 /
+// 3.12 ms per call.
 constexpr int FA_K = FA_K_CHOICE;
-#define FA_KERNEL(spill, wide) kv_append_fused_kernel<FA_K, FA_NB_CHOICE, spill, wide>
+#define FA_KERNEL(spill, wide) kv_append_fused_kernel<FA_K, ((spill) || (wide)) ? 4 : 5, spill, wide>
 
 static int fused_supported() {
   static int cached[64] = {0};
