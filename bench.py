@@ -277,7 +277,7 @@ def belady_leg(torch, dev, skip_cpu):
             "overlapped_with": "20 paged gather+dequant kernels on the compute stream", "wall_ms": round(r["wall_ms"], 3)}
         log(f"tier moves, {name}: {r['d2h_pages']} D2H pages at {r['d2h_GBps']:.1f} GB/s, {r['h2d_pages']} H2D pages "
             f"at {r['h2d_GBps']:.1f} GB/s")
-    out["tier_moves"]["both_directions"] = bidirectional_window(torch, dev, compute)
+    out["tier_moves"]["both_directions"] = bidirectional_window(torch, dev, compute, skip_cpu)
     out["dropin_cache"] = dropin_belady_leg(torch, dev, m.capacity, len(m.sequence))
     out["curriculum"] = curriculum_leg(torch, dev, skip_cpu)
     if not skip_cpu:
@@ -310,20 +310,39 @@ def belady_leg(torch, dev, skip_cpu):
     return out
 
 
-def bidirectional_window(torch, dev, compute):
+def bidirectional_window(torch, dev, compute, skip_cpu=True):
     """Tier moves in both directions at once: configs[3]'s geometry (ring 8 over 1M tokens,
     64-token FP8 pages of 128 KiB, 16,384 pages = 2 GiB per layer) for 3 layers under an
     HBM budget of 12,288 pages (1.5 GiB), smaller than one layer.  Inside layer 1's
     forward window the ring revisits its shards, so Belady writes back victims that are
     used again later (D2H) while pages it evicted earlier come back (H2D); the replay runs
     the two directions on the library's two copy streams at the same time, beside
-    ``compute`` on the compute stream."""
+    ``compute`` on the compute stream.  Also times the schedule itself: with a budget below
+    one layer almost every window of the simulator has victims among the pages it has just
+    seen, the regime where the next victim depends on the one before."""
     from zenyx_amd.train.belayd_kv_cache_tiering import BeladyKVCacheTieringManager
 
     pb = 64 * 8 * 128 * 2
     m = BeladyKVCacheTieringManager(num_devices=8, context_length=2**20, num_layers=3, num_kv_heads=8,
                                     head_dim=128, page_tokens=64, hbm_budget_bytes=12288 * pb, device=dev)
-    m.plan()
+    m.plan()  # warm-up
+    stats = m.plan()
+    sim_s = m.timings["simulate_s"]
+    sched = {"accesses": len(m.sequence), "evictions": stats["evictions"], "simulate_ms": round(sim_s * 1e3, 3),
+             "evictions_per_s": round(stats["evictions"] / sim_s, 1)}
+    log(f"small-budget schedule: {stats['evictions']} evictions over {len(m.sequence)} accesses in "
+        f"{sim_s * 1e3:.1f} ms")
+    if not skip_cpu:
+        from oracle import oracle as O
+
+        trace = m.sequence.trace("cpu").numpy()
+        t0 = time.perf_counter()
+        _, _, st = O.belady_simulate(trace, m.n_pages, m.capacity, evict_cap=1)
+        dt = time.perf_counter() - t0
+        assert st["evictions"] == stats["evictions"], "GPU and CPU Belady disagree on the eviction count"
+        sched["cpu_baseline"] = {"value": round(st["evictions"] / dt, 1), "unit": "evictions/s", "cores": 1,
+                                 "kind": "port", "sample": f"C oracle (indexed binary heap, 1 thread), the same "
+                                                           f"trace: {dt * 1e3:.1f} ms"}
     per_layer = len(m.sequence) // 2 // 3
     a = per_layer
     m.replay_transfers(a, a + per_layer)  # warm-up: pinned pools, copy engines
@@ -334,7 +353,8 @@ def bidirectional_window(torch, dev, compute):
            "d2h_GBps": round(r["d2h_GBps"], 2), "h2d_GBps": round(r["h2d_GBps"], 2),
            "both_directions_GBps": round(r["both_GBps"], 2), "copy_span_ms": round(r["copy_span_ms"], 3),
            "d2h_ms": round(r["d2h_ms"], 3), "h2d_ms": round(r["h2d_ms"], 3),
-           "overlapped_with": "20 paged gather+dequant kernels on the compute stream", "wall_ms": round(r["wall_ms"], 3)}
+           "overlapped_with": "20 paged gather+dequant kernels on the compute stream", "wall_ms": round(r["wall_ms"], 3),
+           "schedule": sched}
     log(f"tier moves, both directions: {r['d2h_pages']} D2H pages at {r['d2h_GBps']:.1f} GB/s and {r['h2d_pages']} "
         f"H2D pages at {r['h2d_GBps']:.1f} GB/s in {r['chunks']} chunks; {r['both_GBps']:.1f} GB/s both ways over "
         f"the {r['copy_span_ms']:.1f} ms span")

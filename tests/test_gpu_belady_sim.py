@@ -54,7 +54,11 @@ def test_random_traces_large(dev, seed):
         run_and_compare(dev, trace, n_pages, cap)
 
 
-@pytest.mark.parametrize("layers,shard,cap_layers", [(6, 64, 2.5), (10, 256, 3.7), (3, 16, 0.3)])
+# budgets below one layer (0.3, 0.5, 0.75): most windows of the simulator then have victims
+# among pages they have just seen (the parking path); (3, 2048, 0.75) is bench.py's
+# both-directions tier window: 786,432 accesses, 245,760 evictions
+@pytest.mark.parametrize("layers,shard,cap_layers", [(6, 64, 2.5), (10, 256, 3.7), (3, 16, 0.3), (4, 512, 0.5),
+                                                     (3, 2048, 0.75)])
 def test_ring_schedule_traces(dev, layers, shard, cap_layers):
     ring = 8
     trace = O.ring_trace(layers, ring, shard)

@@ -107,6 +107,7 @@ struct SimShared {
   int32_t blk_before[BS_EMAX];
   int32_t sort_key[BS_EMAX];  // dynamic candidates sorted by idx (key) -> candidate slot
   int32_t sort_val[BS_EMAX];
+  int32_t sort_rel[BS_EMAX];  // per sorted candidate: evictions at or before its time
   unsigned long long win_bits[BS_W / 64 + 2];  // words of B covering the window's positions
   unsigned long long win_clr[BS_W / 64 + 2];   // bits of those words cleared in this window
   int scan_ws[BS_THREADS / 64 + 1];
@@ -141,6 +142,88 @@ __device__ void sort_candidates(SimShared &sh, int n) {
       }
       __syncthreads();
     }
+}
+
+// Number of entries of the ascending array a[0, n) that are <= x.
+__device__ __forceinline__ int upper_bound(const int32_t *a, int n, int32_t x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] <= x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+__device__ __forceinline__ int32_t lane_of(int32_t v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+__device__ __forceinline__ uint64_t lane_of64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Victims of a window whose dynamic candidates appear between its evictions (wave 0).
+// Eviction k (at window offset ev_t[k]) takes the best (smallest idx) candidate not yet
+// taken: any static, or a dynamic one whose time d_t < ev_t[k].  That online order gives
+// the same victims as parking the candidates in increasing idx order, each at the first
+// free eviction slot it may use (a static: any slot; a dynamic one: slots k with
+// ev_t[k] > d_t): the smallest candidate goes to the first eviction that can see it,
+// and the rest is the same problem without that candidate and that eviction.  So the wave
+// walks the merged idx order of the E statics (sh.s_idx) and the sorted dynamic
+// candidates (sh.sort_key / sort_val / sort_rel) once, with the free slots as a bitmap
+// in registers (lane l < 32: slots [64 l, 64 l + 64)); each candidate costs a ballot,
+// not a scan of the candidates.  Records ev_vidx and ev_dyn per slot, and in ev_vpage the
+// candidate slot (dynamic) or -1 (static: its page is read afterwards).  Returns the
+// number of dynamic victims.
+__device__ int park_victims(SimShared &sh, int E, int nd) {
+  const int lane = threadIdx.x & 63;
+  uint64_t freem = 0;
+  if (lane < 32) {
+    const int lo = lane * 64;
+    freem = lo >= E ? 0ull : (E - lo >= 64 ? ~0ull : ((1ull << (E - lo)) - 1));
+  }
+  int sp = 0, dp = 0, filled = 0, n_dyn = 0;
+  int sbase = -64, dbase = -64;
+  int32_t cs = 0, ck = 0, cv = 0, cr = 0;
+  while (filled < E) {
+    if (sp - sbase >= 64) {
+      sbase = sp;
+      cs = sbase + lane < E ? sh.s_idx[sbase + lane] : 0x7FFFFFFF;
+    }
+    if (dp - dbase >= 64) {
+      dbase = dp;
+      const bool in = dbase + lane < nd;
+      ck = in ? sh.sort_key[dbase + lane] : 0x7FFFFFFF;
+      cv = in ? sh.sort_val[dbase + lane] : -1;
+      cr = in ? sh.sort_rel[dbase + lane] : E;
+    }
+    const int32_t skey = sp < E ? lane_of(cs, sp - sbase) : 0x7FFFFFFF;
+    const int32_t dkey = dp < nd ? lane_of(ck, dp - dbase) : 0x7FFFFFFF;
+    if (skey == 0x7FFFFFFF && dkey == 0x7FFFFFFF) break;  // not reached: E statics fill E slots
+    const bool dyn = dkey < skey;
+    const int rel = dyn ? lane_of(cr, dp - dbase) : 0;
+    const int cand = dyn ? lane_of(cv, dp - dbase) : -1;
+    if (dyn) ++dp;
+    else ++sp;
+    // first free slot >= rel
+    const int lo = lane * 64;
+    uint64_t m = lo >= rel ? freem : ((rel >> 6) == lane ? freem & (~0ull << (rel & 63)) : 0ull);
+    const uint64_t any = __ballot(m != 0ull);
+    if (any == 0ull) continue;  // every slot this candidate may use is taken
+    const int fl = __ffsll((long long)any) - 1;
+    const uint64_t mf = lane_of64(m, fl);
+    const int bit = __ffsll((long long)mf) - 1;
+    const int slot = fl * 64 + bit;
+    if (lane == fl) freem &= ~(1ull << bit);
+    if (lane == 0) {
+      sh.ev_vidx[slot] = dyn ? dkey : skey;
+      sh.ev_vpage[slot] = cand;
+      sh.ev_dyn[slot] = dyn ? 1 : 0;
+    }
+    n_dyn += dyn ? 1 : 0;
+    ++filled;
+  }
+  return n_dyn;
 }
 
 // Number of entries of the ascending array a[0, n) that are < x.
@@ -468,40 +551,29 @@ __global__ void __launch_bounds__(BS_THREADS, 1) belady_sim_kernel(SimArgs a) {
             sh.ev_dyn[rank] = 0;
           }
         }
-      } else if (wid == 0) {  // candidates appear between evictions: one eviction at a time
-        int sp = 0;
-        for (int k = 0; k < E; ++k) {
-          const int tau = sh.ev_t[k];
-          int best = 0x7FFFFFFF, bj = -1;
-          for (int q = lane; q < nd; q += 64)
-            if (!sh.d_taken[q] && sh.d_t[q] < tau && sh.d_idx[q] < best) {
-              best = sh.d_idx[q];
-              bj = q;
-            }
-          for (int off = 32; off >= 1; off >>= 1) {
-            const int ob = __shfl_xor(best, off, 64), oj = __shfl_xor(bj, off, 64);
-            if (ob < best) {
-              best = ob;
-              bj = oj;
-            }
+      } else {  // candidates appear between evictions: park them in idx order (park_victims)
+        for (int q = threadIdx.x; q < nd; q += BS_THREADS) {
+          sh.sort_key[q] = sh.d_idx[q];
+          sh.sort_val[q] = q;
+        }
+        __syncthreads();
+        sort_candidates(sh, nd);
+        for (int q = threadIdx.x; q < nd; q += BS_THREADS) sh.sort_rel[q] = upper_bound(sh.ev_t, E, sh.d_t[sh.sort_val[q]]);
+        __syncthreads();
+        if (wid == 0) {
+          const int n_dyn = park_victims(sh, E, nd);
+          if (lane == 0) sh.n_dyn_victims = n_dyn;
+        }
+        __syncthreads();
+        for (int k = threadIdx.x; k < E; k += BS_THREADS) {
+          if (sh.ev_dyn[k]) {
+            const int q = sh.ev_vpage[k];
+            sh.ev_vpage[k] = sh.d_page[q];
+            sh.d_taken[q] = 1;
+          } else {
+            const int32_t sidx = sh.ev_vidx[k];
+            sh.ev_vpage[k] = sidx < a.n_pages ? sidx : a.trace[top - sidx];
           }
-          const int32_t sidx = sh.s_idx[sp];
-          const bool dyn = bj >= 0 && best < sidx;
-          if (lane == 0) {
-            if (dyn) {
-              sh.ev_vidx[k] = best;
-              sh.ev_vpage[k] = sh.d_page[bj];
-              sh.ev_dyn[k] = 1;
-              sh.d_taken[bj] = 1;
-              ++sh.n_dyn_victims;
-            } else {
-              sh.ev_vidx[k] = sidx;
-              sh.ev_vpage[k] = sidx < a.n_pages ? sidx : a.trace[top - sidx];
-              sh.ev_dyn[k] = 0;
-            }
-          }
-          if (!dyn) ++sp;
-          __builtin_amdgcn_wave_barrier();
         }
       }
       __syncthreads();
