@@ -10,8 +10,8 @@
 //     waits for slab s's scale, encodes slab s and refills that buffer with slab s+5, so
 //     loads stay in flight continuously and no block-wide barrier is ever taken;
 //   * even and odd workgroups take each layer's slabs in two orders that differ at every
-//     step in K/V and in head parity, so the reads and the writes in flight are spread
-//     over both halves of each 4 KiB (see phys_slab);
+//     step in K/V and in the head, so the reads and the writes in flight are spread over
+//     the offsets inside each 4 KiB (see phys_slab);
 //   * a wave's max goes to an LDS slot (ds_max + arrival count); the control wave (the
 //     16th) stores the workgroup's max plus one into its own device-coherent slot of
 //     slab s (slots start at zero), reads all G slots of a slab with one wave-wide load
@@ -114,24 +114,21 @@ __device__ __forceinline__ int64_t vec_src(const FusedArgs &a, int v) {
 // memory system unevenly, and address bit 11 matters most: on MI355X a walk over one
 // 256-byte column of every 4 KiB row reads ~7% slower than one taking column j from half
 // the rows and j ^ 8 (the other 2 KiB half) from the other half.  Both sides of the append
-// have such a bit: in a token row [2][H][D] of bf16, K/V is bit 11 (H = 8, D = 128); in a
-// pool page [2][H][P][D] of codes, the head's parity is bit 11 (P * D = 2 KiB).  So each
-// group of four slabs {K 2g, V 2g, K 2g+1, V 2g+1} of a layer goes as (K 2g, V 2g+1, V 2g,
-// K 2g+1) on even workgroups and as (V 2g+1, K 2g, K 2g+1, V 2g) on odd ones: at every step
-// the two halves of the chip differ in K/V and in head parity, so both the reads and the
-// writes in flight cover both values of bit 11, and every slab is one step apart between
-// the two halves (one step of the exchange's look-ahead).  An odd head count keeps the
-// K/V alternation only.  Sequence index q -> physical slab l * 2H + kv * H + h: the index
-// of scales, exchange slots and pool slabs.
+// have such offsets: a slab (kv, h) sits at kv * 2 KiB + h * 256 B in a token row [2][H][D]
+// of bf16, and at kv * 16 KiB + h * 2 KiB in a pool page [2][H][P][D] of codes (H = 8,
+// D = 128, P = 16).  So each layer's slabs go in pairs (K h, V h ^ m), m = H - 1 for a
+// power-of-two H (else 1), even workgroups taking K h then V h ^ m and odd ones V h ^ m
+// then K h: at every step the two halves of the chip work on slabs whose offsets differ
+// in K/V and in every head bit, on the read side and on the write side, and every slab is
+// one step apart between the halves (one step of the exchange's look-ahead).  An odd head
+// count pairs K h with V h.  Sequence index q -> physical slab l * 2H + kv * H + h: the
+// index of scales, exchange slots and pool slabs.
 __device__ __forceinline__ int phys_slab(const FusedArgs &a, int q) {
   const int two_h = 2 * a.n_heads;
   const int l = q / two_h, r = q - l * two_h;
-  const int odd = (int)(blockIdx.x & 1);
-  if (a.n_heads & 1) return l * two_h + ((r & 1) ^ odd) * a.n_heads + (r >> 1);
-  const int w = r & 3;
-  const int kv = ((w == 1 || w == 2) ? 1 : 0) ^ odd;
-  const int h = (r >> 2) * 2 + ((w & 1) ^ odd);
-  return l * two_h + kv * a.n_heads + h;
+  const int i = r >> 1, kv = (r & 1) ^ (int)(blockIdx.x & 1);
+  const int m = (a.n_heads & 1) ? 0 : ((a.n_heads & (a.n_heads - 1)) == 0 ? a.n_heads - 1 : 1);
+  return l * two_h + kv * a.n_heads + (kv ? (i ^ m) : i);
 }
 
 __device__ __forceinline__ const char *slab_src(const FusedArgs &a, int s, int64_t t_lo) {
