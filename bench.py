@@ -36,7 +36,7 @@ METRIC = "KV quant+append & gather+dequant GB/s (% HBM peak); evictions/sec"
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE and scaled by the same counters on a plain 4 GiB copy (profiles/*.md); keyed by
 # (workload, seed) because the append's size depends on the seed.
-MEASURED_TRAFFIC = {("append", 1): 14_859_108_010, ("gather", 2): 12_889_463_193}
+MEASURED_TRAFFIC = {("append", 1): 14_860_676_704, ("gather", 2): 12_889_463_193}
 TRAFFIC_SOURCE = ("profile figure, not measured in this run: rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 "
                   "per dispatch (profiles/kv_append_fused_configs1.md, profiles/gather_dequant_configs2.md)")
 
