@@ -22,8 +22,9 @@
 //   * candidates are the first E statics (the first E set bits) and the window's
 //     "dynamic" items: a page's last access in the window makes it a candidate from that
 //     time on with key = its next use (beyond t1 or never);
-//   * each eviction takes the best candidate available at its time (one wave scans the
-//     dynamic items, statics are consumed in order).
+//   * each eviction takes the best candidate available at its time: merged by rank when
+//     every dynamic candidate exists before the first eviction, else parked in key order
+//     by one wave (park_victims).
 // When fewer than E statics exist the window is halved (a window of one access always
 // qualifies).  The result equals the sequential algorithm access by access.
 #include "zx_internal.h"
