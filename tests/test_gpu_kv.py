@@ -319,6 +319,8 @@ def test_kv_gather_dequant_nan_codes_and_bad_pages(dev):
     (1, 1, 256, 16, [30000, 20001]),          # share beyond the registers: spill path
     (1, 1, 256, 16, [60000, 41000]),          # share beyond twice the registers: two passes
     (3, 4, 64, 32, [3, 1, 2]),                # fewer tokens than workgroups
+    (2, 3, 128, 16, [700, 45, 1300]),         # odd head count: K h paired with V h
+    (2, 6, 64, 16, [900, 333]),               # even, not a power of two: K h with V h ^ 1
 ])
 def test_kv_quant_append_fused_and_two_pass_bit_exact(dev, two_pass, L, H, D, P, lens):
     x, cu, bt, n_pages, _ = make_append_case(L, H, D, P, lens, seed=L * 1000 + H + D)
