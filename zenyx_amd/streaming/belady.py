@@ -66,6 +66,7 @@ class BeladyApproxCache:
         self._ws: torch.Tensor | None = None
         self._stage = None  # pinned (slot, key, rank) staging arrays and their numpy views
         self._out: torch.Tensor | None = None  # pinned int64 [2]: {slot, key} of the last argmax
+        self._out_np = None  # its numpy view (read without a torch call)
 
     def _reg(self, tensor_id) -> None:
         if tensor_id not in self._rank:
@@ -119,6 +120,7 @@ class BeladyApproxCache:
         self._ws = torch.empty(max(256, lib.zx_belady_argmax_workspace_bytes(cap)), dtype=torch.uint8, device=dev)
         if self._out is None:
             self._out = torch.empty(2, dtype=torch.int64, pin_memory=True)
+            self._out_np = self._out.numpy()
 
     def _flush(self, stream) -> None:
         """Write the dirty slots into the device tables (one launch)."""
@@ -152,7 +154,7 @@ class BeladyApproxCache:
         N.check(lib.zx_belady_argmax(N.ptr(self._keys_dev), None, N.ptr(self._rank_dev), len(self._at),
                                      N.ptr(self._out), N.ptr(self._ws), self._ws.numel(), stream), "belady_argmax")
         cur.synchronize()  # the staging arrays are free again and the result is in pinned memory
-        slot = int(self._out[0])
+        slot = int(self._out_np[0])
         return None if slot < 0 else self._at[slot]
 
     @property
