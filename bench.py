@@ -21,7 +21,7 @@ it; bit-identical to the C oracle), elsewhere the C oracle; each on a bounded sa
 the same workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
-                    [--only append|gather|decode|ring|belady|tiers|weights|configs4|configs4_16gb|configs0|copy|all]
+                    [--only append|gather|decode|ring|belady|tiers|weights|configs4|configs4_16gb|stream|configs0|copy|all]
 """
 from __future__ import annotations
 
@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     ap.add_argument("--only", choices=["append", "gather", "decode", "ring", "belady", "tiers", "weights", "configs4",
-                                       "configs4_16gb",
+                                       "configs4_16gb", "stream",
                                        "configs0", "copy", "all"],
                     default="all")
     ap.add_argument("--seed", type=int, default=1)
@@ -826,14 +826,17 @@ def make_c5_layer(torch, dev, layer, out, seed=5, chunk=65536):
     return out
 
 
-def configs4_setup(torch, dev, timing=False, hbm_layers=None):
+def configs4_setup(torch, dev, timing=False, hbm_layers=None, layers=None, tokens=None):
     """configs[4]'s buffers: block tables (seed 5), the per-layer input, the gather outputs
     and the 80-layer cache streamed through ``hbm_layers`` (default 60) HBM slots and
-    pinned DRAM."""
+    pinned DRAM.  ``layers`` and ``tokens`` (per sequence) override the layer count and
+    the 131,072 tokens of each of the 4 sequences."""
     from zenyx_amd.train.kv_layer_stream import LayerStreamedKVCache
 
     L, H, D, P, B, Tb, S = (C5[k] for k in ("L", "H", "D", "P", "B", "Tb", "hbm_layers"))
     S = hbm_layers or S
+    L = layers or L
+    Tb = tokens or Tb
     T = B * Tb
     n_pages = T // P
     g = torch.Generator().manual_seed(5)
@@ -844,7 +847,7 @@ def configs4_setup(torch, dev, timing=False, hbm_layers=None):
                 kout=torch.empty((B, H, Tb, D), dtype=torch.bfloat16, device=dev),
                 vout=torch.empty((B, H, Tb, D), dtype=torch.bfloat16, device=dev),
                 cache=LayerStreamedKVCache(L, S, n_pages, H, D, P, device=dev, timing=timing),
-                T=T, n_pages=n_pages)
+                T=T, n_pages=n_pages, L=L, Tb=Tb)
 
 
 def configs4_step(torch, dev, c, on_gather=None):
@@ -853,21 +856,21 @@ def configs4_step(torch, dev, c, on_gather=None):
     cache; ``on_gather(l, k, v)`` runs on the compute stream after each gather."""
     cache = c["cache"]
     cache.reset()
-    for l in range(C5["L"]):
+    for l in range(c["L"]):
         make_c5_layer(torch, dev, l, c["x"])
         cache.append_layer(l, c["x"], c["cu"], c["bt"])
-    for l in range(C5["L"] - 1, -1, -1):
-        k, v = cache.gather_layer(l, c["bt"], c["sl"], C5["Tb"], out=(c["kout"], c["vout"]))
+    for l in range(c["L"] - 1, -1, -1):
+        k, v = cache.gather_layer(l, c["bt"], c["sl"], c["Tb"], out=(c["kout"], c["vout"]))
         if on_gather is not None:
             on_gather(l, k, v)
 
 
-def configs4_leg(torch, dev, hbm_layers=None):
+def configs4_leg(torch, dev, hbm_layers=None, tokens=None):
     """70B-shape share, 80 layers x (4 x 128k tokens), streamed through 60 HBM
     layer slots and pinned DRAM (zenyx_amd.train.kv_layer_stream.LayerStreamedKVCache).
-    With ``hbm_layers`` = 15 the same step runs through 16 GB of slots (README.md:154:
-    "Streams 516 GB KV cache through 16 GB HBM"): 65 of the 80 layers go out and come
-    back, PCIe sets the pace and the step's wall time is compared with the copies alone.
+    ``hbm_layers`` and ``tokens`` (per sequence) change the slot count and the layer size:
+    with few slots most layers go out and come back, PCIe sets the pace and the step's wall
+    time is to be compared with the copies alone.
     Forward: each layer's KV is generated, appended (dynamic per-head FP8) into its slot;
     layers 0-19 (the Belady victims of the backward sweep) are written back to pinned host
     memory on a side stream right after their own append, and layer l >= 60 reuses layer
@@ -877,13 +880,14 @@ def configs4_leg(torch, dev, hbm_layers=None):
     on the compute stream; tier moves from events on the side stream."""
     L, H, D, P, B, Tb, S = (C5[k] for k in ("L", "H", "D", "P", "B", "Tb", "hbm_layers"))
     S = hbm_layers or S
-    c = configs4_setup(torch, dev, timing=True, hbm_layers=S)
+    Tb = tokens or Tb
+    c = configs4_setup(torch, dev, timing=True, hbm_layers=S, tokens=Tb)
     T, n_pages, cache = c["T"], c["n_pages"], c["cache"]
     N = T * 2 * H * D
     alg_append = 3 * N + 4 * 2 * H + 4 * n_pages + 4 * (B + 1)
     alg_gather = 3 * N + 4 * n_pages + 4 * 2 * H + 4 * B
 
-    log("configs[4]: warm-up step (80 layers forward + backward)")
+    log(f"configs[4]: {S} HBM slots, 4 x {Tb} tokens; warm-up step (80 layers forward + backward)")
     configs4_step(torch, dev, c)
     torch.cuda.synchronize(dev)
     cache.check_errors()
@@ -894,16 +898,21 @@ def configs4_leg(torch, dev, hbm_layers=None):
     wall = time.perf_counter() - t0
     ms = lambda evs: [a.elapsed_time(b) for a, b in evs]  # noqa: E731
     app_ms, gat_ms = ms(cache.events["append"]), ms(cache.events["gather"])
+    # the library's choice: one pass when a CU's share of a slab (16-byte vectors) is between
+    # half and twice the 5 x 960 its registers hold and the call has >= 32 slabs
+    share = -(-T // torch.cuda.get_device_properties(dev).multi_processor_count) * (D // 8)
+    append_path = ("two-pass (one layer, 16 slabs per call)" if 2 * H < 32 else
+                   "single pass" if 2 * share >= 5 * 960 and share <= 2 * 5 * 960 else "two-pass")
     d2h_ms, h2d_ms = ms(cache.events["d2h"]), ms(cache.events["h2d"])
     a_gbps = L * alg_append / (sum(app_ms) * 1e-3) / 1e9
     g_gbps = L * alg_gather / (sum(gat_ms) * 1e-3) / 1e9
     moved = (L - S) * cache.layer_bytes
     med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
-    out = {"workload": "configs[4]: 80 layers, 8 KV heads, D=128, 4 x 131072 tokens, Student-t(3) KV x "
+    out = {"workload": f"configs[4]: 80 layers, 8 KV heads, D=128, 4 x {Tb} tokens, Student-t(3) KV x "
                        f"per-channel 10**U(-2,2); {S} layer slots in HBM ({S * cache.layer_bytes / 1e9:.1f} GB), "
                        f"{L - S} layers spilled to pinned DRAM ({L * cache.layer_bytes / 1e9:.1f} GB of FP8 KV in all)",
            "append_GBps": round(a_gbps, 2), "append_frac": round(a_gbps / HBM_PEAK_GBPS, 4),
-           "append_ms_per_layer": round(sum(app_ms) / L, 4), "append_path": "two-pass (share > 2x registers)",
+           "append_ms_per_layer": round(sum(app_ms) / L, 4), "append_path": append_path,
            "gather_GBps": round(g_gbps, 2), "gather_frac": round(g_gbps / HBM_PEAK_GBPS, 4),
            "gather_ms_per_layer": round(sum(gat_ms) / L, 4),
            "append_ms_median": round(med(app_ms), 4), "append_ms_min": round(min(app_ms), 4),
@@ -913,6 +922,7 @@ def configs4_leg(torch, dev, hbm_layers=None):
            "tier_bytes_each_way": moved, "step_wall_s": round(wall, 3),
            "copies_only_s": round((sum(d2h_ms) + sum(h2d_ms)) * 1e-3, 3),
            "hbm_slot_bytes": S * cache.layer_bytes, "cache_bytes": L * cache.layer_bytes,
+           "streaming_ratio": round(L / S, 2), "kernels_s": round((sum(app_ms) + sum(gat_ms)) * 1e-3, 4),
            "note": "KV generation (Student-t sampling) runs inside the step and is not in the kernel times"}
     log(f"configs[4]: append {a_gbps:.1f} GB/s ({100 * a_gbps / HBM_PEAK_GBPS:.1f}%), gather {g_gbps:.1f} GB/s "
         f"({100 * g_gbps / HBM_PEAK_GBPS:.1f}%), D2H {out['d2h_GBps']} GB/s, H2D {out['h2d_GBps']} GB/s, "
@@ -1165,6 +1175,11 @@ def main():
         # been shown; configs4_leg(torch, dev, hbm_layers=15) is the code it ran.
         raise SystemExit("configs4_16gb is switched off: its first run crashed (segmentation fault) and the cause "
                          "is not known")
+    if args.only == "stream":
+        # configs[4]'s 80-layer step at a streaming ratio of 40:1 (README.md:154 claims 32:1):
+        # layers of 4 x 32,768 tokens (268 MB), 2 HBM slots, 78 layers through pinned DRAM
+        # (21 GB, the pinned footprint of the 60-slot configs[4] leg)
+        out["stream"] = configs4_leg(torch, dev, hbm_layers=2, tokens=32768)
     if args.only == "configs4":
         out["configs4"] = configs4_leg(torch, dev)
     elif args.only == "all":
@@ -1185,6 +1200,11 @@ def main():
     if args.only == "configs4_16gb" and "value" not in out:
         c = out["configs4_16gb"]
         out.update({"value": c["append_GBps"], "ms_per_step": round(1e3 * c["step_wall_s"], 3),
+                    "config": {"workload": c["workload"]}})
+    if args.only == "stream" and "value" not in out:
+        c = out["stream"]
+        out.update({"value": round(2 * c["tier_bytes_each_way"] / c["step_wall_s"] / 1e9, 2),
+                    "unit": "GB/s through PCIe (both ways, whole step)", "ms_per_step": round(1e3 * c["step_wall_s"], 3),
                     "config": {"workload": c["workload"]}})
     if args.only in ("configs4", "all"):
         if "value" not in out:

@@ -154,11 +154,14 @@ size_t zx_kv_quant_append_workspace_bytes(int32_t n_layers, int64_t n_tok, int32
                                      finite are unaffected */
 #define ZX_APPEND_TWO_PASS 2      /* flag: compute dynamic scales in a separate amax pass
                                      instead of the single-pass cooperative kernel (same
-                                     results).  Without the flag the library picks: one
-                                     pass while a CU's share of a (layer, kv, head) slab
-                                     fits about twice its registers (~150k tokens at
-                                     D = 128 on MI355X), two passes beyond that or on
-                                     devices without cooperative launch. */
+                                     results).  Without this flag or ZX_APPEND_SINGLE_PASS
+                                     the library picks: one pass while a CU's share of a
+                                     (layer, kv, head) slab is between half and twice what
+                                     its registers hold (~38k-150k tokens at D = 128 on
+                                     MI355X) and the call has at least 32 slabs, two passes
+                                     otherwise and on devices without cooperative launch */
+#define ZX_APPEND_SINGLE_PASS 8   /* flag: the single pass whatever the size (where the
+                                     device can co-schedule it; same results) */
 
 /* Paged append with fused FP8 quantisation.  Without
  * ZX_APPEND_STATIC_SCALES the scales are computed from this batch (amax over all

@@ -132,6 +132,10 @@ def test_exclusive_flags_are_refused_before_any_device_call():
     assert rc == N.ZX_ERR_INVALID and b"together" in lib.zx_last_error()
     rc = lib.zx_fp8_quant_heads(p, 1, 1, 1, 16, p, p, 64, None, None, 0, None)
     assert rc == N.ZX_ERR_INVALID and b"unknown flag" in lib.zx_last_error()
+    for fl, msg in ((N.ZX_APPEND_TWO_PASS | N.ZX_APPEND_SINGLE_PASS, b"together"), (64, b"unknown flag")):
+        rc = lib.zx_kv_quant_append(p, 16 * 2 * 8 * 128, 1, 16, 8, 128, p, None, 1, p, 1, 16, p, 2 * 8 * 16 * 128, 1,
+                                    p, fl, None, None, 0, None)
+        assert rc == N.ZX_ERR_INVALID and msg in lib.zx_last_error()
     for fn, extra in ((lib.zx_paged_attention_prefill, ()), (lib.zx_paged_attention_ring, (1,))):
         args = [p, 16, p, p, 8, p, 10, 2, 128, 16, p, p, 4] + [p, p] + list(extra) + [1, 16, 1, 0.1]
         rc = fn(*args, N.ZX_PREFILL_BF16 | N.ZX_PREFILL_FAST_P | N.ZX_PREFILL_EXACT_P, None, None, p, None, None)

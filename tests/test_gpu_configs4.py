@@ -165,3 +165,40 @@ def test_configs4_streamed_step(dev):
         print(f"layer {layer} ({where}): scales and {S} gathered rows bit-exact", flush=True)
     del c, cache, x, got, got_whole
     torch.cuda.empty_cache()
+
+
+def test_streamed_step_through_two_slots(dev):
+    """The streamed cache at a high streaming ratio: 12 layers through 2 HBM layer slots
+    (10 of 12 layers written back to pinned DRAM and prefetched back; 6:1), small layers
+    (4 x 2,048 tokens), two sweeps on the same buffers.  Every gathered K and V value of
+    every layer in both sweeps bit-exact against the oracle's torch restatement of the
+    append followed by its gather, and every scale against fp32(max(amax, 1e-8) / 448)."""
+    L, S, Tb = 12, 2, 2048
+    C = bench.C5
+    H, D, P, B = C["H"], C["D"], C["P"], C["B"]
+    c = bench.configs4_setup(torch, dev, hbm_layers=S, layers=L, tokens=Tb)
+    cache = c["cache"]
+    assert cache.n_spill == L - S and cache.S == S
+    seq_tables = np.arange(B * Tb // P, dtype=np.int32).reshape(B, Tb // P)
+    cu = np.arange(0, B * Tb + 1, Tb, dtype=np.int32)
+    want = {}
+    x = c["x"]
+    for layer in range(L):
+        bench.make_c5_layer(torch, dev, layer, x)
+        wsc, wpool = O.kv_quant_append_torch(x.cpu(), cu, seq_tables, B * Tb // P, P)
+        wk, wv = O.kv_gather_dequant_torch(wpool, wsc, seq_tables, np.full(B, Tb, np.int32), Tb)
+        want[layer] = (wsc.numpy(), wk.view(torch.int16), wv.view(torch.int16))
+    for sweep in range(2):
+        got = {}
+        bench.configs4_step(torch, dev, c, lambda l, k, v: got.__setitem__(l, (k.cpu(), v.cpu())))
+        torch.cuda.synchronize()
+        cache.check_errors()
+        scales = cache.scales.cpu().numpy()
+        for layer in range(L):
+            np.testing.assert_array_equal(scales[layer].view(np.uint32), want[layer][0].view(np.uint32))
+            for name, g_, w_ in (("K", got[layer][0], want[layer][1]), ("V", got[layer][1], want[layer][2])):
+                gi = g_.view(torch.int16)
+                assert torch.equal(gi, w_), f"sweep {sweep} layer {layer} {name}: {(gi != w_).sum().item()} differ"
+        print(f"sweep {sweep}: all {L} layers bit-exact through {S} slots", flush=True)
+    del c, cache
+    torch.cuda.empty_cache()

@@ -216,7 +216,8 @@ def test_kv_quant_append_every_input_below_amax(dev, two_pass):
     assert werr == 0 and sum(lens) == T
     xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
     pool_d = pool.to(dev)
-    sc = kv.kv_quant_append(xt.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass)
+    sc = kv.kv_quant_append(xt.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass,
+                            single_pass=not two_pass)
     np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
     np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
     # and back: every e4m3 code (-0 included) through the paged gather + dequant
@@ -329,7 +330,8 @@ def test_kv_quant_append_fused_and_two_pass_bit_exact(dev, two_pass, L, H, D, P,
     wsc, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, P)
     assert werr == 0
     pool_d = pool.to(dev)
-    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass)
+    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass,
+                            single_pass=not two_pass)
     np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
     np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
 
@@ -354,7 +356,8 @@ def test_kv_quant_append_special_slabs(dev, two_pass):
     assert werr == 0
     assert np.isinf(wsc[1, 1, 1]) and np.isnan(wsc[2, 0, 2])
     pool_d = pool.to(dev)
-    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass)
+    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, two_pass=two_pass,
+                            single_pass=not two_pass)
     np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
     np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)
 
@@ -395,7 +398,8 @@ def test_kv_quant_append_pool_layer_over_2gib(dev, two_pass):
     wsc, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt_small.numpy(), wpool, P)
     assert werr == 0
     pool_d = torch.zeros((L, n_big, 2, H, P, D), dtype=torch.uint8, device=dev)
-    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt_big.to(dev), pool_d, check=True, two_pass=two_pass)
+    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt_big.to(dev), pool_d, check=True, two_pass=two_pass,
+                            single_pass=not two_pass)
     np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
     got = pool_d[:, big_ids.long().to(dev)].cpu().numpy()
     np.testing.assert_array_equal(got, wpool)
@@ -413,6 +417,6 @@ def test_kv_quant_append_repeated_calls_reset_state(dev):
         wpool = pool.numpy().copy()
         wsc, _ = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), wpool, 16)
         pool_d = pool.to(dev)
-        sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True)
+        sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool_d, check=True, single_pass=True)
         np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
         np.testing.assert_array_equal(pool_d.cpu().numpy(), wpool)

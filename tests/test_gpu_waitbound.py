@@ -51,17 +51,17 @@ def test_fused_append_wait_gives_up_then_recovers(dev, zero_wait_bound):
     x, cu, bt, pshape = _append_case(dev)
     pool = torch.zeros(pshape, dtype=torch.uint8, device=dev)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
-    kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool, err=err)
+    kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool, err=err, single_pass=True)
     torch.cuda.synchronize()
     assert int(err.item()) & N.ZX_KERR_SPIN, "a zero wait bound must make the single pass give up"
     with pytest.raises(ValueError, match="wait"):
-        kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool, check=True)
+        kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool, check=True, single_pass=True)
     kv.set_wait_bound_us(None)
     want = np.zeros(pshape, np.uint8)
     wsc, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, bt.numpy(), want, pshape[4])
     assert werr == 0
     pool.zero_()
-    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool, check=True)
+    sc = kv.kv_quant_append(x.to(dev), cu.to(dev), bt.to(dev), pool, check=True, single_pass=True)
     np.testing.assert_array_equal(sc.cpu().numpy().view(np.uint32), wsc.view(np.uint32))
     np.testing.assert_array_equal(pool.cpu().numpy(), want)
 
@@ -103,18 +103,18 @@ def test_paged_cache_raises_and_rolls_back_an_aborted_append(dev, zero_wait_boun
     cache = PagedFP8KVCache(L, H, D, num_pages=pshape[1] + 8, page_size=P, device=dev)
     free_before = list(cache._free)
     with pytest.raises(ValueError, match="wait"):
-        cache.append(x, ["a", "b", "c"], lens, check=True)
+        cache.append(x, ["a", "b", "c"], lens, check=True, single_pass=True)
     assert cache.lengths == {} and cache.pages == {} and sorted(cache._free) == sorted(free_before)
     assert not cache.has_scales
     # unchecked: the error surfaces at the next check
-    cache.append(x, ["a", "b", "c"], lens)
+    cache.append(x, ["a", "b", "c"], lens, single_pass=True)
     with pytest.raises(ValueError, match="wait"):
         cache.check_errors()
     cache.check_errors()  # the words were cleared by the raise
     for s in ("a", "b", "c"):
         cache.free(s)
     kv.set_wait_bound_us(None)
-    cache.append(x, ["a", "b", "c"], lens, dynamic_scales=True, check=True)
+    cache.append(x, ["a", "b", "c"], lens, dynamic_scales=True, check=True, single_pass=True)
     tables = cache._tables(["a", "b", "c"]).cpu().numpy()
     want = np.zeros(tuple(cache.pool.shape), np.uint8)
     wsc, werr = O.kv_quant_append(bits16(x), cu.numpy(), None, tables, want, P)

@@ -52,8 +52,9 @@ def test_noalloc_append_equals_workspace_append(dev, static):
         sc_b = sc_a.clone()
         err_a = torch.zeros(1, dtype=torch.int32, device=dev)
         err_b = torch.zeros(1, dtype=torch.int32, device=dev)
-        kv.kv_quant_append(x, cu, bt, pool_a, scales=sc_a, static_scales=static, err=err_a)
-        flags = N.ZX_APPEND_STATIC_SCALES if static else 0
+        # dynamic scales: the cooperative single pass, whose exchange slots live in the scratch
+        kv.kv_quant_append(x, cu, bt, pool_a, scales=sc_a, static_scales=static, err=err_a, single_pass=not static)
+        flags = N.ZX_APPEND_STATIC_SCALES if static else N.ZX_APPEND_SINGLE_PASS
         N.check(_noalloc(x, cu, bt, pool_b, sc_b, flags, err_b), "kv_quant_append_noalloc")
         torch.cuda.synchronize(dev)
         assert torch.equal(sc_a.view(torch.int32), sc_b.view(torch.int32)), f"call {call}: scales differ"
@@ -90,14 +91,16 @@ def test_noalloc_append_in_a_captured_graph(dev, mode):
     L, H, D, P = 3, 8, 128, 16
     x, cu, bt, n_pages = _case(L, H, D, P, [700, 33, 1500, 1], seed=5, dev=dev)
     static = mode == "static"
-    flags = {"single_pass": 0, "two_pass": N.ZX_APPEND_TWO_PASS, "static": N.ZX_APPEND_STATIC_SCALES}[mode]
+    flags = {"single_pass": N.ZX_APPEND_SINGLE_PASS, "two_pass": N.ZX_APPEND_TWO_PASS,
+             "static": N.ZX_APPEND_STATIC_SCALES}[mode]
     pool_e = torch.zeros((L, n_pages, 2, H, P, D), dtype=torch.uint8, device=dev)
     if static:
         sc_e = torch.rand((L, 2, H), generator=torch.Generator().manual_seed(1)).to(dev) * 0.01 + 0.002
     else:
         sc_e = torch.empty((L, 2, H), dtype=torch.float32, device=dev)
     err_e = torch.zeros(1, dtype=torch.int32, device=dev)
-    kv.kv_quant_append(x, cu, bt, pool_e, scales=sc_e, static_scales=static, two_pass=mode == "two_pass", err=err_e)
+    kv.kv_quant_append(x, cu, bt, pool_e, scales=sc_e, static_scales=static, two_pass=mode == "two_pass",
+                       single_pass=mode == "single_pass", err=err_e)
     pool_g = torch.zeros_like(pool_e)
     sc_g = sc_e.clone()
     err_g = torch.zeros(1, dtype=torch.int32, device=dev)

@@ -419,8 +419,18 @@ static int fused_supported() {
   return ZX_OK;
 }
 
-bool append_fused_preferred(int64_t n_tok, int32_t head_dim) {
-  return ceil_div(n_tok, num_cus()) * (head_dim / 8) <= 2LL * FA_K * FA_DATA_THREADS;
+// The single pass pays a device-wide exchange per slab (~3.6 us on MI355X whatever the
+// slab's size) and fills its pipeline over the first slabs; two passes move 5 B per
+// element against 3 but no exchange, and below the Infinity Cache's size their second
+// read comes from it.  Measured whole calls (MI355X, D = 128, H = 8), single / two passes:
+// 74,752 tokens x 1 layer 0.147 / 0.128 ms, x 2 layers 0.230 / 0.259, x 16 1.430 / 2.106;
+// 32,768 tokens (share = 43% of the registers) x 16 layers 0.917 / 0.890; 131,072 tokens
+// (share = 1.7x the registers, tail re-read) x 1 layer 0.228 / 0.217, x 4 0.890 / 0.914.
+// So: a share between half and twice what the registers hold, and at least 32 slabs.
+bool append_fused_preferred(int64_t n_tok, int32_t head_dim, int64_t n_slabs) {
+  const int64_t share = ceil_div(n_tok, num_cus()) * (head_dim / 8);
+  const int64_t regs = (int64_t)FA_K * FA_DATA_THREADS;
+  return 2 * share >= regs && share <= 2 * regs && n_slabs >= 32;
 }
 
 // workspace: abort flag (+ 60 B pad) | dummy store slots (128 B) | slots [S][G]

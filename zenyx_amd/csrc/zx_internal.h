@@ -12,11 +12,11 @@ int fill_u32(uint32_t *p, int64_t n, uint32_t v, hipStream_t st);
 
 // Single-pass paged append with dynamic scales (zx_append_fused.hip).  Returns
 // ZX_ERR_UNSUPPORTED when the device cannot run it (the caller then uses two passes).
-// append_fused_preferred: whether a workgroup's share of a slab is small enough for the
-// single pass to beat two passes (up to twice what its registers hold: beyond that the
-// re-read part costs more than the second pass does; MI355X, 60k-300k tokens).
+// append_fused_preferred: whether the single pass beats two passes for this call (a
+// workgroup's share of a slab between half and twice what its registers hold, and enough
+// slabs to fill its pipeline; measured on MI355X).
 size_t append_fused_workspace_bytes(int32_t n_layers, int32_t n_heads);
-bool append_fused_preferred(int64_t n_tok, int32_t head_dim);
+bool append_fused_preferred(int64_t n_tok, int32_t head_dim, int64_t n_slabs);
 int append_fused(const uint16_t *x, int64_t x_layer_stride, int32_t n_layers, int64_t n_tok, int32_t n_heads,
                  int32_t head_dim, const int64_t *tok_off, uint8_t *pool, int64_t pool_layer_stride,
                  int32_t page_size, float *scales, int32_t *err, void *ws, hipStream_t st);

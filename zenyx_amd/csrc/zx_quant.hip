@@ -956,6 +956,10 @@ int kv_quant_append_impl(const uint16_t *x, int64_t x_layer_stride, int32_t n_la
                          const int32_t *block_tables, int32_t max_blocks, int32_t page_size, uint8_t *pool,
                          int64_t pool_layer_stride, int64_t n_pages, float *scales, int32_t flags, int32_t *err,
                          void *workspace, size_t workspace_bytes, hipStream_t st) {
+  ZX_REQUIRE(!(flags & ~(ZX_APPEND_STATIC_SCALES | ZX_APPEND_TWO_PASS | ZX_APPEND_SATURATE | ZX_APPEND_SINGLE_PASS)),
+             "kv_quant_append: unknown flag bits 0x%x", (unsigned)flags);
+  ZX_REQUIRE((flags & (ZX_APPEND_TWO_PASS | ZX_APPEND_SINGLE_PASS)) != (ZX_APPEND_TWO_PASS | ZX_APPEND_SINGLE_PASS),
+             "kv_quant_append: ZX_APPEND_TWO_PASS and ZX_APPEND_SINGLE_PASS together");
   ZX_REQUIRE(scales && cu_seqlens && block_tables && pool, "kv_quant_append: null pointer");
   ZX_REQUIRE(x || n_tok == 0, "kv_quant_append: null x");
   ZX_REQUIRE(n_layers > 0 && n_layers <= 65535, "kv_quant_append: n_layers out of range");
@@ -973,8 +977,6 @@ int kv_quant_append_impl(const uint16_t *x, int64_t x_layer_stride, int32_t n_la
   size_t need = zx_kv_quant_append_workspace_bytes(n_layers, n_tok, n_heads, head_dim);
   if (!workspace || workspace_bytes < need)
     return fail(ZX_ERR_WORKSPACE, "kv_quant_append: workspace %zu < %zu bytes", workspace_bytes, need);
-  ZX_REQUIRE(!(flags & ~(ZX_APPEND_STATIC_SCALES | ZX_APPEND_TWO_PASS | ZX_APPEND_SATURATE)),
-             "kv_quant_append: unknown flag bits 0x%x", (unsigned)flags);
   const bool dynamic = !(flags & ZX_APPEND_STATIC_SCALES);
   if (n_tok == 0) return dynamic ? kv_scales_impl(x, g, n_layers, scales, nullptr, st) : ZX_OK;
   int64_t *tok_off = reinterpret_cast<int64_t *>(workspace);
@@ -982,7 +984,8 @@ int kv_quant_append_impl(const uint16_t *x, int64_t x_layer_stride, int32_t n_la
       cu_seqlens, start_pos, n_seqs, block_tables, max_blocks, page_size, n_pages, page_bytes, head_dim,
       n_tok, tok_off, err);
   if ((rc = check_launch("kv_token_offsets"))) return rc;
-  if (dynamic && !(flags & ZX_APPEND_TWO_PASS) && append_fused_preferred(n_tok, head_dim)) {
+  if (dynamic && !(flags & ZX_APPEND_TWO_PASS) &&
+      ((flags & ZX_APPEND_SINGLE_PASS) || append_fused_preferred(n_tok, head_dim, (int64_t)n_layers * 2 * n_heads))) {
     void *fws = static_cast<char *>(workspace) + align256((size_t)n_tok * sizeof(int64_t));
     rc = append_fused(x, x_layer_stride, n_layers, n_tok, n_heads, head_dim, tok_off, pool, pool_layer_stride,
                       page_size, scales, err, fws, st);

@@ -236,7 +236,7 @@ def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: tor
                     pool: torch.Tensor, scales: torch.Tensor | None = None,
                     start_pos: torch.Tensor | None = None, static_scales: bool = False,
                     check: bool = False, two_pass: bool = False, saturate: bool = False,
-                    err: torch.Tensor | None = None) -> torch.Tensor:
+                    err: torch.Tensor | None = None, single_pass: bool = False) -> torch.Tensor:
     """Paged append with fused FP8 quantisation.
 
     x ``[L, n_tok, 2, H, D]`` bf16; cu_seqlens int32 ``[B+1]``; block_tables int32
@@ -245,7 +245,9 @@ def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: tor
     ``scales`` (allocated if None); returns the scales ``[L, 2, H]``.  With static scales a
     token beyond 464 x its scale is stored as the NaN code and flags an overflow, or as
     +-448 with ``saturate``.  ``err`` (device int32 ``[1]``) collects the kernels' error
-    bits across calls (a fresh word by default); ``check`` reads it and raises.
+    bits across calls (a fresh word by default); ``check`` reads it and raises.  Dynamic
+    scales take one cooperative pass or two passes, whichever the library expects to be
+    faster for the call's size; ``two_pass`` / ``single_pass`` force either (same results).
     """
     N.ensure_gpu()
     x = _layers(x)
@@ -275,6 +277,8 @@ def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: tor
         N.require_device(t, name)
     if saturate and not static_scales:
         raise ValueError("saturate applies to static scales (dynamic scales never overflow)")
+    if two_pass and single_pass:
+        raise ValueError("kv_quant_append: two_pass and single_pass are exclusive")
     lib = N.load()
     ws = _workspace(lib.zx_kv_quant_append_workspace_bytes(L, T, H, D), x.device)
     if err is None:
@@ -282,7 +286,7 @@ def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: tor
     elif err.dtype != torch.int32 or err.numel() < 1 or err.device != x.device:
         raise ValueError("err must be an int32 tensor on x's device")
     flags = (N.ZX_APPEND_STATIC_SCALES if static_scales else 0) | (N.ZX_APPEND_TWO_PASS if two_pass else 0) | \
-        (N.ZX_APPEND_SATURATE if saturate else 0)
+        (N.ZX_APPEND_SATURATE if saturate else 0) | (N.ZX_APPEND_SINGLE_PASS if single_pass else 0)
     N.check(lib.zx_kv_quant_append(N.ptr(x), T * 2 * H * D, L, T, H, D, N.ptr(cu_seqlens), N.ptr(start_pos),
                                    block_tables.shape[0], N.ptr(block_tables), block_tables.shape[1], P,
                                    N.ptr(pool), pool[0].numel(), n_pages, N.ptr(scales), flags, N.ptr(err),

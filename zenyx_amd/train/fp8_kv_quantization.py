@@ -212,13 +212,14 @@ class PagedFP8KVCache:
     # ---------------------------------------------------------------- API
 
     def append(self, x: torch.Tensor, seq_ids: list, lengths: list[int], dynamic_scales: bool | None = None,
-               check: bool = False):
+               check: bool = False, single_pass: bool = False):
         """Append new tokens of several sequences.  x: ``[L, n_tok, 2, H, D]`` bf16, tokens of
         sequence ``seq_ids[i]`` packed in order with ``lengths[i]`` tokens each.  Scales are
         computed from this batch on the first append and reused afterwards (static); asking
         for dynamic scales once pages hold tokens is refused, since it would change the
         scale of pages already written.  ``check`` synchronises and raises on any kernel
-        error bit (see ``check_errors``)."""
+        error bit (see ``check_errors``).  ``single_pass`` makes dynamic scales take the
+        cooperative single pass whatever the batch's size (kv.kv_quant_append)."""
         if len(lengths) != len(seq_ids) or len(set(seq_ids)) != len(seq_ids):
             raise ValueError("seq_ids must be distinct, one per entry of lengths")
         if sum(lengths) != x.shape[1]:
@@ -244,7 +245,7 @@ class PagedFP8KVCache:
             kv.kv_quant_append(x.to(self.device), cu, self._tables(seq_ids), self.pool, scales=self.scales,
                                start_pos=self._len.index_select(0, rows),
                                static_scales=not dyn, saturate=(not dyn) and self.overflow == "saturate",
-                               err=word)
+                               err=word, single_pass=single_pass and dyn)
         except BaseException:
             self._release(taken)
             raise
