@@ -1180,6 +1180,14 @@ def main():
         # layers of 4 x 32,768 tokens (268 MB), 2 HBM slots, 78 layers through pinned DRAM
         # (21 GB, the pinned footprint of the 60-slot configs[4] leg)
         out["stream"] = configs4_leg(torch, dev, hbm_layers=2, tokens=32768)
+    elif args.only == "all":
+        import subprocess  # a child process, like configs[4]: 21 GB of pinned memory
+
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", "stream", "--skip-cpu"],
+                           stdout=subprocess.PIPE, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"streaming leg failed with exit code {r.returncode}")
+        out["stream"] = json.loads(r.stdout.strip().splitlines()[-1])["stream"]
     if args.only == "configs4":
         out["configs4"] = configs4_leg(torch, dev)
     elif args.only == "all":
