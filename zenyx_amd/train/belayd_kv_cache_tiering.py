@@ -16,7 +16,6 @@ module, so its behaviour is defined here:
 """
 from __future__ import annotations
 
-import ctypes
 import math
 import time
 
