@@ -122,16 +122,29 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, kg = lane >> 4;
-  const int64_t q_lo = a.cu_q[b];
-  const int n_qb = a.cu_q[b + 1] - a.cu_q[b];
+  const int grp = a.n_q_heads / a.n_kv_heads;
+  const int hq = hg * G + wave % G;
+  const int h = (hg * G) / grp;  // the block's KV head (G divides grp: its G query heads share it)
+  // What the set-up reads that depends only on the (sequence, head group) is loaded in one
+  // round trip: the sequence's queries, its first key range and the head's scales.  Every
+  // dependent round trip of a block's set-up or final merge is a wait of that block, and
+  // they count where blocks are short: a ring step of 1,024 keys per launch (one launch per
+  // step, as a multi-GPU ring runs) took 7% less time per ring with the set-up below (the
+  // pages of the first two steps and Q read together, then the first K/V and the block
+  // table check) and the running output read in one go at the end.
+  const int32_t cq0 = a.cu_q[b], cq1 = a.cu_q[b + 1], qp0_32 = a.q_pos0[b];
+  const int32_t kb0 = a.kv_begin[b], ke0 = a.kv_end[b];
+  const float sk = a.scales[h], sv = a.scales[a.n_kv_heads + h];
+  // (the empty asm takes every value as an operand, so the compiler issues the loads
+  // together here instead of sinking each one to its first use past a branch)
+  asm volatile("" ::"s"(cq0), "s"(cq1), "s"(qp0_32), "s"(kb0), "s"(ke0), "s"(sk), "s"(sv));
+  const int64_t qp0 = qp0_32;
+  const int64_t q_lo = cq0;
+  const int n_qb = cq1 - cq0;
   const int64_t row0_64 = ((int64_t)a.n_qt - 1 - qt_rev) * QT;
   if (row0_64 >= n_qb) return;
   const int row0_blk = (int)row0_64;
-  const int grp = a.n_q_heads / a.n_kv_heads;
-  const int hq = hg * G + wave % G;
-  const int h = hq / grp;
   const int wrow0 = row0_blk + 32 * (wave / G);  // this wave's first row (in the sequence)
-  const int64_t qp0 = a.q_pos0[b];
   const int64_t page_bytes = 2LL * a.n_kv_heads * a.page_size * D;
   const int64_t head_off = (int64_t)h * a.page_size * D;
   const int64_t v_off = (int64_t)a.n_kv_heads * a.page_size * D;
@@ -151,8 +164,9 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   auto range = [&](int r) -> Range {
     Range g;
     const int64_t i = (int64_t)r * a.n_seqs + b;
-    g.kb = a.kv_begin[i] > 0 ? a.kv_begin[i] : 0;
-    g.ke = a.kv_end[i];
+    const int32_t kbr = r == 0 ? kb0 : a.kv_begin[i];
+    g.kb = kbr > 0 ? kbr : 0;
+    g.ke = r == 0 ? ke0 : a.kv_end[i];
     if (g.ke > kmax) {
       e |= ZX_KERR_POS_RANGE;
       g.ke = kmax;
@@ -182,38 +196,16 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   __shared__ __attribute__((aligned(16))) uint8_t vtl[2][PF_VBYTES];
 
   // every page the block may load inside the pool? (then the steps skip the per-tile
-  // block-table checks; otherwise tiles on bad pages count as masked)
-  bool bad = false;
-  for (int r = 0; r < a.n_ranges; ++r) {
-    const Range g = range(r);
-    if (g.s_first >= g.ke) continue;
-    const int p_lo = (int)pf_page_of(a, (uint32_t)g.s_first), p_hi = (int)pf_page_of(a, (uint32_t)(g.ke - 1));
-    for (int pi = p_lo + (int)threadIdx.x; pi <= p_hi; pi += PF_THREADS) {
-      const int64_t pg = bt[pi];
-      bad |= pg < 0 || pg >= a.n_pages;
-    }
-  }
-  const bool all_ok = !__syncthreads_or(bad);
+  // block-table checks; otherwise tiles on bad pages count as masked).  Found below, once
+  // the first step's loads are in flight.
+  bool all_ok = false;
 
   // Q rows as the B operand of S^T = K . Q^T: lane (n, kg) of row tile rt holds row
-  // wrow0 + 16 rt + n, channels 32 kg + 8 c ..+8 for MFMA c (the K operand's channel order)
+  // wrow0 + 16 rt + n, channels 32 kg + 8 c ..+8 for MFMA c (the K operand's channel order);
+  // loaded below, after the first step's page lookup
   att_bf16x8 qa[2][4];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int r = wrow0 + 16 * rt + n;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      att_u32x4 w = {0u, 0u, 0u, 0u};
-      if (r < n_qb) {
-        const uint4 x =
-            *reinterpret_cast<const uint4 *>(a.q + ((q_lo + r) * a.n_q_heads + hq) * D + kg * 32 + c * 8);
-        w = att_u32x4{x.x, x.y, x.z, x.w};
-      }
-      qa[rt][c] = __builtin_bit_cast(att_bf16x8, w);
-    }
-  }
-  const float qs = a.scales[h] * a.sm_log2e;  // K's dequant scale folds into the scores
-  const float vscale = a.scales[a.n_kv_heads + h];
+  const float qs = sk * a.sm_log2e;  // K's dequant scale folds into the scores
+  const float vscale = sv;
 
   // O^T tiles: o[rt][jt] holds channels 16 jt + 4 kg ..+4 of row 16 rt + n; m per row.
   // The softmax denominator l is a ninth tile on the matrix cores: V^T rows of ones, so
@@ -506,12 +498,41 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   auto ke_of = [&](const Pos &p) { return p.rc < a.n_ranges ? p.g.ke : 0; };
   att_u32x4 kc[2], vc[2];
   Pos p0 = {cur.s_first, rc, cur};
-  if (p0.rc < a.n_ranges) {
-    issue_step(lookup_step(p0.s, p0.g.ke), kc, vc);
-    store_step(0, kc, vc);
-  }
+  // the pages of the first two steps and Q are read together, then the first step's K/V
+  // and the block-table check
+  StepPage pg0 = {0, 0, 0u, 0};
+  if (p0.rc < a.n_ranges) pg0 = lookup_step(p0.s, p0.g.ke);
   Pos p1 = advance(p0);
   StepPage pg1 = lookup_step(p1.s, ke_of(p1));
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int r = wrow0 + 16 * rt + n;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      att_u32x4 w = {0u, 0u, 0u, 0u};
+      if (r < n_qb) {
+        const uint4 x =
+            *reinterpret_cast<const uint4 *>(a.q + ((q_lo + r) * a.n_q_heads + hq) * D + kg * 32 + c * 8);
+        w = att_u32x4{x.x, x.y, x.z, x.w};
+      }
+      qa[rt][c] = __builtin_bit_cast(att_bf16x8, w);
+    }
+  }
+  if (p0.rc < a.n_ranges) issue_step(pg0, kc, vc);
+  {
+    bool bad = false;
+    for (int r = 0; r < a.n_ranges; ++r) {
+      const Range g = range(r);
+      if (g.s_first >= g.ke) continue;
+      const int p_lo = (int)pf_page_of(a, (uint32_t)g.s_first), p_hi = (int)pf_page_of(a, (uint32_t)(g.ke - 1));
+      for (int pi = p_lo + (int)threadIdx.x; pi <= p_hi; pi += PF_THREADS) {
+        const int64_t pg = bt[pi];
+        bad |= pg < 0 || pg >= a.n_pages;
+      }
+    }
+    all_ok = !__syncthreads_or(bad);
+  }
+  if (p0.rc < a.n_ranges) store_step(0, kc, vc);
   __syncthreads();
   int buf = 0;
   while (p0.rc < a.n_ranges) {
@@ -526,7 +547,21 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     pg1 = pg2;
   }
 
-  // rows: normalise; merge; store channels 16 jt + 4 kg ..+4
+  // rows: normalise; merge; store channels 16 jt + 4 kg ..+4.  The running output and
+  // log-sum-exp being merged into are read first, all at once (rows past the sequence's
+  // end read its last row and discard it).
+  const bool merge_old = (a.mode & PF_MERGE) && !(a.mode & PF_INIT);
+  float lse_prev[2];
+  float4 o_prev[2][8];
+  if (merge_old) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int64_t row = (q_lo + min(wrow0 + 16 * rt + n, n_qb - 1)) * a.n_q_heads + hq;
+      lse_prev[rt] = a.lse2[row];
+#pragma unroll
+      for (int jt = 0; jt < 8; ++jt) o_prev[rt][jt] = *reinterpret_cast<const float4 *>(a.o_acc + row * D + 16 * jt + 4 * kg);
+    }
+  }
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     const int r = wrow0 + 16 * rt + n;
@@ -536,9 +571,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     const float inv = lt > 0.0f ? vscale / lt : 0.0f;  // V's dequant scale applied once, here
     const int64_t row = (q_lo + r) * a.n_q_heads + hq;
     float wa = 0.0f, wb = 1.0f, lse = lse_new;
-    const bool merge_old = (a.mode & PF_MERGE) && !(a.mode & PF_INIT);
     if (merge_old) {
-      const float lse_old = a.lse2[row];
+      const float lse_old = lse_prev[rt];
       const float mm = fmaxf(lse_old, lse_new);
       if (mm == -INFINITY) {
         wa = 0.0f;
@@ -559,7 +593,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = o[rt][jt][i] * inv * wb;
       if (merge_old) {  // also at weight 0, so that a NaN of an earlier step stays (0 x NaN)
-        const float4 old = *reinterpret_cast<const float4 *>(a.o_acc + idx);
+        const float4 old = o_prev[rt][jt];
         v[0] += wa * old.x;
         v[1] += wa * old.y;
         v[2] += wa * old.z;
