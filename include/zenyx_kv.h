@@ -362,7 +362,10 @@ int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, i
  *   ZX_PREFILL_MERGE: merge (o, lse2) into o_acc [n_q][n_q_heads][128] fp32 (normalised
  *     rows) and lse2 [n_q][n_q_heads] fp32, which hold the steps so far;
  *   ZX_PREFILL_INIT (with MERGE): the first step: overwrite instead of merging;
- *   ZX_PREFILL_BF16: also write the (merged) rows to out as bf16.
+ *   ZX_PREFILL_BF16: also write the (merged) rows to out as bf16;
+ *   ZX_PREFILL_LAST (with MERGE and BF16): merge as MERGE does but write the result to out
+ *     only, leaving o_acc and lse2 as they were (a ring's last step, when the running
+ *     output is not needed afterwards: half of that step's traffic on the running output).
  * Running every step of a ring with MERGE (INIT on the first) and BF16 on the last gives
  * attention over the union of the steps' key ranges.  Needs head_dim 128 and a page size
  * that is a multiple of 16.
@@ -376,7 +379,8 @@ enum {
   ZX_PREFILL_INIT = 2,
   ZX_PREFILL_BF16 = 4,
   ZX_PREFILL_FAST_P = 8,
-  ZX_PREFILL_EXACT_P = 16
+  ZX_PREFILL_EXACT_P = 16,
+  ZX_PREFILL_LAST = 32 /* ABI version 6 */
 };
 /* Precision of P.V.  The row sums use the same rounded softmax weights P as P.V, so a row
  * is an average of V under weights perturbed by at most e relative, which moves it by at

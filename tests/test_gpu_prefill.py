@@ -147,6 +147,38 @@ def test_ring_attention_equals_full_attention(ring, single_launch, precision):
     print(f"  worst |err| / max|V| = {worst:.3g}", flush=True)
 
 
+@pytest.mark.parametrize("precision", ["f16", "exact"])
+def test_last_step_leaves_the_running_output(precision):
+    """ZX_PREFILL_LAST: the last step of a ring writes the same bf16 rows as a merging
+    step and leaves o_acc / lse2 as they were."""
+    c = _ring_case()
+    print(f"last step precision={precision}", flush=True)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    q, cu, qp, pool, scales, bt = c["q"].to(DEV), t(c["cu"]), t(c["qp"]), t(c["pool"]), t(c["scales"]), t(c["bt"])
+    lens = c["lens"].astype(np.int64)
+    R = 3
+    bounds = [t((lens * r // R).astype(np.int32)) for r in range(R + 1)]
+    o_acc = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+    lse2 = torch.empty(q.shape[:2], dtype=torch.float32, device=DEV)
+    for r in range(R - 1):
+        kv.paged_attention_prefill(q, cu, qp, pool, scales, bt, bounds[r], bounds[r + 1], o_acc=o_acc, lse2=lse2,
+                                   first=r == 0, write_bf16=False, check=True, precision=precision)
+    o_keep, l_keep = o_acc.clone(), lse2.clone()
+    out_last = kv.paged_attention_prefill(q, cu, qp, pool, scales, bt, bounds[R - 1], bounds[R], o_acc=o_acc,
+                                          lse2=lse2, first=False, check=True, precision=precision, last=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_acc.view(torch.int32), o_keep.view(torch.int32))
+    assert torch.equal(lse2.view(torch.int32), l_keep.view(torch.int32))
+    out_merge = kv.paged_attention_prefill(q, cu, qp, pool, scales, bt, bounds[R - 1], bounds[R], o_acc=o_acc,
+                                           lse2=lse2, first=False, check=True, precision=precision)
+    torch.cuda.synchronize()
+    assert torch.equal(out_last.view(torch.int16), out_merge.view(torch.int16))
+    assert not torch.equal(o_acc.view(torch.int32), o_keep.view(torch.int32))  # the merging step did write
+    assert_precision(bits16(out_last), c["want"], c["vmax"], precision)
+    with pytest.raises(ValueError):
+        kv.paged_attention_prefill(q, cu, qp, pool, scales, bt, bounds[0], bounds[1], last=True)
+
+
 @pytest.mark.parametrize("ring,single", [(1, True), (8, True), (3, False)])
 def test_ring_attention_bf16_p(ring, single):
     """P rounded once to bf16 for P.V (ZX_PREFILL_FAST_P): within its bound of the oracle

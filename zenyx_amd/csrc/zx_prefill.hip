@@ -32,7 +32,7 @@ constexpr int PF_KROW = 272;                 // K row in LDS (128 channels bf16 
 constexpr int PF_VROW = 144;                 // V^T row (64 keys bf16 + 16 pad)
 constexpr int PF_KBYTES = PF_KEYS * PF_KROW;
 constexpr int PF_VBYTES = 128 * PF_VROW;
-constexpr int PF_MERGE = 1, PF_WRITE_BF16 = 2, PF_INIT = 4;
+constexpr int PF_MERGE = 1, PF_WRITE_BF16 = 2, PF_INIT = 4, PF_LAST = 8;
 // a row's running maximum m is raised only when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^PF_LAZY and O is rarely rescaled
 constexpr float PF_LAZY = 8.0f;
@@ -551,6 +551,8 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   // log-sum-exp being merged into are read first, all at once (rows past the sequence's
   // end read its last row and discard it).
   const bool merge_old = (a.mode & PF_MERGE) && !(a.mode & PF_INIT);
+  // the merged rows go back into the running output unless this is a ring's last step
+  const bool keep = (a.mode & PF_MERGE) && !(a.mode & PF_LAST);
   float lse_prev[2];
   float4 o_prev[2][8];
   if (merge_old) {
@@ -599,11 +601,11 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
         v[2] += wa * old.z;
         v[3] += wa * old.w;
       }
-      if (a.mode & PF_MERGE) *reinterpret_cast<float4 *>(a.o_acc + idx) = make_float4(v[0], v[1], v[2], v[3]);
+      if (keep) *reinterpret_cast<float4 *>(a.o_acc + idx) = make_float4(v[0], v[1], v[2], v[3]);
       if (a.mode & PF_WRITE_BF16)
         *reinterpret_cast<uint2 *>(a.out + idx) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
     }
-    if ((a.mode & PF_MERGE) && kg == 0) a.lse2[row] = lse;
+    if (keep && kg == 0) a.lse2[row] = lse;
   }
   if (e && a.err) atomicOr(a.err, e);
 }
@@ -626,9 +628,11 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
                  n_seqs > 0 && max_q_per_seq >= 0,
              "paged_attention_prefill: sizes must be positive");
   ZX_REQUIRE(n_q_heads % n_kv_heads == 0, "paged_attention_prefill: n_q_heads must be a multiple of n_kv_heads");
-  ZX_REQUIRE((flags & ~(ZX_PREFILL_MERGE | ZX_PREFILL_INIT | ZX_PREFILL_BF16 | ZX_PREFILL_FAST_P | ZX_PREFILL_EXACT_P)) ==
-                 0,
+  ZX_REQUIRE((flags & ~(ZX_PREFILL_MERGE | ZX_PREFILL_INIT | ZX_PREFILL_BF16 | ZX_PREFILL_FAST_P | ZX_PREFILL_EXACT_P |
+                        ZX_PREFILL_LAST)) == 0,
              "paged_attention_prefill: unknown flags");
+  ZX_REQUIRE(!(flags & ZX_PREFILL_LAST) || ((flags & ZX_PREFILL_MERGE) && (flags & ZX_PREFILL_BF16)),
+             "paged_attention_prefill: ZX_PREFILL_LAST needs ZX_PREFILL_MERGE and ZX_PREFILL_BF16");
   ZX_REQUIRE(!((flags & ZX_PREFILL_FAST_P) && (flags & ZX_PREFILL_EXACT_P)),
              "paged_attention_prefill: ZX_PREFILL_FAST_P and ZX_PREFILL_EXACT_P together");
   ZX_REQUIRE(!(flags & ZX_PREFILL_MERGE) || (o_acc && lse2), "paged_attention_prefill: merging needs o_acc and lse2");
@@ -663,7 +667,7 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
   a.page_size = page_size;
   a.max_blocks = max_blocks;
   a.mode = ((flags & ZX_PREFILL_MERGE) ? PF_MERGE : 0) | ((flags & ZX_PREFILL_INIT) ? PF_INIT : 0) |
-           ((flags & ZX_PREFILL_BF16) ? PF_WRITE_BF16 : 0);
+           ((flags & ZX_PREFILL_BF16) ? PF_WRITE_BF16 : 0) | ((flags & ZX_PREFILL_LAST) ? PF_LAST : 0);
   a.causal = causal ? 1 : 0;
   a.sm_log2e = sm_scale * ATT_LOG2E;
   {  // t / page_size = (t * magic) >> (31 + shift) for t < 2^31

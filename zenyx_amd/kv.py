@@ -408,14 +408,16 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
                             o_acc: torch.Tensor | None = None, lse2: torch.Tensor | None = None,
                             first: bool = True, out: torch.Tensor | None = None, write_bf16: bool = True,
                             max_q_per_seq: int | None = None, check: bool = False,
-                            err: torch.Tensor | None = None, precision: str = "f16"):
+                            err: torch.Tensor | None = None, precision: str = "f16", last: bool = False):
     """One ring step of attention over the FP8 pages (zx_paged_attention_prefill).
 
     ``q`` [n_q, Hq, 128] bf16 rows of all sequences (``cu_q`` [B+1] int32 offsets,
     ``q_pos0`` [B] int32 position of each sequence's first query row); keys
     [kv_begin[b], kv_end[b]) of the pool layer through the block tables.  With ``o_acc``
     / ``lse2`` (fp32 [n_q, Hq, 128] / [n_q, Hq]) the step merges into them (``first``
-    overwrites); with ``write_bf16`` the (merged) rows go to ``out`` as bf16.  ``err`` (int32
+    overwrites); with ``write_bf16`` the (merged) rows go to ``out`` as bf16, and ``last``
+    (with both) leaves ``o_acc`` / ``lse2`` unwritten (ZX_PREFILL_LAST: a ring's last step
+    whose running output is not needed afterwards).  ``err`` (int32
     [1], zeroed by the caller) collects the kernel's input-error bits across several calls;
     by default each call uses a fresh one.  ``precision``: see PRECISIONS.  Returns ``out``
     (or None)."""
@@ -458,9 +460,11 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
             raise ValueError("out must be bfloat16 like q")
     if max_q_per_seq is None:
         max_q_per_seq = int((cu_q[1:] - cu_q[:-1]).max().item()) if B else 0
+    if last and (o_acc is None or not write_bf16):
+        raise ValueError("last needs o_acc / lse2 and write_bf16")
     flags = (N.ZX_PREFILL_MERGE if o_acc is not None else 0) | (N.ZX_PREFILL_INIT if o_acc is not None and first
                                                                 else 0) | (N.ZX_PREFILL_BF16 if write_bf16 else 0) | \
-        p_flag
+        (N.ZX_PREFILL_LAST if last else 0) | p_flag
     sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
     dev = q.device
     if err is None:
@@ -580,7 +584,8 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
         paged_attention_prefill(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables, bounds[r, :B],
                                 bounds[r + 1, :B],
                                 causal=causal, sm_scale=sm_scale, o_acc=o_acc, lse2=lse2, first=r == 0, out=out,
-                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, err=err, precision=precision)
+                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, err=err, precision=precision,
+                                last=r == ring_degree - 1)
     if check:
         _raise_kernel_error(err, "ring_attention_fp8")
     return out
