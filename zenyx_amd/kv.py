@@ -296,6 +296,15 @@ def kv_quant_append(x: torch.Tensor, cu_seqlens: torch.Tensor, block_tables: tor
     return scales
 
 
+def _aligned_scales(scales_layer: torch.Tensor) -> torch.Tensor:
+    """One layer's ``[2, H]`` scales as the C ABI takes every pointer (contiguous, 16-byte
+    aligned).  A layer of a ``[L, 2, H]`` tensor starts 8 H bytes after the previous one,
+    so with H odd every other layer is not aligned: such a slice is copied (2 H floats)."""
+    if scales_layer.device.type != "cuda" or (scales_layer.is_contiguous() and scales_layer.data_ptr() % 16 == 0):
+        return scales_layer
+    return scales_layer.clone(memory_format=torch.contiguous_format)
+
+
 def kv_gather_dequant(pool_layer: torch.Tensor, scales_layer: torch.Tensor, block_tables: torch.Tensor,
                       seq_lens: torch.Tensor, out_len: int | None = None, check: bool = False,
                       out: tuple[torch.Tensor, torch.Tensor] | None = None):
@@ -308,6 +317,7 @@ def kv_gather_dequant(pool_layer: torch.Tensor, scales_layer: torch.Tensor, bloc
     n_pages, _, H, P, D = pool_layer.shape
     if scales_layer.shape != (2, H) or scales_layer.dtype != torch.float32:
         raise ValueError(f"scales_layer must be float32 [2, {H}]")
+    scales_layer = _aligned_scales(scales_layer)
     if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
         raise ValueError("block_tables and seq_lens must be int32")
     B = block_tables.shape[0]
@@ -356,6 +366,7 @@ def paged_attention_decode(q: torch.Tensor, pool_layer: torch.Tensor, scales_lay
         raise ValueError("the number of query heads must be a multiple of the number of kv heads")
     if scales_layer.shape != (2, Hkv) or scales_layer.dtype != torch.float32:
         raise ValueError(f"scales_layer must be float32 [2, {Hkv}]")
+    scales_layer = _aligned_scales(scales_layer)
     if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32 or block_tables.dim() != 2:
         raise ValueError("block_tables [B, max_blocks] and seq_lens [B] must be int32")
     if block_tables.shape[0] != B or seq_lens.numel() != B:
@@ -432,6 +443,7 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
     n_q, Hq, Dq = q.shape
     if two != 2 or Dq != D:
         raise ValueError("pool_layer must be [n_pages, 2, n_kv_heads, page_size, head_dim] matching q")
+    scales_layer = _aligned_scales(scales_layer)
     N.require_device(scales_layer, "scales_layer")
     if scales_layer.shape != (2, Hkv) or scales_layer.dtype != torch.float32:
         raise ValueError(f"scales_layer must be float32 [2, {Hkv}]")
@@ -502,6 +514,7 @@ def paged_attention_ring(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tens
     n_q, Hq, Dq = q.shape
     if Dq != D:
         raise ValueError("q and pool_layer disagree on head_dim")
+    scales_layer = _aligned_scales(scales_layer)
     N.require_device(scales_layer, "scales_layer")
     if scales_layer.shape != (2, Hkv) or scales_layer.dtype != torch.float32:
         raise ValueError(f"scales_layer must be float32 [2, {Hkv}]")
