@@ -8,8 +8,10 @@ aligned.
   bit-exact (the oracle's restatement of the reference's e4m3fn cast);
 * paged gather + dequant of every layer that append wrote: bf16 bit-exact;
 * decode attention from the pages: one bf16 ulp + 2^-17 max|V| (test_gpu_attention.py);
-* one prefill / ring step (fp16 P, the default): two bf16 ulps + 2^-10 max|V|
-  (test_gpu_prefill.py).
+* one prefill / ring step, and ring attention over 1-5 shards in one launch or one launch
+  per shard (fp16 P, the default): two bf16 ulps + 2^-10 max|V| (test_gpu_prefill.py);
+* the per-head FP8 quantiser (both paths) and the legacy int8 per-slab functions in
+  every dtype: bit-exact.
 """
 import numpy as np
 import pytest
@@ -153,3 +155,85 @@ def test_paged_cache_odd_kv_head_count(dev, H):
                                           1.0 / np.sqrt(D))
     assert werr == 0
     assert_within_one_ulp(bits16(got), want, v_colmax(pool[1], sc[1], bt, np.array(lens, np.int32), Hq))
+
+
+def _heads_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    return [(i, int(rng.integers(1, 7)), int(rng.integers(1, 6)), int(rng.integers(1, 10)),
+             16 * int(rng.integers(1, 1500))) for i in range(n)]  # runs are whole 16-element groups
+
+
+@pytest.mark.parametrize("case", _heads_cases(10, 5), ids=lambda c: f"h{c[0]}")
+def test_random_fp8_heads(dev, case):
+    """The per-head quantiser ([n_outer, n_batch, n_heads, run] -> one scale per (outer,
+    head)) through both paths, and its dequant, at random shapes."""
+    i, n_outer, B, H, run = case
+    print(f"fp8 heads case {i}: {(n_outer, B, H, run)}", flush=True)
+    g = torch.Generator().manual_seed(700 + i)
+    x = (torch.randn((n_outer, B, H, run), generator=g) *
+         torch.exp2(torch.randint(-8, 9, (n_outer, 1, H, 1), generator=g).float())).to(torch.bfloat16)
+    wc, ws = O.fp8_quant_heads(bits16(x))
+    for mode in ("single", "two"):
+        codes, scales = kv.fp8_quant_heads(x.to(dev), two_pass=mode == "two", single_pass=mode == "single",
+                                           check=True)
+        np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+        np.testing.assert_array_equal(codes.cpu().numpy(), wc)
+    assert_bf16_equal(bits16(kv.fp8_dequant_heads(codes, scales)), O.fp8_dequant_heads(wc, ws))
+
+
+_LEGACY_DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def _legacy_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    return [(i, str(rng.choice(list(_LEGACY_DT))), int(rng.integers(1, 9)), int(rng.integers(1, 5000)))
+            for i in range(n)]
+
+
+@pytest.mark.parametrize("case", _legacy_cases(10, 9), ids=lambda c: f"l{c[0]}")
+def test_random_int8_legacy_slabs(dev, case):
+    """precision.py:8-16 per slab (one launch for all slabs) at random slab counts and
+    lengths (aligned and not), every dtype the reference accepts."""
+    i, dt, n_slabs, n = case
+    print(f"legacy int8 case {i}: {dt} {n_slabs} x {n}", flush=True)
+    g = torch.Generator().manual_seed(900 + i)
+    x = (torch.randn((n_slabs, n), generator=g) *
+         torch.exp2(torch.randint(-10, 10, (n_slabs, 1), generator=g).float())).to(_LEGACY_DT[dt])
+    q, sc = kv.int8_legacy_quant_slabs(x.to(dev))
+    y = kv.int8_legacy_dequant_slabs(q, sc)
+    for s in range(n_slabs):
+        wq, ws = O.int8_legacy_quant(x[s].numpy() if dt == "f32" else bits16(x[s]), dt)
+        np.testing.assert_array_equal(q[s].cpu().numpy(), wq)
+        assert np.float32(sc[s].float().item()).tobytes() == np.float32(ws).tobytes()
+        assert_bf16_equal(bits16(y[s]), O.int8_legacy_dequant(wq, ws))
+
+
+def _ring_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        Hkv = int(rng.integers(1, 5))
+        Hq = Hkv * int(rng.choice([1, 2, 4]))
+        B = int(rng.integers(1, 4))
+        lens = [int(v) for v in rng.integers(1, 700, B)]
+        cases.append((i, Hq, Hkv, lens, int(rng.integers(1, 6)), bool(rng.integers(0, 2)), bool(rng.integers(0, 2))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _ring_cases(8, 13), ids=lambda c: f"r{c[0]}")
+def test_random_ring_attention(dev, case):
+    """Ring attention over R key shards (one launch, or one launch per shard merged through
+    the running output) equals attention over all keys, causal or not."""
+    i, Hq, Hkv, lens, R, single, causal = case
+    print(f"ring case {i}: Hq={Hq} Hkv={Hkv} lens={lens} R={R} single={single} causal={causal}", flush=True)
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, 16, lens, [0] * len(lens), lens, seed=1100 + i)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    kv_len = np.asarray(lens, np.int32)
+    out = kv.ring_attention_fp8(q.to(dev), t(cu), t(qp), t(pool), t(scales), t(bt), t(kv_len), ring_degree=R,
+                                causal=causal, check=True, single_launch=single)
+    torch.cuda.synchronize()
+    zeros = np.zeros(len(lens), np.int32)
+    want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, zeros, kv_len, causal,
+                                             float(np.float32(1.0 / np.sqrt(128))))
+    assert err == 0
+    assert_precision(bits16(out), want, vmax_rows(pool, scales, bt, cu, zeros, kv_len, Hq), "f16")
