@@ -4,8 +4,12 @@
  * Every entry point takes plain device pointers, element counts and a HIP stream
  * (hipStream_t passed as void*; NULL means the legacy default stream), enqueues its
  * kernels on that stream and returns without synchronising.  Buffers are owned by
- * the caller.  Return value: ZX_OK (0) or a negative ZX_ERR_* code; a message for
- * the last failure on the calling thread is available from zx_last_error().
+ * the caller.  The bulk arrays (activations, code pools, outputs) are moved
+ * in 16-byte vectors and must be 16-byte aligned, every layer of them included (hipMalloc
+ * and torch allocations are); a misaligned one is refused with ZX_ERR_INVALID.  Scale
+ * and index arrays need only their element's alignment.  Return value: ZX_OK (0) or a
+ * negative ZX_ERR_* code; a message for the last failure on the calling thread is
+ * available from zx_last_error().
  *
  * Reference interfaces each group replaces (paths relative to the zenyx source tree):
  *   - zenyx/streaming/precision.py:8-12   quantize_to_fp8_storage

@@ -41,6 +41,13 @@ def test_argument_errors_are_status_codes():
     rc = lib.zx_kv_gather_dequant(ctypes.c_void_p(16), 10, 8, 96, 16, ctypes.c_void_p(16), ctypes.c_void_p(16), 4,
                                   ctypes.c_void_p(16), 2, 64, ctypes.c_void_p(16), ctypes.c_void_p(16), None, None)
     assert rc == N.ZX_ERR_UNSUPPORTED and b"head_dim" in lib.zx_last_error()
+    # bulk arrays off a 16-byte boundary are refused before any device call
+    p16, p8 = ctypes.c_void_p(16), ctypes.c_void_p(24)
+    rc = lib.zx_kv_gather_dequant(p8, 10, 8, 128, 16, p16, p16, 4, p16, 2, 64, p16, p16, None, None)
+    assert rc == N.ZX_ERR_INVALID and b"16-byte aligned" in lib.zx_last_error()
+    rc = lib.zx_kv_quant_append(p8, 16 * 2 * 8 * 128, 1, 16, 8, 128, p16, None, 1, p16, 1, 16, p16,
+                                2 * 8 * 16 * 128, 1, p16, 0, None, p16, 1 << 20, None)
+    assert rc == N.ZX_ERR_INVALID and b"16-byte aligned" in lib.zx_last_error()
     rc = lib.zx_int8_legacy_quant(ctypes.c_void_p(16), 0, 0, ctypes.c_void_p(16), ctypes.c_void_p(16),
                                   ctypes.c_void_p(16), 256, None)
     assert rc == N.ZX_ERR_INVALID and b"empty" in lib.zx_last_error()

@@ -713,6 +713,8 @@ extern "C" int zx_paged_attention_decode(const uint16_t *q, int32_t n_q_heads, c
                                          size_t workspace_bytes, zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(q && pool && scales && block_tables && seq_lens && out, "paged_attention_decode: null pointer");
+  ZX_REQUIRE(aligned16(q) && aligned16(pool) && aligned16(out),
+             "paged_attention_decode: q, pool and out must be 16-byte aligned");
   ZX_REQUIRE(n_q_heads > 0 && n_kv_heads > 0 && n_pages > 0 && page_size > 0 && max_blocks > 0 && n_seqs > 0,
              "paged_attention_decode: sizes must be positive");
   ZX_REQUIRE(n_q_heads % n_kv_heads == 0, "paged_attention_decode: n_q_heads must be a multiple of n_kv_heads");

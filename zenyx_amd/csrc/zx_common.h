@@ -32,6 +32,8 @@ int check_launch(const char *what);
   } while (0)
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// The bulk arrays (activations, code pools, outputs) are moved in 16-byte vectors.
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Number of compute units of the current device (cached per device).
 int num_cus();

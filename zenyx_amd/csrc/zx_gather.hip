@@ -185,6 +185,8 @@ extern "C" int zx_kv_gather_dequant(const uint8_t *pool, int64_t n_pages, int32_
   clear_error();
   ZX_REQUIRE(pool && scales && block_tables && seq_lens && k_out && v_out,
              "kv_gather_dequant: null pointer");
+  ZX_REQUIRE(aligned16(pool) && aligned16(k_out) && aligned16(v_out),
+             "kv_gather_dequant: pool, k_out and v_out must be 16-byte aligned");
   ZX_REQUIRE(n_pages > 0 && n_heads > 0 && page_size > 0 && max_blocks > 0 && n_seqs > 0 && out_len >= 0,
              "kv_gather_dequant: sizes must be positive");
   if (!(head_dim == 64 || head_dim == 128 || head_dim == 256))

@@ -638,6 +638,9 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
   ZX_REQUIRE(!(flags & ZX_PREFILL_MERGE) || (o_acc && lse2), "paged_attention_prefill: merging needs o_acc and lse2");
   ZX_REQUIRE(!(flags & ZX_PREFILL_BF16) || out, "paged_attention_prefill: bf16 output requested without out");
   ZX_REQUIRE(flags & (ZX_PREFILL_MERGE | ZX_PREFILL_BF16), "paged_attention_prefill: nothing to write");
+  ZX_REQUIRE(aligned16(q) && aligned16(pool) && (!(flags & ZX_PREFILL_MERGE) || aligned16(o_acc)) &&
+                 (!(flags & ZX_PREFILL_BF16) || aligned16(out)),
+             "paged_attention_prefill: q, pool, o_acc and out must be 16-byte aligned");
   if (head_dim != 128 || page_size % 16)
     return fail(ZX_ERR_UNSUPPORTED, "paged_attention_prefill: needs head_dim 128 and pages of a multiple of 16 tokens "
                                     "(got %d, %d)", head_dim, page_size);

@@ -878,6 +878,7 @@ extern "C" int zx_fp8_quant_heads(const uint16_t *x, int64_t n_outer, int64_t n_
                                   void *workspace, size_t workspace_bytes, zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(x && codes && scales, "fp8_quant_heads: null pointer");
+  ZX_REQUIRE(aligned16(x) && aligned16(codes), "fp8_quant_heads: x and codes must be 16-byte aligned");
   ZX_REQUIRE(!(flags & ~(ZX_HEADS_TWO_PASS | ZX_HEADS_SINGLE_PASS)), "fp8_quant_heads: unknown flag bits 0x%x",
              (unsigned)flags);
   ZX_REQUIRE((flags & (ZX_HEADS_TWO_PASS | ZX_HEADS_SINGLE_PASS)) != (ZX_HEADS_TWO_PASS | ZX_HEADS_SINGLE_PASS),
@@ -916,6 +917,7 @@ extern "C" int zx_fp8_dequant_heads(const uint8_t *codes, const float *scales, i
                                     zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(codes && scales && y, "fp8_dequant_heads: null pointer");
+  ZX_REQUIRE(aligned16(codes) && aligned16(y), "fp8_dequant_heads: codes and y must be 16-byte aligned");
   HeadsGeom g;
   int64_t nb;
   int rc = heads_geom(n_outer, n_batch, n_heads, run, g, nb, (int64_t)QH_THREADS * QH_DQ_VPT);
@@ -929,6 +931,8 @@ extern "C" int zx_kv_scales(const uint16_t *x, int64_t x_layer_stride, int32_t n
                             int32_t n_heads, int32_t head_dim, float *scales, zx_stream_t stream) {
   clear_error();
   ZX_REQUIRE(scales && (x || n_tok == 0), "kv_scales: null pointer");
+  ZX_REQUIRE(aligned16(x) && (n_layers == 1 || x_layer_stride % 8 == 0),
+             "kv_scales: x (and every layer of it) must be 16-byte aligned");
   ZX_REQUIRE(n_layers > 0 && n_layers <= 65535, "kv_scales: n_layers out of range");
   RowGeom g;
   int rc = row_geom(n_heads, head_dim, n_tok, x_layer_stride, g);
@@ -962,6 +966,8 @@ int kv_quant_append_impl(const uint16_t *x, int64_t x_layer_stride, int32_t n_la
              "kv_quant_append: ZX_APPEND_TWO_PASS and ZX_APPEND_SINGLE_PASS together");
   ZX_REQUIRE(scales && cu_seqlens && block_tables && pool, "kv_quant_append: null pointer");
   ZX_REQUIRE(x || n_tok == 0, "kv_quant_append: null x");
+  ZX_REQUIRE(aligned16(x) && aligned16(pool) && (n_layers == 1 || (x_layer_stride % 8 == 0 && pool_layer_stride % 16 == 0)),
+             "kv_quant_append: x and pool (and every layer of them) must be 16-byte aligned");
   ZX_REQUIRE(n_layers > 0 && n_layers <= 65535, "kv_quant_append: n_layers out of range");
   ZX_REQUIRE(n_seqs > 0 && max_blocks > 0 && page_size > 0 && n_pages > 0,
              "kv_quant_append: n_seqs, max_blocks, page_size and n_pages must be positive");
