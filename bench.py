@@ -1,6 +1,6 @@
 """Benchmark of the KV-cache hot path on one MI355X.
 
-Headline (``value``): BASELINE configs[1] -- paged append with fused FP8 quantisation at
+Headline (``value``): configs[1] of the benchmark definition -- paged append with fused FP8 quantisation at
 the Llama-3-8B KV shape (32 layers, 8 KV heads, head_dim 128, page 16, 16 sequences of
 U[1k, 8k] tokens, 5% of each sequence's (layer, head) pairs x50), one step = one append
 of every layer, inputs already resident in HBM.  Reported as algorithmic GB/s

@@ -5,7 +5,7 @@
 * ``reference_kats.json``: the known answers the reference's own tests hold for this path
   (zenyx/tests/test_streaming.py:14-22, 25-28, 31-36), copied as data, plus the OCP OFP8
   e4m3fn boundary table the FP8 encoder follows.
-* ``configs0.json``: the expected results of BASELINE configs[0] (the README toy model's
+* ``configs0.json``: the expected results of the README toy model's case (its
   KV cache ``[12, 2, 1, 12, 4096, 64]`` bf16, ``torch.manual_seed(0)``, N(0, 1) drawn in
   fp32) from the C oracle: all 288 per-(layer, kv, head) FP8 scales and legacy int8
   scales as fp32 bit patterns, and SHA-256 digests of the codes and dequantised values.

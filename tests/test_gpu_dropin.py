@@ -215,7 +215,7 @@ def test_kv_tier_manager_pinned_source_outlives_its_copy(dev):
 
 
 def test_fp8_kv_quantizer_config1_shape(dev):
-    """The README toy model's cache shape with 256 tokens."""
+    """The README toy model's cache shape (12 layers, 12 heads, D = 64) with 256 tokens."""
     g = torch.Generator().manual_seed(0)
     x = torch.randn((12, 2, 1, 12, 256, 64), generator=g).to(torch.bfloat16)
     q = FP8KVQuantizer()

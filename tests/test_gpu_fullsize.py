@@ -1,4 +1,4 @@
-"""Parity at BASELINE's full sizes, on the exact workloads bench.py times.
+"""Parity at the benchmark's full sizes, on the exact workloads bench.py times.
 
 * configs[1] (seed 1: 32 layers x 74,902 tokens, 8 KV heads, D = 128, page 16, outlier
   heads x50): one fused append of all layers; all 512 scales bit-exact against the C

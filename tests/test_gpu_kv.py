@@ -1,7 +1,7 @@
 """GPU parity of the FP8 KV kernels (libzenyx_kv.so) against the CPU oracle.
 
 Codes, scales and gathered bytes must be bit-exact; dequantized bf16 must be bit-exact
-as well (stronger than the 1-ulp tolerance BASELINE.json allows), with NaN compared as
+as well (stronger than a 1-ulp tolerance), with NaN compared as
 a class because torch itself writes different NaN payloads on different paths.
 """
 import numpy as np

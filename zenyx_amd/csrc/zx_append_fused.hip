@@ -1,5 +1,5 @@
 // zx_append_fused.hip -- single-pass paged append with dynamic per-(layer, kv, head) FP8
-// scales.
+// scales (sized for a 32-layer append of ~75k tokens, 8 KV heads, D = 128).
 //
 // A (layer, kv, head) slab's scale needs the amax over all of its tokens before any of
 // them can be encoded.  Instead of reading the input twice (amax pass + quant pass), one

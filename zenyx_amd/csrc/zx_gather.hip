@@ -1,4 +1,4 @@
-// zx_gather.hip -- paged gather + FP8 dequant for decode.
+// zx_gather.hip -- paged gather + FP8 dequant for decode (sized for 64 sequences x 32k tokens).
 // Pool layout per layer: [n_pages][2][H][P][D] uint8; output [B][H][T][D] bf16 per kv.
 // Thread work units are 8 codes (8 B in, 16 B out), so each load instruction of a wave
 // reads 512 contiguous bytes and each store writes 1 KB contiguous; both are
