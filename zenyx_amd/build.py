@@ -29,6 +29,9 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
+# per-file options: under this machine scheduler the fused append's loads issue in longer
+# clauses (0.5-0.8% less time per 32-layer x 74,902-token append on MI355X, same codes)
+FILE_FLAGS = {"zx_append_fused.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
 
 
 def hipcc() -> str:
@@ -40,7 +43,7 @@ def hipcc() -> str:
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
