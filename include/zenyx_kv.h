@@ -370,7 +370,16 @@ int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, i
  *   ZX_PREFILL_LAST (with MERGE and BF16): merge as MERGE does but write the result to out
  *     only, leaving o_acc and lse2 as they were (a ring's last step, when the running
  *     output is not needed afterwards: half of that step's traffic on the running output).
- * Running every step of a ring with MERGE (INIT on the first) and BF16 on the last gives
+ *   ZX_PREFILL_FINAL (with MERGE and BF16, causal, zx_paged_attention_prefill; ABI
+ *     version 7): for a causal ring whose steps cover each sequence's keys in ascending,
+ *     contiguous ranges (the first step's kv_begin 0, each later kv_begin the previous
+ *     kv_end): a row at a position below kv_begin is left alone (an earlier step finished
+ *     it); a row below kv_end sees no later key, so it is written to out as bf16 and not
+ *     to o_acc / lse2; the other rows merge into o_acc / lse2 (with LAST: go to out as
+ *     well, as final).  Each row then reaches out in the step that completes it, and the
+ *     last step converts only the rows it reaches instead of every row.
+ * Running every step of a ring with MERGE (INIT on the first) and BF16 on the last (or
+ * MERGE | BF16 | FINAL on every step, INIT on the first, LAST on the last) gives
  * attention over the union of the steps' key ranges.  Needs head_dim 128 and a page size
  * that is a multiple of 16.
  * NaN codes (e4m3 0x7F / 0xFF): a NaN K element makes the rows that see its key NaN in
@@ -384,7 +393,8 @@ enum {
   ZX_PREFILL_BF16 = 4,
   ZX_PREFILL_FAST_P = 8,
   ZX_PREFILL_EXACT_P = 16,
-  ZX_PREFILL_LAST = 32 /* ABI version 6 */
+  ZX_PREFILL_LAST = 32, /* ABI version 6 */
+  ZX_PREFILL_FINAL = 64 /* ABI version 7 */
 };
 /* Precision of P.V.  The row sums use the same rounded softmax weights P as P.V, so a row
  * is an average of V under weights perturbed by at most e relative, which moves it by at

@@ -122,7 +122,7 @@ def test_header_constants_match_the_python_binding():
 
     consts = header_constants()
     for name in ("ZX_PREFILL_MERGE", "ZX_PREFILL_INIT", "ZX_PREFILL_BF16", "ZX_PREFILL_FAST_P", "ZX_PREFILL_EXACT_P",
-                 "ZX_PREFILL_LAST",
+                 "ZX_PREFILL_LAST", "ZX_PREFILL_FINAL",
                  "ZX_HEADS_TWO_PASS", "ZX_HEADS_SINGLE_PASS", "ZX_APPEND_STATIC_SCALES", "ZX_APPEND_SATURATE",
                  "ZX_APPEND_TWO_PASS", "ZX_KERR_PAGE_RANGE", "ZX_KERR_POS_RANGE", "ZX_KERR_SPIN", "ZX_KERR_OVERFLOW",
                  "ZX_ERR_INVALID", "ZX_ERR_UNSUPPORTED", "ZX_ERR_WORKSPACE"):
@@ -150,6 +150,15 @@ def test_exclusive_flags_are_refused_before_any_device_call():
         assert rc == N.ZX_ERR_INVALID and b"together" in lib.zx_last_error()
         rc = fn(*args, N.ZX_PREFILL_BF16 | N.ZX_PREFILL_LAST, None, None, p, None, None)
         assert rc == N.ZX_ERR_INVALID and b"ZX_PREFILL_LAST needs" in lib.zx_last_error()
+        rc = fn(*args, N.ZX_PREFILL_BF16 | N.ZX_PREFILL_FINAL, None, None, p, None, None)
+        assert rc == N.ZX_ERR_INVALID and b"ZX_PREFILL_FINAL needs" in lib.zx_last_error()
+        rc = fn(*args, 128 | N.ZX_PREFILL_BF16, None, None, p, None, None)
+        assert rc == N.ZX_ERR_INVALID and b"unknown flags" in lib.zx_last_error()
+    # FINAL on a non-causal step
+    args = [p, 16, p, p, 8, p, 10, 2, 128, 16, p, p, 4, p, p, 1, 16, 0, 0.1]
+    rc = lib.zx_paged_attention_prefill(*args, N.ZX_PREFILL_MERGE | N.ZX_PREFILL_BF16 | N.ZX_PREFILL_FINAL, p, p, p,
+                                        None, None)
+    assert rc == N.ZX_ERR_INVALID and b"ZX_PREFILL_FINAL needs" in lib.zx_last_error()
 
 
 def test_attention_precision_names():

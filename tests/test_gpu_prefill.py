@@ -179,6 +179,63 @@ def test_last_step_leaves_the_running_output(precision):
         kv.paged_attention_prefill(q, cu, qp, pool, scales, bt, bounds[0], bounds[1], last=True)
 
 
+def _steps(q, cu, qp, pool, scales, bt, lens, R, final, precision="f16"):
+    """A causal ring of R launches over keys [0, lens) in ascending contiguous shards; out
+    starts as a NaN pattern so that a row no step writes shows."""
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    lens = np.asarray(lens, np.int64)
+    bounds = [t((lens * r // R).astype(np.int32)) for r in range(R + 1)]
+    o_acc = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+    lse2 = torch.empty(q.shape[:2], dtype=torch.float32, device=DEV)
+    out = torch.full(q.shape, 0x7FC1, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+    for r in range(R):
+        kv.paged_attention_prefill(q, cu, qp, pool, scales, bt, bounds[r], bounds[r + 1], o_acc=o_acc, lse2=lse2,
+                                   first=r == 0, out=out, write_bf16=final or r == R - 1, check=True,
+                                   precision=precision, last=r == R - 1, final=final)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("shape", ["ragged", "queries_past_keys", "empty_shards"])
+@pytest.mark.parametrize("R", [3, 8])
+def test_final_steps_equal_the_merged_ring(shape, R):
+    """ZX_PREFILL_FINAL: every step writes as bf16 the rows it completes and the last one
+    converts only the rows it reaches; the output equals, bit for bit, the ring that merges
+    every row into the running output and converts them all in the last step (the same
+    fp32 value goes to bf16 either way), every row is written (none keeps the NaN pattern
+    the output starts with), and it is within the default bound of the oracle."""
+    if shape == "ragged":
+        c = _ring_case()
+        q, pool, scales, bt, cu, qp, lens = c["q"], c["pool"], c["scales"], c["bt"], c["cu"], c["qp"], c["lens"]
+        Hq, want, vmax = 32, c["want"], c["vmax"]
+    else:
+        Hq, Hkv, P = 8, 2, 16
+        if shape == "queries_past_keys":  # rows at positions past the last key see every key
+            n_q, q_pos0, lens = [40, 70, 5], [10, 0, 30], [30, 50, 33]
+        else:  # most shards empty, a sequence's only key in the last shard
+            n_q, q_pos0, lens = [3, 4, 20], [0, 0, 0], [3, 1, 20]
+        q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, n_q, q_pos0, lens, seed=23)
+        lens = np.asarray(lens, np.int32)
+        zeros = np.zeros(len(lens), np.int32)
+        sm = float(np.float32(1.0 / np.sqrt(128)))
+        want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, zeros, lens, True, sm)
+        assert err == 0
+        vmax = vmax_rows(pool, scales, bt, cu, zeros, lens, Hq)
+    print(f"final steps: {shape}, R={R}", flush=True)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    args = (q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), lens, R)
+    got = _steps(*args, final=True)
+    ref = _steps(*args, final=False)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert not torch.isnan(got.float()).any()
+    assert_precision(bits16(got), want, vmax)
+    with pytest.raises(ValueError):
+        kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(np.zeros(len(lens), np.int32)),
+                                   t(np.asarray(lens, np.int32)), causal=False, o_acc=torch.empty(q.shape,
+                                   dtype=torch.float32, device=DEV), lse2=torch.empty(q.shape[:2],
+                                   dtype=torch.float32, device=DEV), final=True)
+
+
 @pytest.mark.parametrize("ring,single", [(1, True), (8, True), (3, False)])
 def test_ring_attention_bf16_p(ring, single):
     """P rounded once to bf16 for P.V (ZX_PREFILL_FAST_P): within its bound of the oracle

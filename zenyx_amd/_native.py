@@ -29,10 +29,11 @@ ZX_APPEND_SATURATE = 4
 ZX_APPEND_SINGLE_PASS = 8
 ZX_PREFILL_MERGE, ZX_PREFILL_INIT, ZX_PREFILL_BF16, ZX_PREFILL_FAST_P, ZX_PREFILL_EXACT_P = 1, 2, 4, 8, 16
 ZX_PREFILL_LAST = 32
+ZX_PREFILL_FINAL = 64
 ZX_HEADS_TWO_PASS = 1
 ZX_HEADS_SINGLE_PASS = 2
 ZX_NEVER = 0x7FFFFFFF
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _P = ctypes.c_void_p
 _I64, _I32, _SZ, _INT = ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t, ctypes.c_int

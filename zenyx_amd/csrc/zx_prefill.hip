@@ -32,7 +32,7 @@ constexpr int PF_KROW = 272;                 // K row in LDS (128 channels bf16 
 constexpr int PF_VROW = 144;                 // V^T row (64 keys bf16 + 16 pad)
 constexpr int PF_KBYTES = PF_KEYS * PF_KROW;
 constexpr int PF_VBYTES = 128 * PF_VROW;
-constexpr int PF_MERGE = 1, PF_WRITE_BF16 = 2, PF_INIT = 4, PF_LAST = 8;
+constexpr int PF_MERGE = 1, PF_WRITE_BF16 = 2, PF_INIT = 4, PF_LAST = 8, PF_FINAL = 16;
 // a row's running maximum m is raised only when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^PF_LAZY and O is rarely rescaled
 constexpr float PF_LAZY = 8.0f;
@@ -185,9 +185,16 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   };
   Range cur;
   int rc = next_range(0, cur);
-  if (rc == a.n_ranges && !(a.mode & (PF_INIT | PF_WRITE_BF16))) {
+  // rows that reach no key still have something to write on a first step (the empty
+  // running output), on a step that writes bf16 for every row, and on a FINAL ring's last
+  // step (rows beyond the keys, finished now)
+  const bool rows_without_keys_write =
+      (a.mode & PF_INIT) ||
+      ((a.mode & PF_WRITE_BF16) && (!(a.mode & PF_FINAL) || (a.mode & PF_LAST)));
+  if (rc == a.n_ranges && !rows_without_keys_write) {
     // no key of any range reaches the block's rows: merging would leave o_acc and lse2 as
-    // they are (block-uniform exit)
+    // they are, and a FINAL step's rows below kv_begin were finished before (block-uniform
+    // exit)
     if (e && a.err && threadIdx.x == 0) atomicOr(a.err, e);
     return;
   }
@@ -569,6 +576,14 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     const int r = wrow0 + 16 * rt + n;
     const float lt = ol[rt][0];
     if (r >= n_qb) continue;
+    // FINAL: rows below kv_begin were finished by an earlier step; rows below kv_end (all
+    // rows on the last step) are finished by this one and go to out only
+    const int64_t pos = qp0 + r;
+    const bool fin_mode = (a.mode & PF_FINAL) != 0;
+    if (fin_mode && pos < kb0) continue;
+    const bool fin = fin_mode && (pos < ke0 || (a.mode & PF_LAST));
+    const bool keep_row = keep && !fin;
+    const bool bf16_row = (a.mode & PF_WRITE_BF16) && (!fin_mode || fin);
     const float lse_new = lt > 0.0f ? m[rt] + (__builtin_amdgcn_logf(lt) - p_shift) : -INFINITY;
     const float inv = lt > 0.0f ? vscale / lt : 0.0f;  // V's dequant scale applied once, here
     const int64_t row = (q_lo + r) * a.n_q_heads + hq;
@@ -601,11 +616,11 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
         v[2] += wa * old.z;
         v[3] += wa * old.w;
       }
-      if (keep) *reinterpret_cast<float4 *>(a.o_acc + idx) = make_float4(v[0], v[1], v[2], v[3]);
-      if (a.mode & PF_WRITE_BF16)
+      if (keep_row) *reinterpret_cast<float4 *>(a.o_acc + idx) = make_float4(v[0], v[1], v[2], v[3]);
+      if (bf16_row)
         *reinterpret_cast<uint2 *>(a.out + idx) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
     }
-    if (keep && kg == 0) a.lse2[row] = lse;
+    if (keep_row && kg == 0) a.lse2[row] = lse;
   }
   if (e && a.err) atomicOr(a.err, e);
 }
@@ -629,8 +644,12 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
              "paged_attention_prefill: sizes must be positive");
   ZX_REQUIRE(n_q_heads % n_kv_heads == 0, "paged_attention_prefill: n_q_heads must be a multiple of n_kv_heads");
   ZX_REQUIRE((flags & ~(ZX_PREFILL_MERGE | ZX_PREFILL_INIT | ZX_PREFILL_BF16 | ZX_PREFILL_FAST_P | ZX_PREFILL_EXACT_P |
-                        ZX_PREFILL_LAST)) == 0,
+                        ZX_PREFILL_LAST | ZX_PREFILL_FINAL)) == 0,
              "paged_attention_prefill: unknown flags");
+  ZX_REQUIRE(!(flags & ZX_PREFILL_FINAL) ||
+                 ((flags & ZX_PREFILL_MERGE) && (flags & ZX_PREFILL_BF16) && causal && n_ranges == 1),
+             "paged_attention_prefill: ZX_PREFILL_FINAL needs ZX_PREFILL_MERGE, ZX_PREFILL_BF16, causal and one key "
+             "range (zx_paged_attention_prefill)");
   ZX_REQUIRE(!(flags & ZX_PREFILL_LAST) || ((flags & ZX_PREFILL_MERGE) && (flags & ZX_PREFILL_BF16)),
              "paged_attention_prefill: ZX_PREFILL_LAST needs ZX_PREFILL_MERGE and ZX_PREFILL_BF16");
   ZX_REQUIRE(!((flags & ZX_PREFILL_FAST_P) && (flags & ZX_PREFILL_EXACT_P)),
@@ -670,7 +689,8 @@ int prefill_impl(const uint16_t *q, int64_t n_q, const int32_t *cu_q, const int3
   a.page_size = page_size;
   a.max_blocks = max_blocks;
   a.mode = ((flags & ZX_PREFILL_MERGE) ? PF_MERGE : 0) | ((flags & ZX_PREFILL_INIT) ? PF_INIT : 0) |
-           ((flags & ZX_PREFILL_BF16) ? PF_WRITE_BF16 : 0) | ((flags & ZX_PREFILL_LAST) ? PF_LAST : 0);
+           ((flags & ZX_PREFILL_BF16) ? PF_WRITE_BF16 : 0) | ((flags & ZX_PREFILL_LAST) ? PF_LAST : 0) |
+           ((flags & ZX_PREFILL_FINAL) ? PF_FINAL : 0);
   a.causal = causal ? 1 : 0;
   a.sm_log2e = sm_scale * ATT_LOG2E;
   {  // t / page_size = (t * magic) >> (31 + shift) for t < 2^31

@@ -57,4 +57,4 @@ extern "C" int zx_set_wait_bound_us(int64_t us) {
 
 extern "C" const char *zx_last_error(void) { return zx::g_msg; }
 
-extern "C" int zx_abi_version(void) { return 6; }
+extern "C" int zx_abi_version(void) { return 7; }

@@ -419,7 +419,8 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
                             o_acc: torch.Tensor | None = None, lse2: torch.Tensor | None = None,
                             first: bool = True, out: torch.Tensor | None = None, write_bf16: bool = True,
                             max_q_per_seq: int | None = None, check: bool = False,
-                            err: torch.Tensor | None = None, precision: str = "f16", last: bool = False):
+                            err: torch.Tensor | None = None, precision: str = "f16", last: bool = False,
+                            final: bool = False):
     """One ring step of attention over the FP8 pages (zx_paged_attention_prefill).
 
     ``q`` [n_q, Hq, 128] bf16 rows of all sequences (``cu_q`` [B+1] int32 offsets,
@@ -428,7 +429,12 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
     / ``lse2`` (fp32 [n_q, Hq, 128] / [n_q, Hq]) the step merges into them (``first``
     overwrites); with ``write_bf16`` the (merged) rows go to ``out`` as bf16, and ``last``
     (with both) leaves ``o_acc`` / ``lse2`` unwritten (ZX_PREFILL_LAST: a ring's last step
-    whose running output is not needed afterwards).  ``err`` (int32
+    whose running output is not needed afterwards).  ``final`` (with both, causal;
+    ZX_PREFILL_FINAL) is for a causal ring whose steps cover each sequence's keys in
+    ascending contiguous ranges from 0: rows below ``kv_begin`` are left alone (finished
+    by an earlier step), rows below ``kv_end`` go to ``out`` only (no later key reaches
+    them), the others merge into ``o_acc`` / ``lse2`` (and go to ``out`` too when ``last``).
+    ``err`` (int32
     [1], zeroed by the caller) collects the kernel's input-error bits across several calls;
     by default each call uses a fresh one.  ``precision``: see PRECISIONS.  Returns ``out``
     (or None)."""
@@ -474,9 +480,11 @@ def paged_attention_prefill(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.T
         max_q_per_seq = int((cu_q[1:] - cu_q[:-1]).max().item()) if B else 0
     if last and (o_acc is None or not write_bf16):
         raise ValueError("last needs o_acc / lse2 and write_bf16")
+    if final and (o_acc is None or not write_bf16 or not causal):
+        raise ValueError("final needs o_acc / lse2, write_bf16 and causal")
     flags = (N.ZX_PREFILL_MERGE if o_acc is not None else 0) | (N.ZX_PREFILL_INIT if o_acc is not None and first
                                                                 else 0) | (N.ZX_PREFILL_BF16 if write_bf16 else 0) | \
-        (N.ZX_PREFILL_LAST if last else 0) | p_flag
+        (N.ZX_PREFILL_LAST if last else 0) | (N.ZX_PREFILL_FINAL if final else 0) | p_flag
     sm = float(sm_scale) if sm_scale is not None else 1.0 / float(D) ** 0.5
     dev = q.device
     if err is None:
@@ -556,7 +564,8 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
     shards with the running softmax state in registers (zx_paged_attention_ring);
     otherwise each step is its own launch (paged_attention_prefill, the unit a ring over R
     GPUs runs) merged into a running fp32 output and log-sum-exp, the last one writing
-    bf16.  Either equals attention over all keys (the exchange between devices is what
+    bf16 (causal: every step writes as bf16 the rows it completes, ZX_PREFILL_FINAL, so
+    the last one converts only the rows it reaches).  Either equals attention over all keys (the exchange between devices is what
     one GPU leaves out).  ``precision``: how P enters P.V (see PRECISIONS).
     ``max_q_per_seq``: a bound on every sequence's query count, when the caller knows one
     (otherwise it is read back from ``cu_q``, which waits for the device).  The kernels
@@ -597,8 +606,8 @@ def ring_attention_fp8(q: torch.Tensor, cu_q: torch.Tensor, q_pos0: torch.Tensor
         paged_attention_prefill(q, cu_q, q_pos0, pool_layer, scales_layer, block_tables, bounds[r, :B],
                                 bounds[r + 1, :B],
                                 causal=causal, sm_scale=sm_scale, o_acc=o_acc, lse2=lse2, first=r == 0, out=out,
-                                write_bf16=r == ring_degree - 1, max_q_per_seq=mq, err=err, precision=precision,
-                                last=r == ring_degree - 1)
+                                write_bf16=causal or r == ring_degree - 1, max_q_per_seq=mq, err=err,
+                                precision=precision, last=r == ring_degree - 1, final=causal)
     if check:
         _raise_kernel_error(err, "ring_attention_fp8")
     return out
