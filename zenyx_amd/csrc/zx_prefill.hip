@@ -191,7 +191,10 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   const bool rows_without_keys_write =
       (a.mode & PF_INIT) ||
       ((a.mode & PF_WRITE_BF16) && (!(a.mode & PF_FINAL) || (a.mode & PF_LAST)));
-  if (rc == a.n_ranges && !rows_without_keys_write) {
+  // a FINAL step leaves rows below kv_begin alone: a block of such rows only would read
+  // the running output for nothing
+  const bool rows_all_done = (a.mode & PF_FINAL) && qp0 + last_row < (int64_t)kb0;
+  if ((rc == a.n_ranges && !rows_without_keys_write) || rows_all_done) {
     // no key of any range reaches the block's rows: merging would leave o_acc and lse2 as
     // they are, and a FINAL step's rows below kv_begin were finished before (block-uniform
     // exit)
