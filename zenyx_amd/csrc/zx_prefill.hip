@@ -32,6 +32,7 @@ constexpr int PF_KROW = 272;                 // K row in LDS (128 channels bf16 
 constexpr int PF_VROW = 144;                 // V^T row (64 keys bf16 + 16 pad)
 constexpr int PF_KBYTES = PF_KEYS * PF_KROW;
 constexpr int PF_VBYTES = 128 * PF_VROW;
+constexpr int PF_RTAB = 64;  // key ranges whose bounds a block keeps in LDS
 constexpr int PF_MERGE = 1, PF_WRITE_BF16 = 2, PF_INIT = 4, PF_LAST = 8, PF_FINAL = 16;
 // a row's running maximum m is raised only when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^PF_LAZY and O is rarely rescaled
@@ -161,12 +162,34 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
   struct Range {
     int kb, ke, s_first, ke_blk;
   };
+  // With several ranges, their bounds go to LDS in one round trip here: read where the
+  // walk reaches them, each would stall the steps for a dependent load.
+  __shared__ int32_t rtab[2][PF_RTAB];
+  const int n_tab = a.n_ranges > 1 ? min(a.n_ranges, PF_RTAB) : 0;
+  if (n_tab) {  // block-uniform
+    for (int r = threadIdx.x; r < n_tab; r += PF_THREADS) {
+      const int64_t i = (int64_t)r * a.n_seqs + b;
+      rtab[0][r] = a.kv_begin[i];
+      rtab[1][r] = a.kv_end[i];
+    }
+    __syncthreads();
+  }
   auto range = [&](int r) -> Range {
     Range g;
     const int64_t i = (int64_t)r * a.n_seqs + b;
-    const int32_t kbr = r == 0 ? kb0 : a.kv_begin[i];
+    int32_t kbr, ker;
+    if (r == 0) {
+      kbr = kb0;
+      ker = ke0;
+    } else if (r < n_tab) {
+      kbr = __builtin_amdgcn_readfirstlane(rtab[0][r]);
+      ker = __builtin_amdgcn_readfirstlane(rtab[1][r]);
+    } else {
+      kbr = a.kv_begin[i];
+      ker = a.kv_end[i];
+    }
     g.kb = kbr > 0 ? kbr : 0;
-    g.ke = r == 0 ? ke0 : a.kv_end[i];
+    g.ke = ker;
     if (g.ke > kmax) {
       e |= ZX_KERR_POS_RANGE;
       g.ke = kmax;
