@@ -374,7 +374,8 @@ int zx_ring_curriculum_trace(const int32_t *degrees, const int32_t *ctx_pages, i
  *     version 7): for a causal ring whose steps cover each sequence's keys in ascending,
  *     contiguous ranges (the first step's kv_begin 0, each later kv_begin the previous
  *     kv_end): a row at a position below kv_begin is left alone (an earlier step finished
- *     it); a row below kv_end sees no later key, so it is written to out as bf16 and not
+ *     it; with INIT no row is); a row below kv_end sees no later key, so it is written to
+ *     out as bf16 and not
  *     to o_acc / lse2; the other rows merge into o_acc / lse2 (with LAST: go to out as
  *     well, as final).  Each row then reaches out in the step that completes it, and the
  *     last step converts only the rows it reaches instead of every row.

@@ -236,6 +236,33 @@ def test_final_steps_equal_the_merged_ring(shape, R):
                                    dtype=torch.float32, device=DEV), final=True)
 
 
+def test_final_first_step_writes_every_row():
+    """ZX_PREFILL_FINAL on a first step (INIT) whose key range starts past some rows: no
+    earlier step finished those rows, so they are written too (no key: zeros), and the
+    one-step ring (INIT | LAST | FINAL) equals a plain merging step bit for bit and the
+    oracle within the default bound."""
+    Hq, Hkv, P = 8, 2, 16
+    n_q, q_pos0, kb, ke = [40, 70], [0, 0], [10, 30], [50, 60]
+    q, pool, scales, bt, cu, qp = make(Hq, Hkv, P, n_q, q_pos0, ke, seed=29)
+    kb, ke = np.asarray(kb, np.int32), np.asarray(ke, np.int32)
+    sm = float(np.float32(1.0 / np.sqrt(128)))
+    want, _, err = O.paged_attention_prefill(bits16(q), cu, qp, pool, scales, bt, kb, ke, True, sm)
+    assert err == 0
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(DEV)  # noqa: E731
+    outs = []
+    for final in (True, False):
+        o_acc = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+        lse2 = torch.empty(q.shape[:2], dtype=torch.float32, device=DEV)
+        out = torch.full(q.shape, 0x7FC1, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+        kv.paged_attention_prefill(q.to(DEV), t(cu), t(qp), t(pool), t(scales), t(bt), t(kb), t(ke), o_acc=o_acc,
+                                   lse2=lse2, first=True, out=out, check=True, last=final, final=final)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert not torch.isnan(outs[0].float()).any()
+    assert_precision(bits16(outs[0]), want, vmax_rows(pool, scales, bt, cu, kb, ke, Hq))
+
+
 @pytest.mark.parametrize("ring,single", [(1, True), (8, True), (3, False)])
 def test_ring_attention_bf16_p(ring, single):
     """P rounded once to bf16 for P.V (ZX_PREFILL_FAST_P): within its bound of the oracle

@@ -216,7 +216,7 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
       ((a.mode & PF_WRITE_BF16) && (!(a.mode & PF_FINAL) || (a.mode & PF_LAST)));
   // a FINAL step leaves rows below kv_begin alone: a block of such rows only would read
   // the running output for nothing
-  const bool rows_all_done = (a.mode & PF_FINAL) && qp0 + last_row < (int64_t)kb0;
+  const bool rows_all_done = (a.mode & PF_FINAL) && !(a.mode & PF_INIT) && qp0 + last_row < (int64_t)kb0;
   if ((rc == a.n_ranges && !rows_without_keys_write) || rows_all_done) {
     // no key of any range reaches the block's rows: merging would leave o_acc and lse2 as
     // they are, and a FINAL step's rows below kv_begin were finished before (block-uniform
@@ -602,11 +602,12 @@ __global__ void __launch_bounds__(PF_THREADS, 2) paged_prefill_mfma_kernel(Prefi
     const int r = wrow0 + 16 * rt + n;
     const float lt = ol[rt][0];
     if (r >= n_qb) continue;
-    // FINAL: rows below kv_begin were finished by an earlier step; rows below kv_end (all
-    // rows on the last step) are finished by this one and go to out only
+    // FINAL: rows below kv_begin were finished by an earlier step (there is none before
+    // the first); rows below kv_end (all rows on the last step) are finished by this one
+    // and go to out only
     const int64_t pos = qp0 + r;
     const bool fin_mode = (a.mode & PF_FINAL) != 0;
-    if (fin_mode && pos < kb0) continue;
+    if (fin_mode && !(a.mode & PF_INIT) && pos < kb0) continue;
     const bool fin = fin_mode && (pos < ke0 || (a.mode & PF_LAST));
     const bool keep_row = keep && !fin;
     const bool bf16_row = (a.mode & PF_WRITE_BF16) && (!fin_mode || fin);
